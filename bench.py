@@ -1,0 +1,239 @@
+#!/usr/bin/env python3
+"""Benchmark of the decode hot path on one MI355X (gfx950).
+
+Headline: GEMV fp16 M = K = 16384 (512 MiB
+matrix), seeded U[-1,1] data generated on the device, FP32 accumulation.
+A step is one GEMV launch; the K timed steps are bracketed by a stream
+synchronisation and timed with HIP events recorded on the runtime's stream
+(the stream the kernel runs on). value = algorithmic bytes (A + x + y) per
+launch / average launch time, in GB/s; roofline.peak = 8000 GB/s (HBM3E).
+
+Secondary lines (same JSON object): GEMM bf16 4096^3 TFLOP/s
+and Qwen3-0.6B-shape batch-1 greedy decode tok/s.
+
+cpu_baseline: the CPU oracle's reference-order GEMV (gemv.cpp:126-134,
+sequential FP32 sum per row) over the same 16384 x 16384 fp16 matrix on all
+host threads, repeated for about 10 s.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--no-secondary]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def timed_gemv(rt, xpu, dtype, m, k, steps, warmup):
+    a, x, y = rt.alloc(m * k * 2), rt.alloc(k * 2), rt.alloc(m * 2)
+    rt.fill_uniform(dtype, a, m * k, 3)
+    rt.fill_uniform(dtype, x, k, 4)
+    for _ in range(warmup):
+        rt.gemv(dtype, a, x, y, m, k, k)
+    rt.synchronize()
+    start, stop = rt.event(), rt.event()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        rt.gemv(dtype, a, x, y, m, k, k)
+    stop.record()
+    rt.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_ms(stop)
+    for p in (a, x, y):
+        rt.free(p)
+    return ms / steps, wall
+
+
+def timed_gemm(rt, dtype, m, n, k, steps, warmup):
+    a, b, c = rt.alloc(m * k * 2), rt.alloc(k * n * 2), rt.alloc(m * n * 2)
+    rt.fill_uniform(dtype, a, m * k, 5)
+    rt.fill_uniform(dtype, b, k * n, 6)
+    for _ in range(warmup):
+        rt.gemm(dtype, a, b, c, m, n, k)
+    rt.synchronize()
+    start, stop = rt.event(), rt.event()
+    start.record()
+    for _ in range(steps):
+        rt.gemm(dtype, a, b, c, m, n, k)
+    stop.record()
+    rt.synchronize()
+    ms = start.elapsed_ms(stop)
+    for p in (a, b, c):
+        rt.free(p)
+    return ms / steps
+
+
+def qwen3_decode(xpu):
+    """Qwen3-0.6B shape, random N(0, 0.02^2) bf16 weights, 128-token seeded
+    prompt, 128 greedy steps; returns (decode tok/s, prompt tok/s)."""
+    import numpy as np
+
+    lib = xpu.library()
+    if not hasattr(lib, "xpu_qwen3_create"):
+        return None
+    import ctypes
+
+    rt = xpu.Runtime()
+    cfg = xpu.Qwen3Config()
+    xpu.check(lib.xpu_qwen3_preset(b"qwen3-0.6b", ctypes.byref(cfg)))
+    eng = ctypes.c_void_p()
+    xpu.check(lib.xpu_qwen3_create(rt.handle, ctypes.byref(cfg), 256, 0, 0.0, ctypes.byref(eng)))
+    try:
+        prompt = np.empty(128, np.uint32)
+        # the same seeded ids as the oracle's orc_fill_tokens(seed 1)
+        from xpu_playground_amd import qwen3 as q3
+
+        prompt[:] = q3.prompt_tokens(128, 1, cfg.vocab)
+        out = (ctypes.c_uint32 * 128)()
+        n_out = ctypes.c_uint32()
+        prompt_ms, decode_ms = ctypes.c_double(), ctypes.c_double()
+        arr = (ctypes.c_uint32 * 128)(*prompt.tolist())
+        for _ in range(2):  # first run builds the graph
+            xpu.check(lib.xpu_qwen3_generate(eng, arr, 128, 128, 0, out, ctypes.byref(n_out),
+                                             ctypes.byref(prompt_ms), ctypes.byref(decode_ms)))
+        decode_steps = n_out.value - 1
+        return {
+            "decode_tok_s": decode_steps / (decode_ms.value * 1e-3),
+            "prompt_tok_s": 128 / (prompt_ms.value * 1e-3),
+            "ms_per_token": decode_ms.value / decode_steps,
+            "generated": n_out.value,
+        }
+    finally:
+        lib.xpu_qwen3_destroy(eng)
+        rt.close()
+
+
+def cpu_baseline(m, k, dtype):
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import numpy as np
+    import oracle_lib as orc
+
+    threads = len(os.sched_getaffinity(0))
+    a = orc.uniform(m * k, 3, dtype)
+    x = orc.uniform(k, 4, dtype)
+    y = np.empty(m, np.float32)
+    times = []
+    t_end = time.perf_counter() + 10.0
+    while time.perf_counter() < t_end and len(times) < 50:
+        times.append(orc.lib().orc_time_gemv_seq(orc.ptr(a), orc.ptr(x), orc.ptr(y), m, k, dtype, threads))
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round((2.0 * m * k + 2.0 * k + 2.0 * m) / med / 1e9, 2),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(times)} full passes of the {m}x{k} fp16 GEMV, reference order "
+        f"(gemv.cpp:126-134, sequential FP32 per row), rows split over {threads} threads; median pass "
+        f"{med * 1e3:.1f} ms",
+    }
+
+
+def read_traffic():
+    """HBM bytes per launch of the headline kernel from the committed PMC
+    summary (profiles/gemv_fp16_16384_traffic.md), if present."""
+    path = os.path.join(REPO, "profiles", "gemv_fp16_16384_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the hot path is "
+              "single-device and sharding is described in DESIGN.md", file=sys.stderr)
+        return 2
+
+    import xpu_playground_amd as xpu
+
+    m = k = 16384
+    dtype = xpu.FP16
+    rt = xpu.Runtime()
+    log(f"device {rt.device_name} {rt.arch} {rt.compute_units} CUs")
+    log(f"GEMV fp16 {m}x{k}: {args.warmup} warmups, {args.steps} timed launches")
+    ms, wall = timed_gemv(rt, xpu, dtype, m, k, args.steps, args.warmup)
+    alg_bytes = 2.0 * m * k + 2.0 * k + 2.0 * m
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    log(f"GEMV {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s (wall {wall:.3f} s)")
+
+    secondary = {}
+    if not args.no_secondary:
+        if hasattr(xpu.library(), "xpu_gemm"):
+            log("GEMM bf16 4096^3: 5 warmups, 20 timed")
+            gms = timed_gemm(rt, xpu.BF16, 4096, 4096, 4096, 20, 5)
+            tflops = 2.0 * 4096**3 / (gms * 1e-3) / 1e12
+            secondary["gemm_bf16_4096"] = {
+                "value": round(tflops, 1), "unit": "TFLOP/s", "ms": round(gms, 4),
+                "roofline_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+            log(f"GEMM {gms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
+            gms2 = timed_gemm(rt, xpu.FP16, 3000, 4097, 2050, 10, 3)
+            secondary["gemm_fp16_3000x4097x2050"] = {
+                "value": round(2.0 * 3000 * 4097 * 2050 / (gms2 * 1e-3) / 1e12, 1), "unit": "TFLOP/s"}
+    rt.close()
+    if not args.no_secondary:
+        log("Qwen3-0.6B decode: 128 prompt + 128 greedy steps")
+        q = qwen3_decode(xpu)
+        if q:
+            secondary["qwen3_0.6b_decode"] = {
+                "value": round(q["decode_tok_s"], 1), "unit": "tok/s", "ms_per_token": round(q["ms_per_token"], 4),
+                "prompt_tok_s": round(q["prompt_tok_s"], 1)}
+            log(f"Qwen3 decode {q['decode_tok_s']:.1f} tok/s")
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle GEMV, reference order)")
+        cpu = cpu_baseline(m, k, dtype)
+        log(f"CPU {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": "GEMV HBM GB/s (% of 8 TB/s); GEMM TFLOP/s; Qwen3-0.6B decode tok/s",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "gemv fp16 16384x16384 (configs[1])", "m": m, "k": k,
+                   "bytes_per_launch": int(alg_bytes), "matrix_only_gbs": round(2.0 * m * k / (ms * 1e-3) / 1e9, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic()},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

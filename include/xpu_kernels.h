@@ -1,0 +1,66 @@
+/*
+ * xpu_kernels.h - C-ABI entry points of the GEMV / GEMM hot path on gfx950.
+ *
+ * Kernel ABI kept from the reference (row-major, contiguous unless an lda is
+ * given, element type bf16 or fp16 as raw 16-bit codes, FP32 accumulation):
+ *   GEMV (A, x, y, m, k)      gemv_kernel.hpp:21-26, level_zero/gem_spv_entry.cpp:11-27,
+ *                             level_zero/peak_l0.cpp:840-842
+ *   GEMM (a, b, c, m, n, k)   gemm_kernel.hpp:28-33, level_zero/gem_spv_entry.cpp:28-60,
+ *                             level_zero/peak_l0.cpp:920-922
+ * Unlike the reference (gemv.cpp:79-80, gemm.cpp:75-85 pad on the host), any
+ * M, N, K >= 1 is handled inside the kernels; no padding is needed.
+ *
+ * All launches are asynchronous on the runtime's stream; rt may be NULL for
+ * none of these functions. Return 0 on success, an XPU_ERR_* code otherwise
+ * (xpu_last_error() has the message).
+ */
+#ifndef XPU_KERNELS_H
+#define XPU_KERNELS_H
+
+#include "xpu_runtime.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XPU_DTYPE_BF16 0
+#define XPU_DTYPE_FP16 1
+
+/* y[M] = A[M x K] . x[K]; lda >= K is the row pitch in elements (K for a
+ * packed matrix). Replaces gemv::Kernel<T> (gemv_kernel.hpp:21-63) launched
+ * by gemv.cpp:170-172 / peak_l0.cpp:849-856. Each y[r] is the canonical-order
+ * FP32 sum rounded to the storage type. */
+int xpu_gemv(xpu_runtime *rt, int dtype, const void *A, const void *x, void *y,
+             uint32_t M, uint32_t K, uint64_t lda);
+
+/* C[M x N] = A[M x K] . B[K x N], row-major, FP32 accumulation on MFMA.
+ * Replaces gemm::Kernel<T, Large> (gemm_kernel.hpp:25-143) launched by
+ * gemm.cpp:243-246 / peak_l0.cpp:929-934. */
+int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
+             uint32_t M, uint32_t N, uint32_t K);
+
+/* Seeded U[-1,1) synthetic data written on the device: element i is
+ * encode(dtype, (2u - 2^24) / 2^24) with u the top 24 bits of
+ * splitmix64(splitmix64(seed) + (i + 1) * 0x9e3779b97f4a7c15). The same
+ * values the CPU oracle's generator produces. */
+int xpu_fill_uniform(xpu_runtime *rt, int dtype, void *dst, uint64_t count, uint64_t seed);
+
+/* The reference's hash initialisation (gemv.cpp:91-103) on the device: the
+ * matrix (m rows, pitch ld) and the vector (k entries). */
+int xpu_fill_reference_gemv(xpu_runtime *rt, int dtype, void *matrix, void *vector,
+                            uint32_t m, uint32_t k, uint32_t ld);
+
+/* Command-line programs with the reference's flags and output lines:
+ * run_gemv: gemv.cpp:157-170 (--size N | --m M --k K, --type bf16|fp16,
+ *           --iterations N (50), --warmups N (5); default 16384 x 16384 bf16)
+ * run_gemm: gemm.cpp:135-155 (--size N | --m M --n N --k K, --type,
+ *           --iterations N (20), --warmups N (5); default 4096^3 bf16)
+ * Both return 0 on success, 1 on error (message "Error: ..." on stderr) and
+ * 2 when verification fails (level_zero/peak_l0.cpp:892,948). */
+int run_gemv(int argc, char **argv);
+int run_gemm(int argc, char **argv);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,195 @@
+// GEMM entry points: xpu_gemm (kernel launch) and the run_gemm command-line
+// program (reference gemm.cpp and the GEMM mode of level_zero/peak_l0.cpp:895-949).
+#include "../../include/xpu_kernels.h"
+#include "host_common.hpp"
+#include "runtime_internal.hpp"
+
+#include <cstdlib>
+#include <iomanip>
+#include <iostream>
+
+using xpu::set_error;
+
+extern "C" int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
+                        uint32_t M, uint32_t N, uint32_t K) {
+  if (!rt || !A || !B || !C) return set_error(XPU_ERR_INVALID, "xpu_gemm: null argument");
+  if (dtype != XPU_DTYPE_BF16 && dtype != XPU_DTYPE_FP16)
+    return set_error(XPU_ERR_INVALID, "xpu_gemm: dtype must be bf16 (0) or fp16 (1)");
+  if (M == 0 || N == 0 || K == 0) return set_error(XPU_ERR_INVALID, "xpu_gemm: M, N, K must be positive");
+  const bool vec = reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0 &&
+                   K % 8 == 0 && N % 8 == 0;
+  const std::string name = std::string("xpu_gemm_") + (dtype ? "fp16" : "bf16") + (vec ? "_vec" : "_any");
+  const xpu::KernelInfo *k = rt->find_exact(name);
+  if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: " + name);
+  const uint64_t tiles = ((static_cast<uint64_t>(M) + 255) / 256) * ((static_cast<uint64_t>(N) + 255) / 256);
+  if (tiles > 0x7fffffffu) return set_error(XPU_ERR_INVALID, "xpu_gemm: too many tiles");
+  const xpu_kernel_arg args[] = {{8, &A}, {8, &B}, {8, &C}, {4, &M}, {4, &N}, {4, &K}};
+  return rt->launch(*k, static_cast<uint32_t>(tiles), 1, 256, 0, args, 6);
+}
+
+namespace {
+
+struct GemmOptions {
+  uint32_t m = 4096, n = 4096, k = 4096;  // gemm.cpp:19
+  unsigned iterations = 20, warmups = 5;  // gemm.cpp:20
+  int dtype = XPU_DTYPE_BF16;
+  bool constant_init = false;             // --init constant: gemm.cpp:81-85 (A = 0.5, B = 0.25)
+  uint64_t seed = 1;
+  uint32_t check_rows = 64;
+};
+
+[[noreturn]] void gemm_usage(const char *program, int status) {
+  std::ostream &out = status ? std::cerr : std::cout;
+  out << "Usage: " << program << " [--size N | --m M --n N --k K] [--type bf16|fp16]\n"
+      << "       [--iterations N] [--warmups N] [--init uniform|constant] [--seed N]\n"
+      << "       [--check-rows N]\n";
+  std::exit(status);
+}
+
+// gemm.cpp:40-59
+GemmOptions parse_gemm(int argc, char **argv) {
+  GemmOptions o;
+  for (int i = 1; i < argc; ++i) {
+    const std::string_view arg(argv[i]);
+    if (arg == "-h" || arg == "--help") gemm_usage(argv[0], 0);
+    if (++i == argc) throw std::invalid_argument(std::string(arg) + " requires a value");
+    const std::string_view value(argv[i]);
+    if (arg == "--size") o.m = o.n = o.k = xpu::parse_positive<uint32_t>(value, arg);
+    else if (arg == "--m") o.m = xpu::parse_positive<uint32_t>(value, arg);
+    else if (arg == "--n") o.n = xpu::parse_positive<uint32_t>(value, arg);
+    else if (arg == "--k") o.k = xpu::parse_positive<uint32_t>(value, arg);
+    else if (arg == "--iterations") o.iterations = xpu::parse_positive<unsigned>(value, arg);
+    else if (arg == "--warmups") o.warmups = xpu::parse_positive<unsigned>(value, arg);
+    else if (arg == "--type" && value == "fp16") o.dtype = XPU_DTYPE_FP16;
+    else if (arg == "--type" && value == "bf16") o.dtype = XPU_DTYPE_BF16;
+    else if (arg == "--type") throw std::invalid_argument("--type must be bf16 or fp16");
+    else if (arg == "--init" && value == "uniform") o.constant_init = false;
+    else if (arg == "--init" && value == "constant") o.constant_init = true;
+    else if (arg == "--init") throw std::invalid_argument("--init must be uniform or constant");
+    else if (arg == "--seed") o.seed = xpu::parse_unsigned<uint64_t>(value, arg);
+    else if (arg == "--check-rows") o.check_rows = xpu::parse_unsigned<uint32_t>(value, arg);
+    else throw std::invalid_argument("unknown option: " + std::string(arg));
+  }
+  return o;
+}
+
+void check(int rc) {
+  if (rc) throw std::runtime_error(xpu_last_error());
+}
+
+struct RuntimeGuard {
+  xpu_runtime *rt = nullptr;
+  ~RuntimeGuard() { xpu_rt_destroy(rt); }
+};
+
+}  // namespace
+
+extern "C" int run_gemm(int argc, char **argv) {
+  try {
+    const GemmOptions o = parse_gemm(argc, argv);
+    RuntimeGuard guard;
+    check(xpu_rt_create(nullptr, -1, &guard.rt));
+    xpu_runtime *rt = guard.rt;
+    std::cout << "Device: " << rt->name << " (" << rt->arch << ", " << rt->compute_units << " CUs)\n";
+    const uint64_t as = static_cast<uint64_t>(o.m) * o.k, bs = static_cast<uint64_t>(o.k) * o.n,
+                   cs = static_cast<uint64_t>(o.m) * o.n;
+    check(xpu_rt_require_device_and_memory(rt, (as + bs + cs) * 2));
+    void *a = nullptr, *b = nullptr, *c = nullptr;
+    check(xpu_rt_alloc(rt, as * 2, 256, &a));
+    check(xpu_rt_alloc(rt, bs * 2, 256, &b));
+    check(xpu_rt_alloc(rt, cs * 2, 256, &c));
+    if (o.constant_init) {
+      // gemm.cpp:81-85: A = 0.5, B = 0.25 (no padding needed here)
+      const uint16_t ha = xpu::encode16(0.5f, o.dtype), hb = xpu::encode16(0.25f, o.dtype);
+      std::vector<uint16_t> fill(std::max(as, bs));
+      std::fill(fill.begin(), fill.begin() + as, ha);
+      check(xpu_rt_copy_to_device(rt, a, fill.data(), as * 2));
+      std::fill(fill.begin(), fill.begin() + bs, hb);
+      check(xpu_rt_copy_to_device(rt, b, fill.data(), bs * 2));
+    } else {
+      check(xpu_fill_uniform(rt, o.dtype, a, as, o.seed));
+      check(xpu_fill_uniform(rt, o.dtype, b, bs, o.seed + 1));
+    }
+    check(xpu_rt_memset(rt, c, 0, cs * 2));
+    for (unsigned i = 0; i < o.warmups; ++i) check(xpu_gemm(rt, o.dtype, a, b, c, o.m, o.n, o.k));
+    check(xpu_rt_synchronize(rt));
+    void *start = nullptr, *stop = nullptr;
+    check(xpu_rt_event_create(rt, &start));
+    check(xpu_rt_event_create(rt, &stop));
+    // gemm.cpp:248-253: one timed launch per iteration, 2*M*N*K FLOP
+    const double flops = 2.0 * o.m * o.n * o.k;
+    std::vector<double> rates, times;
+    for (unsigned i = 0; i < o.iterations; ++i) {
+      check(xpu_rt_event_record(rt, start));
+      check(xpu_gemm(rt, o.dtype, a, b, c, o.m, o.n, o.k));
+      check(xpu_rt_event_record(rt, stop));
+      float ms = 0;
+      check(xpu_rt_event_elapsed_ms(start, stop, &ms));
+      times.push_back(ms * 1e-3);
+      rates.push_back(flops / (ms * 1e-3) / 1e12);
+    }
+    xpu_rt_event_destroy(start);
+    xpu_rt_event_destroy(stop);
+
+    // Verification: constant init checks 0.125 * K (gemm.cpp:254-262); the
+    // uniform init checks the first rows against an FP64 host product,
+    // rounded to the output type, within 2 output ulps + gamma_K sum|a b|.
+    bool valid = true;
+    double err2 = 0, ref2 = 0, max_ulps = 0;
+    const uint32_t rows = std::min(o.m, o.check_rows);
+    if (rows) {
+      std::vector<uint16_t> hc(static_cast<size_t>(rows) * o.n), ha(static_cast<size_t>(rows) * o.k),
+          hb(bs);
+      check(xpu_rt_copy_from_device(rt, hc.data(), c, hc.size() * 2));
+      if (o.constant_init) {
+        const float expected = o.k * 0.125f, tolerance = std::max(0.5f, expected * 0.01f);
+        for (uint16_t v : hc)
+          if (std::fabs(xpu::decode16(v, o.dtype) - expected) > tolerance) valid = false;
+      } else {
+        check(xpu_rt_copy_from_device(rt, ha.data(), a, ha.size() * 2));
+        check(xpu_rt_copy_from_device(rt, hb.data(), b, hb.size() * 2));
+        std::vector<double> bd(bs);
+        for (uint64_t i = 0; i < bs; ++i) bd[i] = xpu::decode16(hb[i], o.dtype);
+        const double gamma = o.k * 0x1p-24 / (1 - o.k * 0x1p-24);
+        std::vector<double> acc(o.n), absacc(o.n);
+        for (uint32_t r = 0; r < rows; ++r) {
+          std::fill(acc.begin(), acc.end(), 0.0);
+          std::fill(absacc.begin(), absacc.end(), 0.0);
+          for (uint32_t kk = 0; kk < o.k; ++kk) {
+            const double av = xpu::decode16(ha[static_cast<size_t>(r) * o.k + kk], o.dtype);
+            const double *brow = bd.data() + static_cast<size_t>(kk) * o.n;
+            for (uint32_t j = 0; j < o.n; ++j) {
+              acc[j] += av * brow[j];
+              absacc[j] += std::fabs(av * brow[j]);
+            }
+          }
+          for (uint32_t j = 0; j < o.n; ++j) {
+            const double ref = xpu::decode16(xpu::encode16(static_cast<float>(acc[j]), o.dtype), o.dtype);
+            const double got = xpu::decode16(hc[static_cast<size_t>(r) * o.n + j], o.dtype);
+            const double ulp = o.dtype ? xpu::fp16_ulp(ref) : xpu::bf16_ulp(ref);
+            err2 += (got - ref) * (got - ref);
+            ref2 += ref * ref;
+            max_ulps = std::max(max_ulps, std::fabs(got - ref) / ulp);
+            if (std::fabs(got - ref) > 2 * ulp + gamma * absacc[j]) valid = false;
+          }
+        }
+        if ((ref2 > 0 ? std::sqrt(err2 / ref2) : std::sqrt(err2)) > 1e-3) valid = false;
+      }
+    }
+    std::cout << "Type: " << (o.dtype ? "FP16" : "BF16") << ", shape: " << o.m << 'x' << o.n << 'x' << o.k
+              << '\n'
+              << std::fixed << std::setprecision(2) << "Median: " << xpu::median_of(rates)
+              << " TFLOP/s\nBest:   " << xpu::max_of(rates) << " TFLOP/s\n"
+              << "MFMA roofline: " << (xpu::median_of(rates) / 2500.0 * 100.0)
+              << "% of 2500 TFLOP/s dense (median " << xpu::median_of(times) * 1e6 << " us)\n";
+    if (rows && !o.constant_init)
+      std::cout << std::scientific << std::setprecision(3) << "Accuracy: rel-L2 "
+                << (ref2 > 0 ? std::sqrt(err2 / ref2) : std::sqrt(err2)) << ", max " << std::fixed
+                << std::setprecision(2) << max_ulps << " ulp over " << rows << " rows\n";
+    std::cout << "Verification: " << (valid ? "PASS" : "FAIL") << '\n';
+    return valid ? 0 : 2;
+  } catch (const std::exception &error) {
+    std::cerr << "Error: " << error.what() << '\n';
+    return 1;
+  }
+}

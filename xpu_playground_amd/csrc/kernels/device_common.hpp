@@ -1,0 +1,128 @@
+// Device helpers shared by the gfx950 kernels: 16-bit codecs, the canonical
+// FP32 reduction order, and the exp used by softmax and SiLU.
+//
+// Canonical order (all GEMV/RMSNorm sums): element k of a length-n sum goes
+// to lane (k / 8) % 64, slot k % 8, chunk k / 512; each of the 512 (lane,
+// slot) accumulators starts at +0 and adds its terms in ascending chunk
+// order; a lane then folds its 8 slots as ((0+1)+(2+3))+((4+5)+(6+7)) and
+// the wave folds lanes with xor-butterflies 32,16,8,4,2,1. The CPU oracle
+// (oracle/oracle.c) evaluates the same sequence, so results agree bit for bit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define XPU_DEVICE __device__ __forceinline__
+
+namespace xpu {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+enum : int { kBf16 = 0, kFp16 = 1 };
+
+XPU_DEVICE float bf16_to_f32(uint32_t code) { return __uint_as_float(code << 16); }
+
+// qwen3/model.cpp:497-502: +0x7fff+lsb then truncate (no NaN special case).
+XPU_DEVICE uint32_t f32_to_bf16(float v) {
+  const uint32_t bits = __float_as_uint(v);
+  return (bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16;
+}
+
+XPU_DEVICE float fp16_to_f32(uint32_t code) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(code)));
+}
+
+// level_zero/peak_l0.cpp:740-761: RNE with subnormals, overflow/NaN -> Inf.
+XPU_DEVICE uint32_t f32_to_fp16(float v) {
+  const uint32_t bits = __float_as_uint(v);
+  const uint32_t sign = (bits >> 16) & 0x8000u;
+  int exponent = static_cast<int>((bits >> 23) & 0xffu) - 127 + 15;
+  uint32_t mantissa = bits & 0x7fffffu;
+  if (exponent <= 0) {
+    if (exponent < -10) return sign;
+    mantissa = (mantissa | 0x800000u) >> (1 - exponent);
+    return sign | ((mantissa + 0xfffu + ((mantissa >> 13) & 1u)) >> 13);
+  }
+  if (exponent >= 31) return sign | 0x7c00u;
+  mantissa += 0xfffu + ((mantissa >> 13) & 1u);
+  if (mantissa & 0x800000u) {
+    mantissa = 0;
+    if (++exponent >= 31) return sign | 0x7c00u;
+  }
+  return sign | (static_cast<uint32_t>(exponent) << 10) | (mantissa >> 13);
+}
+
+template <int DT> XPU_DEVICE float decode(uint32_t code) {
+  if constexpr (DT == kFp16) return fp16_to_f32(code);
+  else return bf16_to_f32(code);
+}
+template <int DT> XPU_DEVICE uint32_t encode(float v) {
+  if constexpr (DT == kFp16) return f32_to_fp16(v);
+  else return f32_to_bf16(v);
+}
+
+XPU_DEVICE float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// Low and high 16-bit halves of a 32-bit word of packed codes.
+template <int DT> XPU_DEVICE float lo16(uint32_t w) {
+  if constexpr (DT == kFp16) return fp16_to_f32(w & 0xffffu);
+  else return __uint_as_float(w << 16);
+}
+template <int DT> XPU_DEVICE float hi16(uint32_t w) {
+  if constexpr (DT == kFp16) return fp16_to_f32(w >> 16);
+  else return __uint_as_float(w & 0xffff0000u);
+}
+
+// 8 packed codes (16 bytes) -> 8 floats
+template <int DT> XPU_DEVICE void unpack8(const u32x4 &v, float (&f)[8]) {
+  f[0] = lo16<DT>(v.x); f[1] = hi16<DT>(v.x);
+  f[2] = lo16<DT>(v.y); f[3] = hi16<DT>(v.y);
+  f[4] = lo16<DT>(v.z); f[5] = hi16<DT>(v.z);
+  f[6] = lo16<DT>(v.w); f[7] = hi16<DT>(v.w);
+}
+
+XPU_DEVICE float fold8(const float (&a)[8]) {
+  return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+}
+
+// xor-butterfly over the 64 lanes of a wavefront; every lane ends with the
+// same value because IEEE addition is commutative.
+XPU_DEVICE float wave_butterfly(float s) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) s = s + __shfl_xor(s, m, 64);
+  return s;
+}
+
+// exp: Cody-Waite reduction and degree-7 Taylor polynomial, the same
+// operation sequence as orc_exp in the oracle.
+XPU_DEVICE float pow2i(int e) { return __uint_as_float(static_cast<uint32_t>(e + 127) << 23); }
+
+XPU_DEVICE float canonical_exp(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_inff();
+  if (x < -103.972084045410156f) return 0.0f;
+  const float n = __builtin_rintf(x * 1.44269502162933349609f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.42860676533018704504e-06f, r);
+  float p = 1.98412698412698412526e-04f;
+  p = __builtin_fmaf(p, r, 1.38888888888888894189e-03f);
+  p = __builtin_fmaf(p, r, 8.33333333333333321769e-03f);
+  p = __builtin_fmaf(p, r, 4.16666666666666643537e-02f);
+  p = __builtin_fmaf(p, r, 1.66666666666666657415e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int e = static_cast<int>(n);
+  if (e > 127) { p = p * 2.0f; e -= 1; }
+  if (e < -126) return (p * pow2i(e + 64)) * 0x1p-64f;
+  return p * pow2i(e);
+}
+
+XPU_DEVICE u32x4 load_nt16(const void *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
+
+XPU_DEVICE uint32_t lane_id() { return threadIdx.x & 63u; }
+
+}  // namespace xpu

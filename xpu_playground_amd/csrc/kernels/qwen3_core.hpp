@@ -1,0 +1,268 @@
+// Qwen3 decode building blocks for gfx950 (head_dim 128): block RMSNorm,
+// per-head QK-norm + RoPE, single-query attention, argmax reduction.
+//
+// Rounding points follow transformers' eager bf16 Qwen3 (the arithmetic
+// behind the reference oracle qwen3/reference.py); operations follow the
+// reference kernels qwen3/kernels.hpp:36-246. Summation orders are the
+// canonical ones also evaluated by the CPU oracle (oracle/oracle.c).
+#pragma once
+
+#include "gemv_core.hpp"
+
+namespace xpu {
+
+constexpr uint32_t kHeadDim = 128;
+constexpr uint32_t kAttnChunk = 4096;  // positions per softmax / P.V chunk
+
+// Block-cooperative RMSNorm of x[0..W) into LDS buffer xs (bf16 codes,
+// zero-padded to a multiple of 512). xs may alias nothing else; red is one
+// float of LDS. qwen3/kernels.hpp:43-54 with transformers rounding:
+// out = bf16(w * bf16(x * (1 / sqrt(sum(x^2) / W + eps)))).
+XPU_DEVICE void block_rmsnorm(uint16_t *xs, const uint16_t *__restrict__ x,
+                              const uint16_t *__restrict__ w, uint32_t W, float eps, float *red) {
+  const uint32_t wpad = (W + 511u) & ~511u;
+  stage_vector<false>(xs, x, W, wpad);
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const uint32_t lane = threadIdx.x;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t j = 0; j < wpad; j += 512u) {
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(xs + j + lane * 8u);
+      float f[8];
+      unpack8<kBf16>(v, f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(f[e], f[e], acc[e]);
+    }
+    const float ss = wave_butterfly(fold8(acc));
+    if (lane == 0) red[0] = 1.0f / __builtin_sqrtf(ss / static_cast<float>(W) + eps);
+  }
+  __syncthreads();
+  const float scale = red[0];
+  for (uint32_t i = threadIdx.x; i < W; i += blockDim.x)
+    xs[i] = static_cast<uint16_t>(
+        f32_to_bf16(bf16_to_f32(w[i]) * round_bf16(bf16_to_f32(xs[i]) * scale)));
+  __syncthreads();
+}
+
+// One wavefront: RMSNorm over a 128-wide head then rotate-half RoPE
+// (qwen3/kernels.hpp:76-124 with transformers rounding:
+// out[i] = bf16(bf16(n[i] * cos[i]) + bf16(rot[i] * sin[i])), rot = (-n[64:], n[:64])).
+// Lanes 0..15 hold 8 consecutive entries each; lanes 16..63 contribute
+// zeros to the sum. normed_out (optional) receives the normed, un-rotated
+// codes; roped_out the rotated ones.
+XPU_DEVICE void head_norm_rope(const uint16_t *src, const uint16_t *__restrict__ w,
+                               const uint16_t *__restrict__ cos_row,
+                               const uint16_t *__restrict__ sin_row, float eps,
+                               uint16_t *normed_out, uint16_t *roped_out) {
+  const uint32_t lane = lane_id();
+  const bool active = lane < 16;
+  float x[8];
+  if (active) {
+    unpack8<kBf16>(*reinterpret_cast<const u32x4 *>(src + lane * 8u), x);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+  }
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(x[e], x[e], 0.0f);
+  const float ss = wave_butterfly(fold8(acc));
+  const float scale = 1.0f / __builtin_sqrtf(ss / static_cast<float>(kHeadDim) + eps);
+  float n[8], p[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t i = (lane & 15u) * 8u + e;
+    n[e] = active ? round_bf16(bf16_to_f32(w[i]) * round_bf16(x[e] * scale)) : 0.0f;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(n[e], 8, 64);
+  if (active) {
+    uint32_t codes[8], ncodes[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t i = lane * 8u + e;
+      const float rot = lane < 8 ? -p[e] : p[e];
+      const float a = round_bf16(n[e] * bf16_to_f32(cos_row[i]));
+      const float b = round_bf16(rot * bf16_to_f32(sin_row[i]));
+      codes[e] = f32_to_bf16(a + b);
+      ncodes[e] = f32_to_bf16(n[e]);
+    }
+    *reinterpret_cast<u32x4 *>(roped_out + lane * 8u) =
+        u32x4{codes[0] | (codes[1] << 16), codes[2] | (codes[3] << 16),
+              codes[4] | (codes[5] << 16), codes[6] | (codes[7] << 16)};
+    if (normed_out)
+      *reinterpret_cast<u32x4 *>(normed_out + lane * 8u) =
+          u32x4{ncodes[0] | (ncodes[1] << 16), ncodes[2] | (ncodes[3] << 16),
+                ncodes[4] | (ncodes[5] << 16), ncodes[6] | (ncodes[7] << 16)};
+  }
+}
+
+XPU_DEVICE float block_max(float v, float *red) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  const uint32_t wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  __syncthreads();
+  if (lane_id() == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (uint32_t i = 1; i < nwaves; ++i) r = fmaxf(r, red[i]);
+  __syncthreads();
+  return r;
+}
+
+// Attention score of query qs (LDS, roped bf16) against key row krow:
+// bf16(bf16(lane-local 8-slot dot) * scale) (transformers eager: bf16 matmul
+// then bf16 * scaling).
+XPU_DEVICE float attention_score(const uint16_t *qs, const uint16_t *krow, float scale) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll 4
+  for (uint32_t j = 0; j < kHeadDim; j += 8u) {
+    float q[8], k[8];
+    unpack8<kBf16>(*reinterpret_cast<const u32x4 *>(qs + j), q);
+    unpack8<kBf16>(*reinterpret_cast<const u32x4 *>(krow + j), k);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(q[e], k[e], acc[e]);
+  }
+  return round_bf16(round_bf16(fold8(acc)) * scale);
+}
+
+// Single-query attention of one head with a 256-thread block
+// (qwen3/kernels.hpp:157-192): positions 0..n-1, row t of K/V at
+// kbase/vbase + t * stride, except that when HAS_CURRENT the last position
+// reads kcur/vcur (the new token, not yet visible in the cache).
+// p_t = bf16(exp(s_t - max) * (1 / sum_t exp)), out = bf16(sum_t p_t v_t).
+// sbuf: kAttnChunk floats of LDS; red: >= 4*128 floats of LDS.
+template <bool HAS_CURRENT>
+XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const uint16_t *vbase,
+                               uint64_t stride, uint32_t n, const uint16_t *kcur,
+                               const uint16_t *vcur, float scale, uint16_t *out, float *sbuf,
+                               float *red) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t nchunks = (n + kAttnChunk - 1) / kAttnChunk;
+  auto krow_of = [&](uint32_t t) -> const uint16_t * {
+    return (HAS_CURRENT && t + 1 == n) ? kcur : kbase + static_cast<uint64_t>(t) * stride;
+  };
+  auto vrow_of = [&](uint32_t t) -> const uint16_t * {
+    return (HAS_CURRENT && t + 1 == n) ? vcur : vbase + static_cast<uint64_t>(t) * stride;
+  };
+  // pass 1: scores (kept in sbuf when one chunk holds them all) and the max
+  float local_max = -__builtin_inff();
+  for (uint32_t c = 0; c < nchunks; ++c) {
+    const uint32_t base = c * kAttnChunk;
+    const uint32_t len = min(kAttnChunk, n - base);
+    for (uint32_t i = tid; i < len; i += blockDim.x) {
+      const float s = attention_score(qs, krow_of(base + i), scale);
+      sbuf[i] = s;
+      local_max = fmaxf(local_max, s);
+    }
+  }
+  const float mx = block_max(local_max, red);
+  // pass 2: exponentials and the chunked canonical sum
+  float total = 0.0f;
+  for (uint32_t c = 0; c < nchunks; ++c) {
+    const uint32_t base = c * kAttnChunk;
+    const uint32_t len = min(kAttnChunk, n - base);
+    for (uint32_t i = tid; i < len; i += blockDim.x) {
+      const float s = nchunks == 1 ? sbuf[i] : attention_score(qs, krow_of(base + i), scale);
+      sbuf[i] = canonical_exp(s - mx);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (uint32_t j = 0; j < kAttnChunk; j += 512u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t k = j + tid * 8u + e;
+          if (k < len) acc[e] = acc[e] + sbuf[k];
+        }
+      const float chunk_sum = wave_butterfly(fold8(acc));
+      total = total + chunk_sum;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) red[0] = 1.0f / total;
+  __syncthreads();
+  const float inv = red[0];
+  __syncthreads();
+  // pass 3: probabilities and P.V in 16 residue classes (wave w owns
+  // residues 4w..4w+3, lane l owns dims 2l and 2l+1)
+  const uint32_t wave = tid >> 6, lane = lane_id();
+  float tot[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+  for (uint32_t c = 0; c < nchunks; ++c) {
+    const uint32_t base = c * kAttnChunk;
+    const uint32_t len = min(kAttnChunk, n - base);
+    for (uint32_t i = tid; i < len; i += blockDim.x) {
+      const float e = nchunks == 1 ? sbuf[i]
+                                   : canonical_exp(attention_score(qs, krow_of(base + i), scale) - mx);
+      sbuf[i] = round_bf16(e * inv);
+    }
+    __syncthreads();
+    float part[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+    for (uint32_t i0 = 0; i0 < len; i0 += 16u) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const uint32_t i = i0 + wave * 4u + rr;
+        if (i < len) {
+          const float pt = sbuf[i];
+          const uint32_t vv = *reinterpret_cast<const uint32_t *>(vrow_of(base + i) + lane * 2u);
+          part[rr][0] = __builtin_fmaf(pt, lo16<kBf16>(vv), part[rr][0]);
+          part[rr][1] = __builtin_fmaf(pt, hi16<kBf16>(vv), part[rr][1]);
+        }
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      tot[rr][0] = tot[rr][0] + part[rr][0];
+      tot[rr][1] = tot[rr][1] + part[rr][1];
+    }
+    __syncthreads();
+  }
+  red[wave * kHeadDim + lane * 2u] = (tot[0][0] + tot[1][0]) + (tot[2][0] + tot[3][0]);
+  red[wave * kHeadDim + lane * 2u + 1] = (tot[0][1] + tot[1][1]) + (tot[2][1] + tot[3][1]);
+  __syncthreads();
+  if (tid < kHeadDim) {
+    const float r = (red[tid] + red[kHeadDim + tid]) + (red[2 * kHeadDim + tid] + red[3 * kHeadDim + tid]);
+    out[tid] = static_cast<uint16_t>(f32_to_bf16(r));
+  }
+  __syncthreads();
+}
+
+// (value, index) argmax step with the reference's tie rule (strict >, so the
+// lowest index wins among equal values; kernels.hpp:238-242).
+XPU_DEVICE void argmax_merge(float &v, uint32_t &i, float ov, uint32_t oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+XPU_DEVICE bool finite_f(float v) { return v == v && v != __builtin_inff() && v != -__builtin_inff(); }
+
+// Block-wide argmax of (v, i) pairs plus an OR of bad flags; result valid in
+// thread 0. red needs 3 * (blockDim/64) words of LDS.
+XPU_DEVICE void block_argmax(float &v, uint32_t &i, uint32_t &bad, float *redv, uint32_t *redi,
+                             uint32_t *redb) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(v, m, 64);
+    const uint32_t oi = __shfl_xor(i, m, 64);
+    bad |= __shfl_xor(bad, m, 64);
+    argmax_merge(v, i, ov, oi);
+  }
+  const uint32_t wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  __syncthreads();
+  if (lane_id() == 0) {
+    redv[wave] = v;
+    redi[wave] = i;
+    redb[wave] = bad;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (uint32_t w = 1; w < nwaves; ++w) {
+      argmax_merge(v, i, redv[w], redi[w]);
+      bad |= redb[w];
+    }
+  }
+}
+
+}  // namespace xpu

@@ -1,0 +1,371 @@
+// Qwen3 decode kernels for gfx950.
+//
+// Part 1: the reference's eight entries with the reference's names and
+// argument order (qwen3/kernels_entry.cpp:8-72), launchable through the
+// runtime's work-item convention (xpu_rt_launch). The reference hard-codes
+// the 8B shape (kernels.hpp:20-22, hidden 4096 at :32); the shape is passed
+// as trailing arguments instead. KV caches use the reference layout
+// [position][kv_head][128] (kernels.hpp:128-131).
+//
+// Part 2: the fused decode path the engine runs (one hipGraph per token):
+//   xpu_q3_norm_gemv        RMSNorm + QKV projection (layer 0: + embedding)
+//   xpu_q3_attention        QK-norm + RoPE + KV-cache write + attention
+//   xpu_q3_gemv_residual    o_proj / down_proj + residual add
+//   xpu_q3_norm_gemv_swiglu RMSNorm + gate/up projection + SiLU * up
+//   xpu_q3_norm_gemv_logits final RMSNorm + tied lm_head + per-block argmax
+//   xpu_q3_argmax_finish    argmax, next token, position advance
+// The decode position and token live in device memory (state[0], state[1])
+// so one captured graph serves every step. Engine KV caches are head-major
+// [kv_head][max_seq][128].
+#include "qwen3_core.hpp"
+
+using xpu::u32x4;
+
+// ------------------------------------------------------------ reference entries
+
+// kernels.hpp:24-34: out[i] = table[token * hidden + i]
+extern "C" __global__ __launch_bounds__(256) void QwenEmbedding(
+    const uint16_t *__restrict__ table, uint16_t *__restrict__ out, uint32_t token, uint32_t hidden) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < hidden) out[i] = table[static_cast<uint64_t>(token) * hidden + i];
+}
+
+// kernels.hpp:36-56 (one block; the reference uses one work-item)
+extern "C" __global__ __launch_bounds__(256) void QwenRmsNorm(
+    const uint16_t *__restrict__ input, const uint16_t *__restrict__ weight,
+    uint16_t *__restrict__ output, uint32_t width, float epsilon) {
+  extern __shared__ __align__(16) uint16_t xs[];
+  __shared__ float red[1];
+  xpu::block_rmsnorm(xs, input, weight, width, epsilon, red);
+  for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) output[i] = xs[i];
+}
+
+// kernels_entry.cpp:271-277: bf16 GEMV with lda = columns
+extern "C" __global__ __launch_bounds__(256) void QwenGemv(
+    const uint16_t *__restrict__ matrix, const uint16_t *__restrict__ vector,
+    uint16_t *__restrict__ output, uint32_t rows, uint32_t columns) {
+  extern __shared__ __align__(16) uint16_t xs[];
+  const bool vec = (reinterpret_cast<uintptr_t>(matrix) % 16 == 0) &&
+                   (reinterpret_cast<uintptr_t>(vector) % 16 == 0) && columns % 8 == 0;
+  const uint32_t kpad = (columns + 511u) & ~511u;
+  if (vec) xpu::stage_vector<true>(xs, vector, columns, kpad);
+  else xpu::stage_vector<false>(xs, vector, columns, kpad);
+  __syncthreads();
+  const uint32_t wave = threadIdx.x >> 6, lane = xpu::lane_id();
+  for (uint32_t base = blockIdx.x * 8u; base < rows; base += gridDim.x * 8u) {
+    for (uint32_t half = 0; half < 2; ++half) {
+      const uint32_t row0 = base + half * 4u + wave;
+      if (row0 >= rows) continue;
+      float out[1];
+      if (vec) xpu::gemv_rows<xpu::kBf16, 1, 4, true>(matrix, columns, columns, rows, xs, row0, out);
+      else xpu::gemv_rows<xpu::kBf16, 1, 2, false>(matrix, columns, columns, rows, xs, row0, out);
+      if (lane == 0) output[row0] = static_cast<uint16_t>(xpu::f32_to_bf16(out[0]));
+    }
+  }
+}
+
+// kernels.hpp:58-155, one wavefront per query head: q normed + roped in
+// place; heads < kv_heads also norm k in place, write roped k and v to the
+// cache slot (position * kv_heads + head) * 128. Skipped when position >=
+// maximum_sequence (:74-75).
+extern "C" __global__ __launch_bounds__(64) void QwenQkvRopeCache(
+    uint16_t *query, uint16_t *key, const uint16_t *__restrict__ value,
+    const uint16_t *__restrict__ query_norm, const uint16_t *__restrict__ key_norm,
+    const uint16_t *__restrict__ rope_cos, const uint16_t *__restrict__ rope_sin,
+    uint16_t *__restrict__ key_cache, uint16_t *__restrict__ value_cache, uint32_t position,
+    uint32_t maximum_sequence, uint32_t heads, uint32_t kv_heads) {
+  const uint32_t head = blockIdx.x;
+  if (position >= maximum_sequence || head >= heads) return;
+  const uint16_t *cos_row = rope_cos + static_cast<uint64_t>(position) * xpu::kHeadDim;
+  const uint16_t *sin_row = rope_sin + static_cast<uint64_t>(position) * xpu::kHeadDim;
+  __shared__ __align__(16) uint16_t roped[xpu::kHeadDim];
+  uint16_t *q = query + head * xpu::kHeadDim;
+  xpu::head_norm_rope(q, query_norm, cos_row, sin_row, 1.0e-6f, nullptr, roped);
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < xpu::kHeadDim; i += 64) q[i] = roped[i];
+  __syncthreads();
+  if (head < kv_heads) {
+    uint16_t *k = key + head * xpu::kHeadDim;
+    const uint64_t slot = (static_cast<uint64_t>(position) * kv_heads + head) * xpu::kHeadDim;
+    xpu::head_norm_rope(k, key_norm, cos_row, sin_row, 1.0e-6f, k, key_cache + slot);
+    for (uint32_t i = threadIdx.x; i < xpu::kHeadDim; i += 64)
+      value_cache[slot + i] = value[head * xpu::kHeadDim + i];
+  }
+}
+
+// kernels.hpp:157-192: one block per query head over cache positions
+// 0..position, kv head = head / (heads / kv_heads).
+extern "C" __global__ __launch_bounds__(256) void QwenAttention(
+    const uint16_t *__restrict__ query, const uint16_t *__restrict__ key_cache,
+    const uint16_t *__restrict__ value_cache, uint16_t *__restrict__ output, uint32_t position,
+    uint32_t heads, uint32_t kv_heads) {
+  __shared__ float sbuf[xpu::kAttnChunk];
+  __shared__ float red[4 * xpu::kHeadDim];
+  __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
+  const uint32_t head = blockIdx.x;
+  if (head >= heads) return;
+  const uint32_t kv = head / (heads / kv_heads);
+  if (threadIdx.x < xpu::kHeadDim) qs[threadIdx.x] = query[head * xpu::kHeadDim + threadIdx.x];
+  __syncthreads();
+  const uint64_t stride = static_cast<uint64_t>(kv_heads) * xpu::kHeadDim;
+  xpu::attention_head<false>(qs, key_cache + kv * xpu::kHeadDim, value_cache + kv * xpu::kHeadDim,
+                             stride, position + 1, nullptr, nullptr, 0.08838834764831845f,
+                             output + head * xpu::kHeadDim, sbuf, red);
+}
+
+// kernels.hpp:194-207: left = bf16(left + right)
+extern "C" __global__ __launch_bounds__(256) void QwenAdd(uint16_t *left, const uint16_t *right,
+                                                          uint32_t width) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < width)
+    left[i] = static_cast<uint16_t>(
+        xpu::f32_to_bf16(xpu::bf16_to_f32(left[i]) + xpu::bf16_to_f32(right[i])));
+}
+
+// kernels.hpp:209-223 with transformers rounding: bf16(bf16(silu(g)) * u)
+XPU_DEVICE uint32_t silu_mul_code(float g, float u) {
+  const float act = xpu::round_bf16(g / (1.0f + xpu::canonical_exp(-g)));
+  return xpu::f32_to_bf16(act * u);
+}
+
+extern "C" __global__ __launch_bounds__(256) void QwenSiluMultiply(uint16_t *gate, const uint16_t *up,
+                                                                   uint32_t width) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < width)
+    gate[i] = static_cast<uint16_t>(silu_mul_code(xpu::bf16_to_f32(gate[i]), xpu::bf16_to_f32(up[i])));
+}
+
+// kernels.hpp:225-246 (one block): first maximum, NaN/Inf -> 0xffffffff
+extern "C" __global__ __launch_bounds__(1024) void QwenArgmax(const uint16_t *__restrict__ values,
+                                                              uint32_t *token, uint32_t width) {
+  __shared__ float redv[16];
+  __shared__ uint32_t redi[16], redb[16];
+  float best = -__builtin_inff();
+  uint32_t best_index = 0xffffffffu, bad = 0;
+  for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) {
+    const float v = xpu::bf16_to_f32(values[i]);
+    if (!xpu::finite_f(v)) bad = 1;
+    xpu::argmax_merge(best, best_index, v, i);
+  }
+  xpu::block_argmax(best, best_index, bad, redv, redi, redb);
+  if (threadIdx.x == 0) *token = bad ? 0xffffffffu : (best_index == 0xffffffffu ? 0u : best_index);
+}
+
+// ------------------------------------------------------------ fused decode path
+
+namespace {
+
+// Grid-stride loop over tiles of 4 wavefronts x R rows; body(row0, out[R]).
+template <int R, int U, typename Body>
+XPU_DEVICE void for_row_tiles(const uint16_t *__restrict__ W, uint32_t M, uint32_t K,
+                              const uint16_t *xs, Body body) {
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t rows_per_block = (blockDim.x >> 6) * R;
+  for (uint32_t base = blockIdx.x * rows_per_block; base < M; base += gridDim.x * rows_per_block) {
+    const uint32_t row0 = base + wave * R;
+    if (row0 >= M) continue;
+    float out[R];
+    xpu::gemv_rows<xpu::kBf16, R, U, true>(W, K, K, M, xs, row0, out);
+    body(row0, out);
+  }
+}
+
+}  // namespace
+
+// out[M] = W[M x K] . rmsnorm(x). When embed is non-null (first layer) the
+// source row is embed[state[1]] and block 0 also stores it into x.
+template <int R, int U>
+XPU_DEVICE void q3_norm_gemv(const uint16_t *__restrict__ W, uint16_t *x,
+                             const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ out,
+                             uint32_t M, uint32_t K, float eps, const uint16_t *__restrict__ embed,
+                             const uint32_t *__restrict__ state, uint32_t vocab) {
+  extern __shared__ __align__(16) uint16_t xs[];
+  __shared__ float red[1];
+  const uint16_t *src = x;
+  if (embed) {
+    uint32_t token = state[1];
+    if (token >= vocab) token = 0;
+    src = embed + static_cast<uint64_t>(token) * K;
+    if (blockIdx.x == 0)
+      for (uint32_t i = threadIdx.x; i < K; i += blockDim.x) x[i] = src[i];
+  }
+  xpu::block_rmsnorm(xs, src, norm_w, K, eps, red);
+  const uint32_t lane = xpu::lane_id();
+  for_row_tiles<R, U>(W, M, K, xs, [&](uint32_t row0, const float (&o)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (lane == static_cast<uint32_t>(r) && row0 + r < M)
+        out[row0 + r] = static_cast<uint16_t>(xpu::f32_to_bf16(o[r]));
+  });
+}
+
+// x[M] = bf16(x + bf16(W[M x K] . v))
+template <int R, int U>
+XPU_DEVICE void q3_gemv_residual(const uint16_t *__restrict__ W, const uint16_t *__restrict__ v,
+                                 uint16_t *x, uint32_t M, uint32_t K) {
+  extern __shared__ __align__(16) uint16_t xs[];
+  xpu::stage_vector<true>(xs, v, K, (K + 511u) & ~511u);
+  __syncthreads();
+  const uint32_t lane = xpu::lane_id();
+  for_row_tiles<R, U>(W, M, K, xs, [&](uint32_t row0, const float (&o)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (lane == static_cast<uint32_t>(r) && row0 + r < M) {
+        const float sum = xpu::bf16_to_f32(x[row0 + r]) + xpu::round_bf16(o[r]);
+        x[row0 + r] = static_cast<uint16_t>(xpu::f32_to_bf16(sum));
+      }
+  });
+}
+
+// h[I] = bf16(bf16(silu(g)) * u), (g, u) = rows (2i, 2i+1) of the
+// interleaved gate/up matrix times rmsnorm(x)
+template <int R, int U>
+XPU_DEVICE void q3_norm_gemv_swiglu(const uint16_t *__restrict__ Wgu, const uint16_t *__restrict__ x,
+                                    const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ h,
+                                    uint32_t I, uint32_t K, float eps) {
+  static_assert(R % 2 == 0, "gate/up rows come in pairs");
+  extern __shared__ __align__(16) uint16_t xs[];
+  __shared__ float red[1];
+  xpu::block_rmsnorm(xs, x, norm_w, K, eps, red);
+  const uint32_t lane = xpu::lane_id();
+  for_row_tiles<R, U>(Wgu, 2 * I, K, xs, [&](uint32_t row0, const float (&o)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; r += 2)
+      if (lane == static_cast<uint32_t>(r) && row0 + r < 2 * I) {
+        const float g = xpu::round_bf16(o[r]);
+        const float u = xpu::round_bf16(o[r + 1]);
+        h[(row0 + r) / 2] = static_cast<uint16_t>(silu_mul_code(g, u));
+      }
+  });
+}
+
+// logits[V] = E[V x K] . rmsnorm(x); block b also writes its (max, index,
+// non-finite flag) to part_*[b]
+template <int R, int U>
+XPU_DEVICE void q3_norm_gemv_logits(const uint16_t *__restrict__ E, const uint16_t *__restrict__ x,
+                                    const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ logits,
+                                    uint32_t V, uint32_t K, float eps, float *__restrict__ part_val,
+                                    uint32_t *__restrict__ part_idx, uint32_t *__restrict__ part_bad) {
+  extern __shared__ __align__(16) uint16_t xs[];
+  __shared__ float red[1];
+  __shared__ float redv[4];
+  __shared__ uint32_t redi[4], redb[4];
+  xpu::block_rmsnorm(xs, x, norm_w, K, eps, red);
+  const uint32_t lane = xpu::lane_id();
+  float best = -__builtin_inff();
+  uint32_t best_index = 0xffffffffu, bad = 0;
+  for_row_tiles<R, U>(E, V, K, xs, [&](uint32_t row0, const float (&o)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (row0 + r >= V) break;
+      const uint32_t code = xpu::f32_to_bf16(o[r]);
+      if (lane == static_cast<uint32_t>(r)) logits[row0 + r] = static_cast<uint16_t>(code);
+      const float v = xpu::bf16_to_f32(code);
+      if (!xpu::finite_f(v)) bad = 1;
+      xpu::argmax_merge(best, best_index, v, row0 + r);
+    }
+  });
+  xpu::block_argmax(best, best_index, bad, redv, redi, redb);
+  if (threadIdx.x == 0) {
+    part_val[blockIdx.x] = best;
+    part_idx[blockIdx.x] = best_index;
+    part_bad[blockIdx.x] = bad;
+  }
+}
+
+#define XPU_Q3_GEMV_KERNELS(SUFFIX, R, U)                                                       \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_norm_gemv##SUFFIX(                   \
+      const uint16_t *__restrict__ W, uint16_t *x, const uint16_t *__restrict__ norm_w,         \
+      uint16_t *__restrict__ out, uint32_t M, uint32_t K, float eps,                            \
+      const uint16_t *__restrict__ embed, const uint32_t *__restrict__ state, uint32_t vocab) { \
+    q3_norm_gemv<R, U>(W, x, norm_w, out, M, K, eps, embed, state, vocab);                      \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_gemv_residual##SUFFIX(               \
+      const uint16_t *__restrict__ W, const uint16_t *__restrict__ v, uint16_t *x, uint32_t M,  \
+      uint32_t K) {                                                                             \
+    q3_gemv_residual<R, U>(W, v, x, M, K);                                                      \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_norm_gemv_swiglu##SUFFIX(            \
+      const uint16_t *__restrict__ Wgu, const uint16_t *__restrict__ x,                         \
+      const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ h, uint32_t I, uint32_t K,    \
+      float eps) {                                                                              \
+    q3_norm_gemv_swiglu<R, U>(Wgu, x, norm_w, h, I, K, eps);                                    \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_norm_gemv_logits##SUFFIX(            \
+      const uint16_t *__restrict__ E, const uint16_t *__restrict__ x,                           \
+      const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ logits, uint32_t V,           \
+      uint32_t K, float eps, float *__restrict__ part_val, uint32_t *__restrict__ part_idx,     \
+      uint32_t *__restrict__ part_bad) {                                                        \
+    q3_norm_gemv_logits<R, U>(E, x, norm_w, logits, V, K, eps, part_val, part_idx, part_bad);   \
+  }
+
+XPU_Q3_GEMV_KERNELS(_r2, 2, 2)
+XPU_Q3_GEMV_KERNELS(_r4, 4, 2)
+
+// One block per query head: QK-norm + RoPE of q and of its kv head's k; the
+// first query head of each group writes k and v into the head-major cache at
+// position state[0]; then attention over positions 0..state[0].
+extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
+    const uint16_t *__restrict__ qkv, const uint16_t *__restrict__ qnorm_w,
+    const uint16_t *__restrict__ knorm_w, const uint16_t *__restrict__ rope_cos,
+    const uint16_t *__restrict__ rope_sin, uint16_t *__restrict__ kcache,
+    uint16_t *__restrict__ vcache, uint16_t *__restrict__ out, const uint32_t *__restrict__ state,
+    uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float eps, float scale) {
+  __shared__ float sbuf[xpu::kAttnChunk];
+  __shared__ float red[4 * xpu::kHeadDim];
+  __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
+  __shared__ __align__(16) uint16_t ks[xpu::kHeadDim];
+  const uint32_t head = blockIdx.x;
+  const uint32_t pos = state[0];
+  if (head >= heads || pos >= max_seq) return;
+  const uint32_t group = heads / kv_heads;
+  const uint32_t kv = head / group;
+  const uint16_t *cos_row = rope_cos + static_cast<uint64_t>(pos) * xpu::kHeadDim;
+  const uint16_t *sin_row = rope_sin + static_cast<uint64_t>(pos) * xpu::kHeadDim;
+  const uint16_t *qsrc = qkv + head * xpu::kHeadDim;
+  const uint16_t *ksrc = qkv + (heads + kv) * xpu::kHeadDim;
+  const uint16_t *vsrc = qkv + (heads + kv_heads + kv) * xpu::kHeadDim;
+  const uint32_t wave = threadIdx.x >> 6;
+  if (wave == 0) xpu::head_norm_rope(qsrc, qnorm_w, cos_row, sin_row, eps, nullptr, qs);
+  else if (wave == 1) xpu::head_norm_rope(ksrc, knorm_w, cos_row, sin_row, eps, nullptr, ks);
+  __syncthreads();
+  const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
+  if (head % group == 0 && threadIdx.x < xpu::kHeadDim) {
+    const uint64_t slot = head_base + static_cast<uint64_t>(pos) * xpu::kHeadDim + threadIdx.x;
+    kcache[slot] = ks[threadIdx.x];
+    vcache[slot] = vsrc[threadIdx.x];
+  }
+  xpu::attention_head<true>(qs, kcache + head_base, vcache + head_base, xpu::kHeadDim, pos + 1, ks,
+                            vsrc, scale, out + head * xpu::kHeadDim, sbuf, red);
+}
+
+// Reduce the per-block argmax partials; token = 0xffffffff if any logit was
+// non-finite. Then advance: position + 1, next token = next prompt id while
+// the prompt lasts, else the argmax; generated tokens are appended to gen.
+extern "C" __global__ __launch_bounds__(256) void xpu_q3_argmax_finish(
+    const float *__restrict__ part_val, const uint32_t *__restrict__ part_idx,
+    const uint32_t *__restrict__ part_bad, uint32_t nparts, uint32_t *state,
+    const uint32_t *__restrict__ prompt, uint32_t n_prompt, uint32_t *__restrict__ gen,
+    uint32_t gen_capacity) {
+  __shared__ float redv[4];
+  __shared__ uint32_t redi[4], redb[4];
+  float best = -__builtin_inff();
+  uint32_t best_index = 0xffffffffu, bad = 0;
+  for (uint32_t i = threadIdx.x; i < nparts; i += blockDim.x) {
+    bad |= part_bad[i];
+    xpu::argmax_merge(best, best_index, part_val[i], part_idx[i]);
+  }
+  xpu::block_argmax(best, best_index, bad, redv, redi, redb);
+  if (threadIdx.x == 0) {
+    const uint32_t token = bad ? 0xffffffffu : (best_index == 0xffffffffu ? 0u : best_index);
+    const uint32_t pos = state[0];
+    const uint32_t next_pos = pos + 1;
+    state[2] = token;
+    state[1] = next_pos < n_prompt ? prompt[next_pos] : token;
+    state[0] = next_pos;
+    if (next_pos >= n_prompt) {
+      const uint32_t g = next_pos - n_prompt;
+      if (g < gen_capacity) gen[g] = token;
+    }
+  }
+}

@@ -1,0 +1,73 @@
+// Internal definitions shared by the runtime and the entry-point libraries.
+#pragma once
+
+#include "../../include/xpu_runtime.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace xpu {
+
+int set_error(int code, const std::string &message);
+void clear_error();
+std::string hip_message(hipError_t e, const char *expr, const char *file, int line);
+
+struct Geometry {
+  uint32_t grid = 0, block = 0, shared = 0;
+};
+
+// Reference work-item convention (qwen3/level_zero_runtime.cpp:148-155,248):
+// each launchable-by-fragment kernel derives its grid from the work-item
+// count and, where needed, from its arguments. signature: one character per
+// argument, p = pointer, q = 64-bit integer, u = 32-bit integer, f = float.
+struct LaunchRule {
+  const char *name;
+  const char *signature;
+  int (*geometry)(uint32_t work_items, const xpu_kernel_arg *args, const struct ::xpu_runtime &rt,
+                  Geometry &g);
+};
+
+const LaunchRule *find_rule(const std::string &kernel_name);
+
+struct KernelInfo {
+  std::string name;
+  hipFunction_t function = nullptr;
+  const LaunchRule *rule = nullptr;
+};
+
+template <typename T> T arg_value(const xpu_kernel_arg *args, uint32_t index) {
+  return *static_cast<const T *>(args[index].value);
+}
+
+}  // namespace xpu
+
+struct xpu_runtime {
+  int device = -1;
+  std::string name, arch, module_path;
+  uint64_t total_memory = 0;
+  uint32_t compute_units = 0, max_shared = 0;
+  hipStream_t stream = nullptr;
+  hipModule_t module = nullptr;
+  std::vector<xpu::KernelInfo> kernels;
+  std::map<void *, void *> allocations;
+
+  xpu_runtime() = default;
+  xpu_runtime(const xpu_runtime &) = delete;
+  xpu_runtime &operator=(const xpu_runtime &) = delete;
+  ~xpu_runtime();
+  const xpu::KernelInfo *find_exact(const std::string &name) const;
+  int launch(const xpu::KernelInfo &k, uint32_t gx, uint32_t gy, uint32_t bx, uint32_t shared,
+             const xpu_kernel_arg *args, uint32_t nargs);
+};
+
+#define XPU_HIP_RETURN(expr)                                                                 \
+  do {                                                                                       \
+    const hipError_t xpu_e_ = (expr);                                                        \
+    if (xpu_e_ != hipSuccess)                                                                \
+      return ::xpu::set_error(XPU_ERR_HIP, ::xpu::hip_message(xpu_e_, #expr, __FILE__, __LINE__)); \
+  } while (0)
