@@ -539,7 +539,7 @@ uint32_t orc_argmax(const uint16_t *logits, uint32_t width) {
 struct orc_qwen3 {
   orc_qwen3_config c;
   uint32_t max_seq;
-  uint16_t *embed, *final_norm;
+  uint16_t *embed, *final_norm, *lm_head;
   uint16_t **w; /* [layer * 11 + kind] for kinds 0..10 */
   uint16_t *kcache, *vcache; /* [layer][kv][max_seq][head_dim] */
   uint16_t *cos_t, *sin_t;
@@ -557,7 +557,7 @@ uint64_t orc_qwen3_tensor_elems(const orc_qwen3_config *c, int kind) {
   case ORC_W_GATE: case ORC_W_UP: return in * h;
   case ORC_W_DOWN: return h * in;
   case ORC_W_INNORM: case ORC_W_POSTNORM: case ORC_W_FINALNORM: return h;
-  case ORC_W_EMBED: return (uint64_t)c->vocab * h;
+  case ORC_W_EMBED: case ORC_W_LMHEAD: return (uint64_t)c->vocab * h;
   default: return 0;
   }
 }
@@ -596,6 +596,11 @@ orc_qwen3 *orc_qwen3_create(const orc_qwen3_config *c, uint64_t seed,
   orc_qwen3_fill_tensor(c, seed, gain_std, ORC_W_EMBED, 0, m->embed);
   m->final_norm = (uint16_t *)malloc(2 * (uint64_t)c->hidden);
   orc_qwen3_fill_tensor(c, seed, gain_std, ORC_W_FINALNORM, 0, m->final_norm);
+  m->lm_head = m->embed;
+  if (!c->tied) {
+    m->lm_head = (uint16_t *)malloc(2 * orc_qwen3_tensor_elems(c, ORC_W_LMHEAD));
+    orc_qwen3_fill_tensor(c, seed, gain_std, ORC_W_LMHEAD, 0, m->lm_head);
+  }
   const uint64_t cache = (uint64_t)c->layers * c->kv_heads * max_seq * c->head_dim;
   m->kcache = (uint16_t *)calloc(cache, 2);
   m->vcache = (uint16_t *)calloc(cache, 2);
@@ -620,6 +625,7 @@ void orc_qwen3_destroy(orc_qwen3 *m) {
   if (!m) return;
   for (uint32_t i = 0; i < m->c.layers * 11; ++i) free(m->w[i]);
   free(m->w);
+  if (m->lm_head != m->embed) free(m->lm_head);
   free(m->embed); free(m->final_norm); free(m->kcache); free(m->vcache);
   free(m->cos_t); free(m->sin_t); free(m->x); free(m->norm); free(m->q);
   free(m->k); free(m->v); free(m->attn); free(m->tmp); free(m->gate);
@@ -630,6 +636,7 @@ void orc_qwen3_destroy(orc_qwen3 *m) {
 uint16_t *orc_qwen3_weight(orc_qwen3 *m, int kind, uint32_t layer) {
   if (kind == ORC_W_EMBED) return m->embed;
   if (kind == ORC_W_FINALNORM) return m->final_norm;
+  if (kind == ORC_W_LMHEAD) return m->lm_head;
   return m->w[layer * 11 + kind];
 }
 
@@ -640,8 +647,8 @@ static void gemv_bf16(const uint16_t *a, const uint16_t *x, uint16_t *y, uint32_
   orc_gemv_canonical(a, x, y, rows, cols, cols, 0);
 }
 
-/* qwen3/main.cpp:159-226 (Engine::decode), shape-parameterised and with the
- * lm_head tied to the embedding. */
+/* qwen3/main.cpp:159-226 (Engine::decode), shape-parameterised; lm_head is
+ * the embedding when the config is tied. */
 uint32_t orc_qwen3_decode(orc_qwen3 *m, uint32_t token, uint32_t position,
                           uint16_t *logits) {
   const orc_qwen3_config *c = &m->c;
@@ -679,7 +686,7 @@ uint32_t orc_qwen3_decode(orc_qwen3 *m, uint32_t token, uint32_t position,
     orc_add(m->x, m->tmp, H);
   }
   orc_rmsnorm(m->x, m->final_norm, m->norm, H, c->rms_eps);
-  gemv_bf16(m->embed, m->norm, m->logits, c->vocab, H);
+  gemv_bf16(m->lm_head, m->norm, m->logits, c->vocab, H);
   if (logits) memcpy(logits, m->logits, 2 * (uint64_t)c->vocab);
   return orc_argmax(m->logits, c->vocab);
 }

@@ -102,6 +102,7 @@ typedef struct {
   uint32_t hidden, intermediate, layers, heads, kv_heads, head_dim, vocab;
   float rms_eps;
   double rope_theta;
+  uint32_t tied; /* lm_head == embed_tokens */
 } orc_qwen3_config;
 
 float orc_exp(float x);
@@ -126,7 +127,8 @@ typedef struct orc_qwen3 orc_qwen3;
 enum {
   ORC_W_Q = 0, ORC_W_K = 1, ORC_W_V = 2, ORC_W_O = 3, ORC_W_QNORM = 4,
   ORC_W_KNORM = 5, ORC_W_GATE = 6, ORC_W_UP = 7, ORC_W_DOWN = 8,
-  ORC_W_INNORM = 9, ORC_W_POSTNORM = 10, ORC_W_EMBED = 11, ORC_W_FINALNORM = 12
+  ORC_W_INNORM = 9, ORC_W_POSTNORM = 10, ORC_W_EMBED = 11, ORC_W_FINALNORM = 12,
+  ORC_W_LMHEAD = 13
 };
 uint64_t orc_qwen3_tensor_elems(const orc_qwen3_config *c, int kind);
 void orc_qwen3_fill_tensor(const orc_qwen3_config *c, uint64_t seed, float gain_std,

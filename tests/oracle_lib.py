@@ -19,7 +19,7 @@ REF_DIR = os.path.join(ORACLE_DIR, "_ref")
 
 EOS_TOKENS = (151645, 151643)
 
-W_Q, W_K, W_V, W_O, W_QNORM, W_KNORM, W_GATE, W_UP, W_DOWN, W_INNORM, W_POSTNORM, W_EMBED, W_FINALNORM = range(13)
+W_Q, W_K, W_V, W_O, W_QNORM, W_KNORM, W_GATE, W_UP, W_DOWN, W_INNORM, W_POSTNORM, W_EMBED, W_FINALNORM, W_LMHEAD = range(14)
 
 
 class OrcConfig(ctypes.Structure):
@@ -33,6 +33,7 @@ class OrcConfig(ctypes.Structure):
         ("vocab", c_uint32),
         ("rms_eps", c_float),
         ("rope_theta", c_double),
+        ("tied", c_uint32),
     ]
 
 
@@ -40,7 +41,8 @@ PRESETS = {
     # Qwen3-0.6B architecture
     "qwen3-0.6b": dict(hidden=1024, intermediate=3072, layers=28, heads=16, kv_heads=8, head_dim=128, vocab=151936),
     # reference engine shape (qwen3/model.hpp:11-22)
-    "qwen3-8b": dict(hidden=4096, intermediate=12288, layers=36, heads=32, kv_heads=8, head_dim=128, vocab=151936),
+    "qwen3-8b": dict(hidden=4096, intermediate=12288, layers=36, heads=32, kv_heads=8, head_dim=128, vocab=151936,
+                     tied=0),
     # small shapes for fast tests
     "tiny": dict(hidden=256, intermediate=512, layers=2, heads=4, kv_heads=2, head_dim=128, vocab=1000),
     "small": dict(hidden=1024, intermediate=3072, layers=2, heads=16, kv_heads=8, head_dim=128, vocab=4096),
@@ -48,7 +50,8 @@ PRESETS = {
 
 
 def config(name: str = "qwen3-0.6b", **over) -> OrcConfig:
-    d = dict(PRESETS[name])
+    d = dict(tied=1)
+    d.update(PRESETS[name])
     d.update(over)
     return OrcConfig(rms_eps=1e-6, rope_theta=1e6, **d)
 
@@ -262,8 +265,8 @@ class Model:
         self.handle = lib().orc_qwen3_create(ctypes.byref(cfg), seed, gain_std, max_seq)
 
     def close(self):
-        if self.handle:
-            lib().orc_qwen3_destroy(self.handle)
+        if getattr(self, "handle", None) and _lib is not None:
+            _lib.orc_qwen3_destroy(self.handle)
             self.handle = None
 
     def __del__(self):

@@ -1,0 +1,188 @@
+"""Qwen3 decode engine on gfx950 vs the CPU oracle: tokens, logits and hidden
+states bit for bit in all three modes (graph, eager, the reference's kernel
+sequence), the BASELINE 0.6B workload against the golden fixtures, the
+checkpoint path and the NaN sentinel."""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+import xpu_playground_amd as xpu
+from xpu_playground_amd import qwen3
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+MODES = [qwen3.GRAPH, qwen3.EAGER, qwen3.REFERENCE]
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_decode_steps_match_oracle_bitwise(rt, mode):
+    cfg = orc.config("tiny")
+    m = orc.Model(cfg, seed=5, gain_std=0.1, max_seq=48)
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=48, seed=5, gain_std=0.1, runtime=rt)
+    eng.set_mode(mode)
+    prompt = orc.tokens(20, 9, cfg.vocab)
+    token = int(prompt[0])
+    for pos in range(40):
+        print(f"mode={mode} pos={pos}", flush=True)
+        ref_tok, ref_logits = m.decode(token, pos, want_logits=True)
+        tok = eng.decode(token, pos)
+        assert np.array_equal(eng.logits(), ref_logits), pos
+        assert np.array_equal(eng.hidden(), m.hidden()), pos
+        assert tok == ref_tok
+        token = int(prompt[pos + 1]) if pos + 1 < len(prompt) else tok
+    eng.close()
+
+
+def test_generate_small_config_all_modes_agree(rt):
+    cfg = orc.config("small")
+    prompt = orc.tokens(24, 4, cfg.vocab)
+    m = orc.Model(cfg, seed=3, gain_std=0.05, max_seq=96)
+    ref, _ = m.generate(prompt, 48)
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=96, seed=3, gain_std=0.05, runtime=rt)
+    for mode in MODES:
+        eng.set_mode(mode)
+        out, pm, dm = eng.generate(prompt, 48, stop_on_eos=False)
+        assert out.tolist() == ref.tolist(), mode
+    eng.close()
+
+
+def test_attention_past_one_softmax_chunk(rt):
+    # positions beyond 4096 take the chunked (recomputing) attention path
+    cfg = orc.config("tiny", layers=1, vocab=512)
+    n_prompt = 4100
+    prompt = orc.tokens(n_prompt, 6, cfg.vocab)
+    m = orc.Model(cfg, seed=8, gain_std=0.1, max_seq=n_prompt + 4)
+    ref, logits = m.generate(prompt, 4, logit_steps=4)
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=n_prompt + 4, seed=8, gain_std=0.1, runtime=rt)
+    out, _, _ = eng.generate(prompt, 4, stop_on_eos=False)
+    assert out.tolist() == ref.tolist()
+    assert np.array_equal(eng.logits(), logits[3])
+    eng.close()
+
+
+def test_baseline_workload_qwen3_0_6b(rt):
+    # 128 seeded prompt ids, 128 greedy steps
+    path = os.path.join(GOLDEN, "qwen3_qwen3-0.6b.json")
+    fx = json.load(open(path))
+    cfg = qwen3.preset("qwen3-0.6b")
+    eng = qwen3.Engine(cfg, max_seq=256, seed=fx["weight_seed"], gain_std=fx["gain_std"], runtime=rt)
+    prompt = np.array(fx["prompt"], np.uint32)
+    assert np.array_equal(prompt, qwen3.prompt_tokens(128, fx["prompt_seed"], cfg.vocab))
+    out, pm, dm = eng.generate(prompt, fx["new_tokens"], stop_on_eos=False)
+    print(f"0.6B: prompt {pm:.2f} ms, decode {dm:.2f} ms ({(len(out) - 1) / dm * 1e3:.1f} tok/s)")
+    # bit-exact canonical arithmetic: all 128 tokens equal the oracle's
+    assert out.tolist() == fx["oracle_tokens"]
+    # BASELINE bar against transformers: first 32 tokens identical
+    assert out[:32].tolist() == fx["hf_steps"][:32] == fx["hf_generate"][:32]
+    # logits of the first generated token: equal to the oracle's top-16,
+    # within 2e-2 of transformers'
+    eng.set_mode(qwen3.EAGER)
+    tok = 0
+    for p, t in enumerate(prompt):
+        tok = eng.decode(int(t), p)
+    row = orc.decode(eng.logits(), 0)
+    for i, v in fx["oracle_top16"][0]:
+        assert row[i] == np.float32(v)
+    for i, v in fx["hf_steps_top16"][0]:
+        assert abs(row[i] - v) <= 2e-2
+    assert tok == fx["hf_steps"][0]
+    eng.close()
+
+
+def write_checkpoint(directory, cfg, seed, gain_std, sharded=False, nan_embed=False):
+    import torch
+    from safetensors.torch import save_file
+
+    names = ["self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+             "self_attn.o_proj.weight", "self_attn.q_norm.weight", "self_attn.k_norm.weight",
+             "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight", "input_layernorm.weight",
+             "post_attention_layernorm.weight"]
+    h, hd = cfg.hidden, cfg.head_dim
+    shapes = [(cfg.heads * hd, h), (cfg.kv_heads * hd, h), (cfg.kv_heads * hd, h), (h, cfg.heads * hd), (hd,),
+              (hd,), (cfg.intermediate, h), (cfg.intermediate, h), (h, cfg.intermediate), (h,), (h,)]
+
+    def tensor(kind, layer, shape):
+        a = orc.fill_tensor(cfg, seed, gain_std, kind, layer)
+        return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).reshape(shape)
+
+    tensors = {}
+    for layer in range(cfg.layers):
+        for kind, (n, shape) in enumerate(zip(names, shapes)):
+            tensors[f"model.layers.{layer}.{n}"] = tensor(kind, layer, shape)
+    emb = tensor(orc.W_EMBED, 0, (cfg.vocab, h))
+    if nan_embed:
+        emb = emb.clone()
+        emb[:, 7] = float("nan")
+    tensors["model.embed_tokens.weight"] = emb
+    tensors["model.norm.weight"] = tensor(orc.W_FINALNORM, 0, (h,))
+    if not cfg.tied:
+        tensors["lm_head.weight"] = tensor(orc.W_LMHEAD, 0, (cfg.vocab, h))
+    config = {"hidden_size": h, "intermediate_size": cfg.intermediate, "head_dim": hd,
+              "num_attention_heads": cfg.heads, "num_key_value_heads": cfg.kv_heads,
+              "num_hidden_layers": cfg.layers, "vocab_size": cfg.vocab, "max_position_embeddings": 40960,
+              "eos_token_id": 151645, "rms_norm_eps": 1e-6, "rope_theta": 1000000.0,
+              "tie_word_embeddings": bool(cfg.tied), "hidden_act": "silu", "model_type": "qwen3",
+              "torch_dtype": "bfloat16", "rope_scaling": None}
+    with open(os.path.join(directory, "config.json"), "w") as fh:
+        json.dump(config, fh)
+    if not sharded:
+        save_file(tensors, os.path.join(directory, "model.safetensors"))
+        return
+    keys = sorted(tensors)
+    half = len(keys) // 2
+    shards = {"model-00001-of-00002.safetensors": keys[:half], "model-00002-of-00002.safetensors": keys[half:]}
+    weight_map = {}
+    for shard, ks in shards.items():
+        save_file({k: tensors[k] for k in ks}, os.path.join(directory, shard))
+        weight_map.update({k: shard for k in ks})
+    total = sum(t.numel() * 2 for t in tensors.values())
+    with open(os.path.join(directory, "model.safetensors.index.json"), "w") as fh:
+        json.dump({"metadata": {"total_size": total}, "weight_map": weight_map}, fh)
+
+
+@pytest.mark.parametrize("tied,sharded", [(1, False), (0, True)])
+def test_checkpoint_loading(rt, tmp_path, tied, sharded):
+    cfg = orc.config("tiny", tied=tied)
+    write_checkpoint(str(tmp_path), cfg, seed=11, gain_std=0.1, sharded=sharded)
+    eng = qwen3.Engine(runtime=rt, model_dir=str(tmp_path), max_seq=32)
+    assert eng.cfg.tied == tied and eng.cfg.hidden == cfg.hidden
+    m = orc.Model(cfg, seed=11, gain_std=0.1, max_seq=32)
+    prompt = orc.tokens(10, 2, cfg.vocab)
+    ref, _ = m.generate(prompt, 8)
+    out, _, _ = eng.generate(prompt, 8, stop_on_eos=False)
+    assert out.tolist() == ref.tolist()
+    eng.close()
+
+
+def test_non_finite_logits_raise(rt, tmp_path):
+    # main.cpp:223-224: a NaN anywhere in the logits is an error
+    cfg = orc.config("tiny")
+    write_checkpoint(str(tmp_path), cfg, seed=1, gain_std=0.0, nan_embed=True)
+    eng = qwen3.Engine(runtime=rt, model_dir=str(tmp_path), max_seq=16)
+    for mode in MODES:
+        eng.set_mode(mode)
+        with pytest.raises(xpu.XpuError, match="NaN"):
+            eng.decode(3, 0)
+    eng.close()
+
+
+def test_command_line_matches_oracle(tmp_path):
+    cfg = orc.config("tiny")
+    prompt = orc.tokens(12, 5, cfg.vocab)
+    ids = tmp_path / "ids.txt"
+    ids.write_text(" ".join(map(str, prompt.tolist())) + "\n")
+    m = orc.Model(cfg, seed=0, gain_std=0.0, max_seq=64)
+    ref, _ = m.generate(prompt, 10, stop_on_eos=True)
+    exe = os.path.join(xpu.BUILD_DIR, "qwen3_hip")
+    out = subprocess.run([exe, "--synthetic", "tiny", "--input-ids", str(ids), "--max-new-tokens", "10",
+                          "--max-seq-len", "64"], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert json.loads(out.stdout)["generated_ids"] == ref.tolist()
+    bad = subprocess.run([exe, "--synthetic", "tiny", "--input-ids", str(ids), "--max-new-tokens", "60",
+                          "--max-seq-len", "64"], capture_output=True, text=True, timeout=120)
+    assert bad.returncode == 1 and "exceeds --max-seq-len" in bad.stderr

@@ -126,7 +126,13 @@ def _declare(lib):
                 POINTER(c_double),
             ],
         ),
-        "xpu_qwen3_reset": (c_int, [c_void_p]),
+        "xpu_qwen3_read_config": (c_int, [c_char_p, POINTER(Qwen3Config)]),
+        "xpu_qwen3_get_config": (c_int, [c_void_p, POINTER(Qwen3Config)]),
+        "xpu_qwen3_create_from_checkpoint": (c_int, [c_void_p, c_char_p, c_uint32, POINTER(c_void_p)]),
+        "xpu_synth_tokens": (c_int, [c_void_p, c_uint64, c_uint64, c_uint32]),
+        "run_gemv": (c_int, [c_int, POINTER(c_char_p)]),
+        "run_gemm": (c_int, [c_int, POINTER(c_char_p)]),
+        "run_qwen3": (c_int, [c_int, POINTER(c_char_p)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

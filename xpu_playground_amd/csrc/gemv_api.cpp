@@ -36,7 +36,7 @@ int plan_gemv(const xpu_runtime &rt, int dtype, const void *A, const void *x, ui
   const bool vec = (reinterpret_cast<uintptr_t>(A) % 16 == 0) &&
                    (reinterpret_cast<uintptr_t>(x) % 16 == 0) && K % 8 == 0 && lda % 8 == 0;
   uint32_t rows = env_u32("XPU_GEMV_R", 1);
-  uint32_t unroll = env_u32("XPU_GEMV_U", 8);
+  uint32_t unroll = env_u32("XPU_GEMV_U", 4);
   const bool known = (rows == 1 && (unroll == 4 || unroll == 8 || unroll == 16)) ||
                      (rows == 2 && (unroll == 4 || unroll == 8)) || (rows == 4 && (unroll == 2 || unroll == 4));
   if (!known) rows = 1, unroll = 8;
@@ -50,7 +50,7 @@ int plan_gemv(const xpu_runtime &rt, int dtype, const void *A, const void *x, ui
   if (!vec) rows = 1, unroll = 2;
   plan.shared = global_x ? 0 : static_cast<uint32_t>(kpad * 2);
   const uint32_t per_cu_lds = std::max<uint32_t>(1, 163840u / std::max<uint32_t>(plan.shared, 4096));
-  const uint32_t blocks_per_cu = std::min<uint32_t>(env_u32("XPU_GEMV_BPC", 2), per_cu_lds);
+  const uint32_t blocks_per_cu = std::min<uint32_t>(env_u32("XPU_GEMV_BPC", 1), per_cu_lds);
   const uint64_t tiles = (static_cast<uint64_t>(M) + 4 * rows - 1) / (4 * rows);
   plan.grid = static_cast<uint32_t>(
       std::min<uint64_t>(tiles, static_cast<uint64_t>(rt.compute_units) * std::max(1u, blocks_per_cu)));

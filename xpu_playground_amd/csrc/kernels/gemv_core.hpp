@@ -63,9 +63,12 @@ XPU_DEVICE void fma_chunk(float (&acc)[R][8], const u32x4 (&a)[R], const u32x4 &
 // Canonical dot products of rows row0 .. row0+R-1 (indices clamped to M-1,
 // so rows past the end re-read the last row and are discarded by the
 // caller) with the LDS-staged vector xs. All lanes must be active.
-template <int DT, int R, int U, bool VEC>
+// PAIRED: rows r < R/2 are row0 + r and rows r >= R/2 are
+// row0 + pair_offset + r - R/2 (gate and up halves of a [gate; up] matrix).
+template <int DT, int R, int U, bool VEC, bool PAIRED = false>
 XPU_DEVICE void gemv_rows(const uint16_t *__restrict__ A, uint64_t lda, uint32_t K,
-                          uint32_t M, const uint16_t *xs, uint32_t row0, float (&out)[R]) {
+                          uint32_t M, const uint16_t *xs, uint32_t row0, float (&out)[R],
+                          uint32_t pair_offset = 0) {
   const uint32_t lane = lane_id();
   float acc[R][8];
 #pragma unroll
@@ -75,7 +78,8 @@ XPU_DEVICE void gemv_rows(const uint16_t *__restrict__ A, uint64_t lda, uint32_t
   const uint16_t *rows[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const uint32_t row = row0 + r < M ? row0 + r : M - 1;
+    const uint32_t want = PAIRED ? (r < R / 2 ? row0 + r : row0 + pair_offset + (r - R / 2)) : row0 + r;
+    const uint32_t row = want < M ? want : M - 1;
     rows[r] = A + static_cast<uint64_t>(row) * lda + lane * 8u;
   }
   const uint16_t *xl = xs + lane * 8u;

@@ -12,6 +12,7 @@
 //   xpu_q3_attention        QK-norm + RoPE + KV-cache write + attention
 //   xpu_q3_gemv_residual    o_proj / down_proj + residual add
 //   xpu_q3_norm_gemv_swiglu RMSNorm + gate/up projection + SiLU * up
+//                           (gate/up stored as one [gate; up] matrix)
 //   xpu_q3_norm_gemv_logits final RMSNorm + tied lm_head + per-block argmax
 //   xpu_q3_argmax_finish    argmax, next token, position advance
 // The decode position and token live in device memory (state[0], state[1])
@@ -217,26 +218,30 @@ XPU_DEVICE void q3_gemv_residual(const uint16_t *__restrict__ W, const uint16_t 
   });
 }
 
-// h[I] = bf16(bf16(silu(g)) * u), (g, u) = rows (2i, 2i+1) of the
-// interleaved gate/up matrix times rmsnorm(x)
+// h[i] = bf16(bf16(silu(g_i)) * u_i) for i < I, with g = gate . rmsnorm(x)
+// and u = up . rmsnorm(x) from the [gate; up] matrix (2I x K); a wavefront
+// computes P = R/2 consecutive outputs (rows i.. of each half).
 template <int R, int U>
 XPU_DEVICE void q3_norm_gemv_swiglu(const uint16_t *__restrict__ Wgu, const uint16_t *__restrict__ x,
                                     const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ h,
                                     uint32_t I, uint32_t K, float eps) {
   static_assert(R % 2 == 0, "gate/up rows come in pairs");
+  constexpr int P = R / 2;
   extern __shared__ __align__(16) uint16_t xs[];
   __shared__ float red[1];
   xpu::block_rmsnorm(xs, x, norm_w, K, eps, red);
-  const uint32_t lane = xpu::lane_id();
-  for_row_tiles<R, U>(Wgu, 2 * I, K, xs, [&](uint32_t row0, const float (&o)[R]) {
+  const uint32_t lane = xpu::lane_id(), wave = threadIdx.x >> 6;
+  const uint32_t per_block = (blockDim.x >> 6) * P;
+  for (uint32_t base = blockIdx.x * per_block; base < I; base += gridDim.x * per_block) {
+    const uint32_t i0 = base + wave * P;
+    if (i0 >= I) continue;
+    float o[R];
+    xpu::gemv_rows<xpu::kBf16, R, U, true, true>(Wgu, K, K, 2 * I, xs, i0, o, I);
 #pragma unroll
-    for (int r = 0; r < R; r += 2)
-      if (lane == static_cast<uint32_t>(r) && row0 + r < 2 * I) {
-        const float g = xpu::round_bf16(o[r]);
-        const float u = xpu::round_bf16(o[r + 1]);
-        h[(row0 + r) / 2] = static_cast<uint16_t>(silu_mul_code(g, u));
-      }
-  });
+    for (int p = 0; p < P; ++p)
+      if (lane == static_cast<uint32_t>(p) && i0 + p < I)
+        h[i0 + p] = static_cast<uint16_t>(silu_mul_code(xpu::round_bf16(o[p]), xpu::round_bf16(o[P + p])));
+  }
 }
 
 // logits[V] = E[V x K] . rmsnorm(x); block b also writes its (max, index,
@@ -273,24 +278,27 @@ XPU_DEVICE void q3_norm_gemv_logits(const uint16_t *__restrict__ E, const uint16
   }
 }
 
-#define XPU_Q3_GEMV_KERNELS(SUFFIX, R, U)                                                       \
+#define XPU_Q3_NORM_GEMV(SUFFIX, R, U)                                                          \
   extern "C" __global__ __launch_bounds__(256) void xpu_q3_norm_gemv##SUFFIX(                   \
       const uint16_t *__restrict__ W, uint16_t *x, const uint16_t *__restrict__ norm_w,         \
       uint16_t *__restrict__ out, uint32_t M, uint32_t K, float eps,                            \
       const uint16_t *__restrict__ embed, const uint32_t *__restrict__ state, uint32_t vocab) { \
     q3_norm_gemv<R, U>(W, x, norm_w, out, M, K, eps, embed, state, vocab);                      \
-  }                                                                                             \
+  }
+#define XPU_Q3_GEMV_RESIDUAL(SUFFIX, R, U)                                                      \
   extern "C" __global__ __launch_bounds__(256) void xpu_q3_gemv_residual##SUFFIX(               \
       const uint16_t *__restrict__ W, const uint16_t *__restrict__ v, uint16_t *x, uint32_t M,  \
       uint32_t K) {                                                                             \
     q3_gemv_residual<R, U>(W, v, x, M, K);                                                      \
-  }                                                                                             \
+  }
+#define XPU_Q3_SWIGLU(SUFFIX, R, U)                                                             \
   extern "C" __global__ __launch_bounds__(256) void xpu_q3_norm_gemv_swiglu##SUFFIX(            \
       const uint16_t *__restrict__ Wgu, const uint16_t *__restrict__ x,                         \
       const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ h, uint32_t I, uint32_t K,    \
       float eps) {                                                                              \
     q3_norm_gemv_swiglu<R, U>(Wgu, x, norm_w, h, I, K, eps);                                    \
-  }                                                                                             \
+  }
+#define XPU_Q3_LOGITS(SUFFIX, R, U)                                                             \
   extern "C" __global__ __launch_bounds__(256) void xpu_q3_norm_gemv_logits##SUFFIX(            \
       const uint16_t *__restrict__ E, const uint16_t *__restrict__ x,                           \
       const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ logits, uint32_t V,           \
@@ -299,8 +307,14 @@ XPU_DEVICE void q3_norm_gemv_logits(const uint16_t *__restrict__ E, const uint16
     q3_norm_gemv_logits<R, U>(E, x, norm_w, logits, V, K, eps, part_val, part_idx, part_bad);   \
   }
 
-XPU_Q3_GEMV_KERNELS(_r2, 2, 2)
-XPU_Q3_GEMV_KERNELS(_r4, 4, 2)
+XPU_Q3_NORM_GEMV(_r1, 1, 2)
+XPU_Q3_NORM_GEMV(_r2, 2, 2)
+XPU_Q3_GEMV_RESIDUAL(_r1, 1, 2)
+XPU_Q3_GEMV_RESIDUAL(_r2, 2, 2)
+XPU_Q3_SWIGLU(_r2, 2, 2)
+XPU_Q3_SWIGLU(_r4, 4, 2)
+XPU_Q3_LOGITS(_r2, 2, 2)
+XPU_Q3_LOGITS(_r4, 4, 2)
 
 // One block per query head: QK-norm + RoPE of q and of its kv head's k; the
 // first query head of each group writes k and v into the head-major cache at
@@ -341,12 +355,13 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
 
 // Reduce the per-block argmax partials; token = 0xffffffff if any logit was
 // non-finite. Then advance: position + 1, next token = next prompt id while
-// the prompt lasts, else the argmax; generated tokens are appended to gen.
+// the prompt lasts (state[3] = prompt length), else the argmax; the argmax
+// after position p >= prompt length - 1 is stored at gen[p + 1 - length].
+// state: [0] position, [1] input token, [2] last argmax, [3] prompt length.
 extern "C" __global__ __launch_bounds__(256) void xpu_q3_argmax_finish(
     const float *__restrict__ part_val, const uint32_t *__restrict__ part_idx,
     const uint32_t *__restrict__ part_bad, uint32_t nparts, uint32_t *state,
-    const uint32_t *__restrict__ prompt, uint32_t n_prompt, uint32_t *__restrict__ gen,
-    uint32_t gen_capacity) {
+    const uint32_t *__restrict__ prompt, uint32_t *__restrict__ gen, uint32_t gen_capacity) {
   __shared__ float redv[4];
   __shared__ uint32_t redi[4], redb[4];
   float best = -__builtin_inff();
@@ -358,7 +373,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_argmax_finish(
   xpu::block_argmax(best, best_index, bad, redv, redi, redb);
   if (threadIdx.x == 0) {
     const uint32_t token = bad ? 0xffffffffu : (best_index == 0xffffffffu ? 0u : best_index);
-    const uint32_t pos = state[0];
+    const uint32_t pos = state[0], n_prompt = state[3];
     const uint32_t next_pos = pos + 1;
     state[2] = token;
     state[1] = next_pos < n_prompt ? prompt[next_pos] : token;
