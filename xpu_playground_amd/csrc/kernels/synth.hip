@@ -50,3 +50,12 @@ extern "C" __global__ __launch_bounds__(256) void xpu_fill_reference_gemv(
     }
   }
 }
+
+// Plain streaming copy of n16 16-byte words, the known-traffic reference
+// against which the HBM byte counters of the other kernels are scaled.
+extern "C" __global__ __launch_bounds__(256) void xpu_stream_copy(const xpu::u32x4 *__restrict__ src,
+                                                                 xpu::u32x4 *__restrict__ dst, uint64_t n16) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride)
+    dst[i] = __builtin_nontemporal_load(src + i);
+}
