@@ -142,6 +142,29 @@ def cpu_baseline(m, k, dtype):
     }
 
 
+def traffic_workload() -> int:
+    """One xpu_stream_copy over 512 MiB (known traffic: 512 MiB read, 512 MiB
+    written) and one headline GEMV launch, so that rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE can be calibrated on the copy and applied to the
+    GEMV (profiles/gemv_fp16_16384_traffic.md)."""
+    import xpu_playground_amd as xpu
+    from xpu_playground_amd import Args
+
+    rt = xpu.Runtime()
+    n = 512 << 20
+    src, dst = rt.alloc(n), rt.alloc(n)
+    rt.fill_uniform(xpu.FP16, src, n // 2, 1)
+    rt.launch_grid("xpu_stream_copy", 4096, 256, 0, Args().ptr(src).ptr(dst).u64(n // 16))
+    m = k = 16384
+    a, x, y = rt.alloc(m * k * 2), rt.alloc(k * 2), rt.alloc(m * 2)
+    rt.fill_uniform(xpu.FP16, a, m * k, 3)
+    rt.fill_uniform(xpu.FP16, x, k, 4)
+    rt.gemv(xpu.FP16, a, x, y, m, k, k)
+    rt.synchronize()
+    log("traffic workload done")
+    return 0
+
+
 def read_traffic():
     """HBM bytes per launch of the headline kernel from the committed PMC
     summary (profiles/gemv_fp16_16384_traffic.md), if present."""
@@ -164,7 +187,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-workload", action="store_true",
+                    help="run one 512 MiB streaming copy and one GEMV launch (for rocprofv3 --pmc)")
     args = ap.parse_args()
+    if args.traffic_workload:
+        return traffic_workload()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the hot path is "
               "single-device and sharding is described in DESIGN.md", file=sys.stderr)

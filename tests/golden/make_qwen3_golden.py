@@ -50,7 +50,12 @@ def build_hf(preset: str, seed: int, gain_std: float):
                       rms_norm_eps=1e-6, rope_theta=1e6, tie_word_embeddings=True, hidden_act="silu",
                       attention_bias=False)
     cfg._attn_implementation = "eager"
-    model = Qwen3ForCausalLM(cfg).to(torch.bfloat16).eval()
+    # the way from_pretrained(..., torch_dtype=torch.bfloat16) builds it
+    # (qwen3/reference.py:15-24): parameters in bf16, while the RoPE inv_freq
+    # buffer, computed explicitly in FP32, stays FP32 (a blanket .to(bf16)
+    # would round it to bf16 and shift every cos/sin table entry)
+    model = Qwen3ForCausalLM._from_config(cfg, dtype=torch.bfloat16).eval()
+    assert model.model.rotary_emb.inv_freq.dtype == torch.float32
     oc = orc.config(preset)
     hd, h, inter = 128, p["hidden"], p["intermediate"]
 

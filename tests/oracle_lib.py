@@ -146,6 +146,13 @@ def encode(values: np.ndarray, dtype: int) -> np.ndarray:
     return out
 
 
+def bf16_ulp(value: float) -> float:
+    """Spacing of bf16 codes at |value| (the gap to the next code up)."""
+    code = int(encode(np.float32([abs(value)]), 0)[0])
+    pair = decode(np.array([code, code + 1], np.uint16), 0)
+    return float(pair[1] - pair[0])
+
+
 # ---------------------------------------------------------------- synth
 def uniform(n: int, seed: int, dtype: int) -> np.ndarray:
     out = np.empty(n, np.uint16)

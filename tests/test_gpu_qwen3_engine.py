@@ -77,20 +77,31 @@ def test_baseline_workload_qwen3_0_6b(rt):
     print(f"0.6B: prompt {pm:.2f} ms, decode {dm:.2f} ms ({(len(out) - 1) / dm * 1e3:.1f} tok/s)")
     # bit-exact canonical arithmetic: all 128 tokens equal the oracle's
     assert out.tolist() == fx["oracle_tokens"]
-    # BASELINE bar against transformers: first 32 tokens identical
+    # the decode bar against transformers: the first 32 tokens identical (all
+    # 128 equal its step-by-step decode)
     assert out[:32].tolist() == fx["hf_steps"][:32] == fx["hf_generate"][:32]
-    # logits of the first generated token: equal to the oracle's top-16,
-    # within 2e-2 of transformers'
+    assert out.tolist() == fx["hf_steps"]
+    # logits of the first 32 generated tokens: equal to the oracle's top-16;
+    # against transformers' top-16 within 2e-2 or 2 bf16 ulps of its value,
+    # whichever is larger (transformers' own batched-prompt and step paths
+    # differ by 0.031 = 2 ulps at |logit| in [2, 4) on these weights)
     eng.set_mode(qwen3.EAGER)
-    tok = 0
-    for p, t in enumerate(prompt):
-        tok = eng.decode(int(t), p)
-    row = orc.decode(eng.logits(), 0)
-    for i, v in fx["oracle_top16"][0]:
-        assert row[i] == np.float32(v)
-    for i, v in fx["hf_steps_top16"][0]:
-        assert abs(row[i] - v) <= 2e-2
-    assert tok == fx["hf_steps"][0]
+    eng_logits = []
+    token = int(prompt[0])
+    for p in range(128 + 31):
+        tok = eng.decode(token, p)
+        if p >= 127:
+            eng_logits.append(orc.decode(eng.logits(), 0))
+        token = int(prompt[p + 1]) if p + 1 < 128 else tok
+    worst = 0.0
+    for step, row in enumerate(eng_logits):
+        for i, v in fx["oracle_top16"][step]:
+            assert row[i] == np.float32(v), (step, i)
+        for i, v in fx["hf_steps_top16"][step]:
+            tol = max(2e-2, 2.0 * float(orc.bf16_ulp(v)))
+            assert abs(row[i] - v) <= tol, (step, i, row[i], v)
+            worst = max(worst, abs(row[i] - v))
+    print(f"max |logit - transformers| over 32 steps x top-16: {worst}")
     eng.close()
 
 

@@ -191,3 +191,15 @@ def test_argmax_tie_nan_and_random(rt):
     rand = b(np.random.default_rng(1).standard_normal(width))
     rt.copy_to(dl, rand)
     assert run() == orc.argmax(rand)
+
+
+def test_cpp_runtime_wrapper_dispatch_program():
+    # the same checks from C++ through include/xpu_runtime.hpp (the
+    # LevelZeroRuntime-shaped wrapper), at the 8B and 0.6B head layouts
+    import os
+    import subprocess
+
+    exe = os.path.join(xpu.BUILD_DIR, "qwen3_dispatch_test")
+    out = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert "kernel dispatch: PASS" in out.stdout

@@ -63,12 +63,42 @@ XPU_DEVICE void fma_chunk(float (&acc)[R][8], const u32x4 (&a)[R], const u32x4 &
 // Canonical dot products of rows row0 .. row0+R-1 (indices clamped to M-1,
 // so rows past the end re-read the last row and are discarded by the
 // caller) with the LDS-staged vector xs. All lanes must be active.
+// Row pointers (lane offset included) of the R rows a wavefront computes.
 // PAIRED: rows r < R/2 are row0 + r and rows r >= R/2 are
 // row0 + pair_offset + r - R/2 (gate and up halves of a [gate; up] matrix).
+// Indices past M are clamped to M - 1 (re-read and discarded by the caller).
+template <int R, bool PAIRED = false>
+XPU_DEVICE void gemv_row_ptrs(const uint16_t *__restrict__ A, uint64_t lda, uint32_t M, uint32_t row0,
+                              uint32_t pair_offset, const uint16_t *(&rows)[R]) {
+  const uint32_t lane = lane_id();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t want = PAIRED ? (r < R / 2 ? row0 + r : row0 + pair_offset + (r - R / 2)) : row0 + r;
+    const uint32_t row = want < M ? want : M - 1;
+    rows[r] = A + static_cast<uint64_t>(row) * lda + lane * 8u;
+  }
+}
+
+template <int R, int U, bool VEC>
+XPU_DEVICE void gemv_load_batch(u32x4 (&buf)[U][R], const uint16_t *const (&rows)[R], uint32_t j0,
+                                uint32_t K) {
+  const uint32_t lane = lane_id();
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      buf[u][r] = load_row8<VEC>(rows[r] + (j0 + u) * 512u, (j0 + u) * 512u + lane * 8u, K);
+}
+
+// Canonical dot products of R rows (see gemv_row_ptrs) with the staged
+// vector xs. All lanes must be active. When use_first is set (wave-uniform),
+// `first` holds the rows' first batch (chunks 0..U-1), loaded earlier by the
+// caller with gemv_load_batch so that its latency overlaps other work; it is
+// only used when K has at least U full chunks.
 template <int DT, int R, int U, bool VEC, bool PAIRED = false>
-XPU_DEVICE void gemv_rows(const uint16_t *__restrict__ A, uint64_t lda, uint32_t K,
-                          uint32_t M, const uint16_t *xs, uint32_t row0, float (&out)[R],
-                          uint32_t pair_offset = 0) {
+XPU_DEVICE void gemv_rows_first(const uint16_t *__restrict__ A, uint64_t lda, uint32_t K,
+                                uint32_t M, const uint16_t *xs, uint32_t row0, float (&out)[R],
+                                uint32_t pair_offset, const u32x4 (&first)[U][R], bool use_first) {
   const uint32_t lane = lane_id();
   float acc[R][8];
 #pragma unroll
@@ -76,25 +106,14 @@ XPU_DEVICE void gemv_rows(const uint16_t *__restrict__ A, uint64_t lda, uint32_t
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
   const uint16_t *rows[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const uint32_t want = PAIRED ? (r < R / 2 ? row0 + r : row0 + pair_offset + (r - R / 2)) : row0 + r;
-    const uint32_t row = want < M ? want : M - 1;
-    rows[r] = A + static_cast<uint64_t>(row) * lda + lane * 8u;
-  }
+  gemv_row_ptrs<R, PAIRED>(A, lda, M, row0, pair_offset, rows);
   const uint16_t *xl = xs + lane * 8u;
   const uint32_t nfull = K / 512u;
   // Batches of U chunks (U x R 16-byte loads per lane) are software
   // pipelined: the loads of batch j + U are issued before the FMAs of batch
   // j, and a scheduling barrier keeps the compiler from interleaving each
   // load with its use (which would leave one load in flight per wave).
-  auto load_batch = [&](u32x4 (&buf)[U][R], uint32_t j0) {
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        buf[u][r] = load_row8<VEC>(rows[r] + (j0 + u) * 512u, (j0 + u) * 512u + lane * 8u, K);
-  };
+  auto load_batch = [&](u32x4 (&buf)[U][R], uint32_t j0) { gemv_load_batch<R, U, VEC>(buf, rows, j0, K); };
   auto fma_batch = [&](const u32x4 (&buf)[U][R], uint32_t j0) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -103,7 +122,14 @@ XPU_DEVICE void gemv_rows(const uint16_t *__restrict__ A, uint64_t lda, uint32_t
   uint32_t j = 0;
   if (nfull >= static_cast<uint32_t>(U)) {
     u32x4 b0[U][R], b1[U][R];
-    load_batch(b0, 0);
+    if (use_first) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int r = 0; r < R; ++r) b0[u][r] = first[u][r];
+    } else {
+      load_batch(b0, 0);
+    }
     while (true) {
       if (j + 2 * U > nfull) { fma_batch(b0, j); j += U; break; }
       load_batch(b1, j + U);
@@ -134,6 +160,13 @@ XPU_DEVICE void gemv_rows(const uint16_t *__restrict__ A, uint64_t lda, uint32_t
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) out[r] = wave_butterfly(fold8(acc[r]));
+}
+
+template <int DT, int R, int U, bool VEC, bool PAIRED = false>
+XPU_DEVICE void gemv_rows(const uint16_t *__restrict__ A, uint64_t lda, uint32_t K, uint32_t M,
+                          const uint16_t *xs, uint32_t row0, float (&out)[R], uint32_t pair_offset = 0) {
+  u32x4 unused[U][R];
+  gemv_rows_first<DT, R, U, VEC, PAIRED>(A, lda, K, M, xs, row0, out, pair_offset, unused, false);
 }
 
 }  // namespace xpu

@@ -15,9 +15,10 @@ constexpr uint32_t kHeadDim = 128;
 constexpr uint32_t kAttnChunk = 4096;  // positions per softmax / P.V chunk
 
 // Block-cooperative RMSNorm of x[0..W) into LDS buffer xs (bf16 codes,
-// zero-padded to a multiple of 512). xs may alias nothing else; red is one
-// float of LDS. qwen3/kernels.hpp:43-54 with transformers rounding:
+// zero-padded to a multiple of 512). red is one float of LDS.
+// qwen3/kernels.hpp:43-54 with transformers rounding:
 // out = bf16(w * bf16(x * (1 / sqrt(sum(x^2) / W + eps)))).
+// Generic form: any width, any alignment.
 XPU_DEVICE void block_rmsnorm(uint16_t *xs, const uint16_t *__restrict__ x,
                               const uint16_t *__restrict__ w, uint32_t W, float eps, float *red) {
   const uint32_t wpad = (W + 511u) & ~511u;
@@ -41,6 +42,62 @@ XPU_DEVICE void block_rmsnorm(uint16_t *xs, const uint16_t *__restrict__ x,
   for (uint32_t i = threadIdx.x; i < W; i += blockDim.x)
     xs[i] = static_cast<uint16_t>(
         f32_to_bf16(bf16_to_f32(w[i]) * round_bf16(bf16_to_f32(xs[i]) * scale)));
+  __syncthreads();
+}
+
+// Same result for 16-byte aligned x, w with W a multiple of 8 and
+// W <= 8 * 8 * blockDim: x and the gains are fetched together with 16-byte
+// loads (one memory round trip) and kept in registers.
+XPU_DEVICE void block_rmsnorm_vec(uint16_t *xs, const uint16_t *__restrict__ x,
+                                  const uint16_t *__restrict__ w, uint32_t W, float eps, float *red) {
+  constexpr int kGroups = 8;
+  const uint32_t wpad = (W + 511u) & ~511u;
+  u32x4 xv[kGroups], wv[kGroups];
+#pragma unroll
+  for (int q = 0; q < kGroups; ++q) {
+    const uint32_t i = (threadIdx.x + q * blockDim.x) * 8u;
+    if (i < W) {
+      xv[q] = *reinterpret_cast<const u32x4 *>(x + i);
+      wv[q] = *reinterpret_cast<const u32x4 *>(w + i);
+    } else {
+      xv[q] = u32x4{0, 0, 0, 0};
+      wv[q] = u32x4{0, 0, 0, 0};
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kGroups; ++q) {
+    const uint32_t i = (threadIdx.x + q * blockDim.x) * 8u;
+    if (i < wpad) *reinterpret_cast<u32x4 *>(xs + i) = xv[q];
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const uint32_t lane = threadIdx.x;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t j = 0; j < wpad; j += 512u) {
+      float f[8];
+      unpack8<kBf16>(*reinterpret_cast<const u32x4 *>(xs + j + lane * 8u), f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(f[e], f[e], acc[e]);
+    }
+    const float ss = wave_butterfly(fold8(acc));
+    if (lane == 0) red[0] = 1.0f / __builtin_sqrtf(ss / static_cast<float>(W) + eps);
+  }
+  __syncthreads();
+  const float scale = red[0];
+#pragma unroll
+  for (int q = 0; q < kGroups; ++q) {
+    const uint32_t i = (threadIdx.x + q * blockDim.x) * 8u;
+    if (i < W) {
+      float xf[8], wf[8];
+      unpack8<kBf16>(xv[q], xf);
+      unpack8<kBf16>(wv[q], wf);
+      uint32_t c[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) c[e] = f32_to_bf16(wf[e] * round_bf16(xf[e] * scale));
+      *reinterpret_cast<u32x4 *>(xs + i) =
+          u32x4{c[0] | (c[1] << 16), c[2] | (c[3] << 16), c[4] | (c[5] << 16), c[6] | (c[7] << 16)};
+    }
+  }
   __syncthreads();
 }
 
@@ -112,46 +169,66 @@ XPU_DEVICE float block_max(float v, float *red) {
 
 // Attention score of query qs (LDS, roped bf16) against key row krow:
 // bf16(bf16(lane-local 8-slot dot) * scale) (transformers eager: bf16 matmul
-// then bf16 * scaling).
+// then bf16 * scaling). The 16 row loads are independent and issued
+// together.
 XPU_DEVICE float attention_score(const uint16_t *qs, const uint16_t *krow, float scale) {
+  u32x4 kv[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) kv[j] = *reinterpret_cast<const u32x4 *>(krow + j * 8);
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll 4
-  for (uint32_t j = 0; j < kHeadDim; j += 8u) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
     float q[8], k[8];
-    unpack8<kBf16>(*reinterpret_cast<const u32x4 *>(qs + j), q);
-    unpack8<kBf16>(*reinterpret_cast<const u32x4 *>(krow + j), k);
+    unpack8<kBf16>(*reinterpret_cast<const u32x4 *>(qs + j * 8), q);
+    unpack8<kBf16>(kv[j], k);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(q[e], k[e], acc[e]);
   }
   return round_bf16(round_bf16(fold8(acc)) * scale);
 }
 
+constexpr uint32_t kAttnTile = 256;             // positions per V tile in LDS
+constexpr uint32_t kVPitch = kHeadDim + 8;      // LDS row pitch of the V tile (bank spread)
+
 // Single-query attention of one head with a 256-thread block
 // (qwen3/kernels.hpp:157-192): positions 0..n-1, row t of K/V at
 // kbase/vbase + t * stride, except that when HAS_CURRENT the last position
 // reads kcur/vcur (the new token, not yet visible in the cache).
 // p_t = bf16(exp(s_t - max) * (1 / sum_t exp)), out = bf16(sum_t p_t v_t).
-// sbuf: kAttnChunk floats of LDS; red: >= 4*128 floats of LDS.
+// sbuf: kAttnChunk floats of LDS; vtile: kAttnTile * kVPitch codes of LDS;
+// red: >= 4*128 floats of LDS. Position t is handled by thread t % 256 in
+// the score pass; V rows go through vtile so that the P.V pass reads LDS.
 template <bool HAS_CURRENT>
 XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const uint16_t *vbase,
                                uint64_t stride, uint32_t n, const uint16_t *kcur,
                                const uint16_t *vcur, float scale, uint16_t *out, float *sbuf,
-                               float *red) {
+                               uint16_t *vtile, float *red) {
   const uint32_t tid = threadIdx.x;
   const uint32_t nchunks = (n + kAttnChunk - 1) / kAttnChunk;
+  const bool single_tile = n <= kAttnTile;
   auto krow_of = [&](uint32_t t) -> const uint16_t * {
     return (HAS_CURRENT && t + 1 == n) ? kcur : kbase + static_cast<uint64_t>(t) * stride;
   };
   auto vrow_of = [&](uint32_t t) -> const uint16_t * {
     return (HAS_CURRENT && t + 1 == n) ? vcur : vbase + static_cast<uint64_t>(t) * stride;
   };
-  // pass 1: scores (kept in sbuf when one chunk holds them all) and the max
+  auto stage_v_row = [&](uint32_t t, uint32_t slot) {
+    const uint16_t *src = vrow_of(t);
+    u32x4 vv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) vv[j] = *reinterpret_cast<const u32x4 *>(src + j * 8);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) *reinterpret_cast<u32x4 *>(vtile + slot * kVPitch + j * 8) = vv[j];
+  };
+  // pass 1: scores (kept in sbuf when one chunk holds them all) and the max;
+  // a single-tile context also stages its V rows here
   float local_max = -__builtin_inff();
   for (uint32_t c = 0; c < nchunks; ++c) {
     const uint32_t base = c * kAttnChunk;
     const uint32_t len = min(kAttnChunk, n - base);
     for (uint32_t i = tid; i < len; i += blockDim.x) {
       const float s = attention_score(qs, krow_of(base + i), scale);
+      if (single_tile) stage_v_row(base + i, i);
       sbuf[i] = s;
       local_max = fmaxf(local_max, s);
     }
@@ -169,7 +246,7 @@ XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const 
     __syncthreads();
     if (tid < 64) {
       float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (uint32_t j = 0; j < kAttnChunk; j += 512u)
+      for (uint32_t j = 0; j < len; j += 512u)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const uint32_t k = j + tid * 8u + e;
@@ -185,7 +262,7 @@ XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const 
   const float inv = red[0];
   __syncthreads();
   // pass 3: probabilities and P.V in 16 residue classes (wave w owns
-  // residues 4w..4w+3, lane l owns dims 2l and 2l+1)
+  // residues 4w..4w+3, lane l owns dims 2l and 2l+1), V read from LDS
   const uint32_t wave = tid >> 6, lane = lane_id();
   float tot[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
   for (uint32_t c = 0; c < nchunks; ++c) {
@@ -198,17 +275,31 @@ XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const 
     }
     __syncthreads();
     float part[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
-    for (uint32_t i0 = 0; i0 < len; i0 += 16u) {
+    for (uint32_t i0 = 0; i0 < len; i0 += kAttnTile) {
+      const uint32_t tile_len = min(kAttnTile, len - i0);
+      if (!single_tile) {
+        if (tid < tile_len) stage_v_row(base + i0 + tid, tid);
+        __syncthreads();
+      }
+      for (uint32_t ii = 0; ii < tile_len; ii += 16u) {
+        float pt[4];
+        uint32_t vv[4];
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const uint32_t i = i0 + wave * 4u + rr;
-        if (i < len) {
-          const float pt = sbuf[i];
-          const uint32_t vv = *reinterpret_cast<const uint32_t *>(vrow_of(base + i) + lane * 2u);
-          part[rr][0] = __builtin_fmaf(pt, lo16<kBf16>(vv), part[rr][0]);
-          part[rr][1] = __builtin_fmaf(pt, hi16<kBf16>(vv), part[rr][1]);
+        for (int rr = 0; rr < 4; ++rr) {
+          const uint32_t i = ii + wave * 4u + rr;
+          const bool ok = i < tile_len;
+          pt[rr] = ok ? sbuf[i0 + i] : 0.0f;
+          vv[rr] = ok ? *reinterpret_cast<const uint32_t *>(vtile + i * kVPitch + lane * 2u) : 0u;
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          if (ii + wave * 4u + rr < tile_len) {
+            part[rr][0] = __builtin_fmaf(pt[rr], lo16<kBf16>(vv[rr]), part[rr][0]);
+            part[rr][1] = __builtin_fmaf(pt[rr], hi16<kBf16>(vv[rr]), part[rr][1]);
+          }
         }
       }
+      if (!single_tile) __syncthreads();
     }
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {

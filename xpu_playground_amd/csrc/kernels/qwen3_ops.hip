@@ -103,6 +103,7 @@ extern "C" __global__ __launch_bounds__(256) void QwenAttention(
   __shared__ float sbuf[xpu::kAttnChunk];
   __shared__ float red[4 * xpu::kHeadDim];
   __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
+  __shared__ __align__(16) uint16_t vtile[xpu::kAttnTile * xpu::kVPitch];
   const uint32_t head = blockIdx.x;
   if (head >= heads) return;
   const uint32_t kv = head / (heads / kv_heads);
@@ -111,7 +112,7 @@ extern "C" __global__ __launch_bounds__(256) void QwenAttention(
   const uint64_t stride = static_cast<uint64_t>(kv_heads) * xpu::kHeadDim;
   xpu::attention_head<false>(qs, key_cache + kv * xpu::kHeadDim, value_cache + kv * xpu::kHeadDim,
                              stride, position + 1, nullptr, nullptr, 0.08838834764831845f,
-                             output + head * xpu::kHeadDim, sbuf, red);
+                             output + head * xpu::kHeadDim, sbuf, vtile, red);
 }
 
 // kernels.hpp:194-207: left = bf16(left + right)
@@ -156,18 +157,37 @@ extern "C" __global__ __launch_bounds__(1024) void QwenArgmax(const uint16_t *__
 
 namespace {
 
-// Grid-stride loop over tiles of 4 wavefronts x R rows; body(row0, out[R]).
-template <int R, int U, typename Body>
-XPU_DEVICE void for_row_tiles(const uint16_t *__restrict__ W, uint32_t M, uint32_t K,
-                              const uint16_t *xs, Body body) {
+// Grid-stride loop of a fused GEMV kernel over output units (rows, or row
+// pairs when PAIRED) in tiles of 4 wavefronts; each wavefront computes R
+// rows. The first tile's first load batch is issued before the prologue
+// (which stages the input vector in LDS) so that the weight stream's latency
+// overlaps it. body(unit0, out[R]).
+template <int R, int U, bool PAIRED, typename Prologue, typename Body>
+XPU_DEVICE void fused_gemv(const uint16_t *__restrict__ W, uint32_t units, uint32_t K, const uint16_t *xs,
+                           Prologue prologue, Body body) {
+  constexpr uint32_t per_wave = PAIRED ? R / 2 : R;
   const uint32_t wave = threadIdx.x >> 6;
-  const uint32_t rows_per_block = (blockDim.x >> 6) * R;
-  for (uint32_t base = blockIdx.x * rows_per_block; base < M; base += gridDim.x * rows_per_block) {
-    const uint32_t row0 = base + wave * R;
-    if (row0 >= M) continue;
+  const uint32_t per_block = (blockDim.x >> 6) * per_wave;
+  const uint32_t rows_total = PAIRED ? 2 * units : units;
+  const uint32_t pair_offset = PAIRED ? units : 0;
+  xpu::u32x4 first[U][R];
+  bool have_first = false;
+  uint32_t base = blockIdx.x * per_block;
+  if (base + wave * per_wave < units && K / 512u >= static_cast<uint32_t>(U)) {
+    const uint16_t *rows[R];
+    xpu::gemv_row_ptrs<R, PAIRED>(W, K, rows_total, base + wave * per_wave, pair_offset, rows);
+    xpu::gemv_load_batch<R, U, true>(first, rows, 0, K);
+    have_first = true;
+  }
+  prologue();
+  for (; base < units; base += gridDim.x * per_block) {
+    const uint32_t u0 = base + wave * per_wave;
+    if (u0 >= units) continue;
     float out[R];
-    xpu::gemv_rows<xpu::kBf16, R, U, true>(W, K, K, M, xs, row0, out);
-    body(row0, out);
+    xpu::gemv_rows_first<xpu::kBf16, R, U, true, PAIRED>(W, K, K, rows_total, xs, u0, out, pair_offset,
+                                                         first, have_first);
+    have_first = false;
+    body(u0, out);
   }
 }
 
@@ -190,14 +210,15 @@ XPU_DEVICE void q3_norm_gemv(const uint16_t *__restrict__ W, uint16_t *x,
     if (blockIdx.x == 0)
       for (uint32_t i = threadIdx.x; i < K; i += blockDim.x) x[i] = src[i];
   }
-  xpu::block_rmsnorm(xs, src, norm_w, K, eps, red);
   const uint32_t lane = xpu::lane_id();
-  for_row_tiles<R, U>(W, M, K, xs, [&](uint32_t row0, const float (&o)[R]) {
+  fused_gemv<R, U, false>(
+      W, M, K, xs, [&] { xpu::block_rmsnorm_vec(xs, src, norm_w, K, eps, red); },
+      [&](uint32_t row0, const float (&o)[R]) {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (lane == static_cast<uint32_t>(r) && row0 + r < M)
-        out[row0 + r] = static_cast<uint16_t>(xpu::f32_to_bf16(o[r]));
-  });
+        for (int r = 0; r < R; ++r)
+          if (lane == static_cast<uint32_t>(r) && row0 + r < M)
+            out[row0 + r] = static_cast<uint16_t>(xpu::f32_to_bf16(o[r]));
+      });
 }
 
 // x[M] = bf16(x + bf16(W[M x K] . v))
@@ -205,17 +226,21 @@ template <int R, int U>
 XPU_DEVICE void q3_gemv_residual(const uint16_t *__restrict__ W, const uint16_t *__restrict__ v,
                                  uint16_t *x, uint32_t M, uint32_t K) {
   extern __shared__ __align__(16) uint16_t xs[];
-  xpu::stage_vector<true>(xs, v, K, (K + 511u) & ~511u);
-  __syncthreads();
   const uint32_t lane = xpu::lane_id();
-  for_row_tiles<R, U>(W, M, K, xs, [&](uint32_t row0, const float (&o)[R]) {
+  fused_gemv<R, U, false>(
+      W, M, K, xs,
+      [&] {
+        xpu::stage_vector<true>(xs, v, K, (K + 511u) & ~511u);
+        __syncthreads();
+      },
+      [&](uint32_t row0, const float (&o)[R]) {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (lane == static_cast<uint32_t>(r) && row0 + r < M) {
-        const float sum = xpu::bf16_to_f32(x[row0 + r]) + xpu::round_bf16(o[r]);
-        x[row0 + r] = static_cast<uint16_t>(xpu::f32_to_bf16(sum));
-      }
-  });
+        for (int r = 0; r < R; ++r)
+          if (lane == static_cast<uint32_t>(r) && row0 + r < M) {
+            const float sum = xpu::bf16_to_f32(x[row0 + r]) + xpu::round_bf16(o[r]);
+            x[row0 + r] = static_cast<uint16_t>(xpu::f32_to_bf16(sum));
+          }
+      });
 }
 
 // h[i] = bf16(bf16(silu(g_i)) * u_i) for i < I, with g = gate . rmsnorm(x)
@@ -229,19 +254,15 @@ XPU_DEVICE void q3_norm_gemv_swiglu(const uint16_t *__restrict__ Wgu, const uint
   constexpr int P = R / 2;
   extern __shared__ __align__(16) uint16_t xs[];
   __shared__ float red[1];
-  xpu::block_rmsnorm(xs, x, norm_w, K, eps, red);
-  const uint32_t lane = xpu::lane_id(), wave = threadIdx.x >> 6;
-  const uint32_t per_block = (blockDim.x >> 6) * P;
-  for (uint32_t base = blockIdx.x * per_block; base < I; base += gridDim.x * per_block) {
-    const uint32_t i0 = base + wave * P;
-    if (i0 >= I) continue;
-    float o[R];
-    xpu::gemv_rows<xpu::kBf16, R, U, true, true>(Wgu, K, K, 2 * I, xs, i0, o, I);
+  const uint32_t lane = xpu::lane_id();
+  fused_gemv<R, U, true>(
+      Wgu, I, K, xs, [&] { xpu::block_rmsnorm_vec(xs, x, norm_w, K, eps, red); },
+      [&](uint32_t i0, const float (&o)[R]) {
 #pragma unroll
-    for (int p = 0; p < P; ++p)
-      if (lane == static_cast<uint32_t>(p) && i0 + p < I)
-        h[i0 + p] = static_cast<uint16_t>(silu_mul_code(xpu::round_bf16(o[p]), xpu::round_bf16(o[P + p])));
-  }
+        for (int p = 0; p < P; ++p)
+          if (lane == static_cast<uint32_t>(p) && i0 + p < I)
+            h[i0 + p] = static_cast<uint16_t>(silu_mul_code(xpu::round_bf16(o[p]), xpu::round_bf16(o[P + p])));
+      });
 }
 
 // logits[V] = E[V x K] . rmsnorm(x); block b also writes its (max, index,
@@ -255,21 +276,22 @@ XPU_DEVICE void q3_norm_gemv_logits(const uint16_t *__restrict__ E, const uint16
   __shared__ float red[1];
   __shared__ float redv[4];
   __shared__ uint32_t redi[4], redb[4];
-  xpu::block_rmsnorm(xs, x, norm_w, K, eps, red);
   const uint32_t lane = xpu::lane_id();
   float best = -__builtin_inff();
   uint32_t best_index = 0xffffffffu, bad = 0;
-  for_row_tiles<R, U>(E, V, K, xs, [&](uint32_t row0, const float (&o)[R]) {
+  fused_gemv<R, U, false>(
+      E, V, K, xs, [&] { xpu::block_rmsnorm_vec(xs, x, norm_w, K, eps, red); },
+      [&](uint32_t row0, const float (&o)[R]) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if (row0 + r >= V) break;
-      const uint32_t code = xpu::f32_to_bf16(o[r]);
-      if (lane == static_cast<uint32_t>(r)) logits[row0 + r] = static_cast<uint16_t>(code);
-      const float v = xpu::bf16_to_f32(code);
-      if (!xpu::finite_f(v)) bad = 1;
-      xpu::argmax_merge(best, best_index, v, row0 + r);
-    }
-  });
+        for (int r = 0; r < R; ++r) {
+          if (row0 + r >= V) break;
+          const uint32_t code = xpu::f32_to_bf16(o[r]);
+          if (lane == static_cast<uint32_t>(r)) logits[row0 + r] = static_cast<uint16_t>(code);
+          const float v = xpu::bf16_to_f32(code);
+          if (!xpu::finite_f(v)) bad = 1;
+          xpu::argmax_merge(best, best_index, v, row0 + r);
+        }
+      });
   xpu::block_argmax(best, best_index, bad, redv, redi, redb);
   if (threadIdx.x == 0) {
     part_val[blockIdx.x] = best;
@@ -329,6 +351,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   __shared__ float red[4 * xpu::kHeadDim];
   __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
   __shared__ __align__(16) uint16_t ks[xpu::kHeadDim];
+  __shared__ __align__(16) uint16_t vtile[xpu::kAttnTile * xpu::kVPitch];
   const uint32_t head = blockIdx.x;
   const uint32_t pos = state[0];
   if (head >= heads || pos >= max_seq) return;
@@ -350,7 +373,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
     vcache[slot] = vsrc[threadIdx.x];
   }
   xpu::attention_head<true>(qs, kcache + head_base, vcache + head_base, xpu::kHeadDim, pos + 1, ks,
-                            vsrc, scale, out + head * xpu::kHeadDim, sbuf, red);
+                            vsrc, scale, out + head * xpu::kHeadDim, sbuf, vtile, red);
 }
 
 // Reduce the per-block argmax partials; token = 0xffffffff if any logit was
