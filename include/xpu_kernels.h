@@ -60,6 +60,27 @@ int xpu_fill_reference_gemv(xpu_runtime *rt, int dtype, void *matrix, void *vect
 int run_gemv(int argc, char **argv);
 int run_gemm(int argc, char **argv);
 
+/* Peak-rate microbenchmarks, the measured ceilings of the rooflines.
+ * xpu_peak_mfma: `blocks` x 256 threads, each wavefront running `rounds`
+ * batches of 8 independent v_mfma_f32_32x32x16_bf16 on the 8 bf16 codes at
+ * `operand` (replaces peak_compute_dpas_kernel.cpp:10-68); sink receives one
+ * float per thread (28 + 32 * rounds for operands of 0.5) and clock four
+ * uint64 (shader clock and constant-rate clock before / after the loop of
+ * block 0). xpu_peak_read: streaming 16-byte reads of `bytes` (replaces
+ * peak_mem_2d_kernel.cpp:13-52); sink needs blocks * 1024 bytes. */
+int xpu_peak_mfma(xpu_runtime *rt, const void *operand, void *sink, void *clock, uint32_t blocks,
+                  uint32_t rounds);
+int xpu_peak_read(xpu_runtime *rt, const void *input, uint64_t bytes, void *sink, uint32_t blocks);
+
+/* run_peak_compute: peak_compute_dpas.cpp (--waves-per-simd N (2),
+ *   --rounds N (8192), --iterations N (100)); prints median / best TFLOP/s
+ *   against 2500 TFLOP/s, the shader clock during the loop, checksum.
+ * run_peak_mem: peak_mem_2d.cpp (--size-mib N (4096), --iterations N (100));
+ *   prints median / best read GB/s against 8000 GB/s.
+ * 0 on success, 1 on error. */
+int run_peak_compute(int argc, char **argv);
+int run_peak_mem(int argc, char **argv);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,13 +61,22 @@ def test_runtime_errors_cross_the_abi_as_codes():
     assert lib.xpu_module_kernel_names(b"/nonexistent.hsaco", ctypes.create_string_buffer(16), 16) == 3
 
 
-@pytest.mark.parametrize("program", ["gemv", "gemm", "qwen3_hip"])
+@pytest.mark.parametrize("program", ["gemv", "gemm", "qwen3_hip", "peak compute", "peak mem", "peak gemm"])
 def test_cli_rejects_bad_flags_without_touching_a_gpu(program):
-    exe = os.path.join(xpu.BUILD_DIR, program)
-    if program == "qwen3_hip" and not os.path.exists(os.path.join(INCLUDE, "xpu_qwen3.h")):
-        pytest.skip("qwen3 engine not built yet")
-    out = subprocess.run([exe, "--bogus", "1"], capture_output=True, text=True, timeout=60)
+    program, *mode = program.split()
+    exe = [os.path.join(xpu.BUILD_DIR, program)] + mode
+    out = subprocess.run(exe + ["--bogus", "1"], capture_output=True, text=True, timeout=60)
     assert out.returncode == 1
     assert "unknown option" in out.stderr
-    out = subprocess.run([exe, "--help"], capture_output=True, text=True, timeout=60)
+    out = subprocess.run(exe + ["--help"], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0 and "Usage" in out.stdout
+
+
+def test_peak_launcher_modes():
+    exe = os.path.join(xpu.BUILD_DIR, "peak")
+    out = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 1 and "missing benchmark mode" in out.stderr
+    out = subprocess.run([exe, "flops"], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 1 and "unknown benchmark mode" in out.stderr
+    out = subprocess.run([exe, "--help"], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0 and "compute" in out.stdout and "mem" in out.stdout

@@ -4,11 +4,31 @@
 #include "host_common.hpp"
 #include "runtime_internal.hpp"
 
+#include <algorithm>
 #include <cstdlib>
 #include <iomanip>
 #include <iostream>
 
 using xpu::set_error;
+
+namespace {
+
+uint64_t round_up8(uint64_t v) { return (v + 7) & ~uint64_t{7}; }
+
+// Copies a rows x cols matrix (row stride src_ld) into dst with dst_cols
+// columns, zero-filling columns cols..dst_cols-1 (kernels/gemm.hip
+// xpu_pad_rows).
+int pad_rows(xpu_runtime *rt, const void *src, uint64_t src_ld, uint32_t rows, uint32_t cols, void *dst,
+             uint32_t dst_cols) {
+  const xpu::KernelInfo *k = rt->find_exact("xpu_pad_rows");
+  if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: xpu_pad_rows");
+  const uint64_t threads = static_cast<uint64_t>(rows) * (dst_cols / 8);
+  const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>((threads + 255) / 256, rt->compute_units * 16ull));
+  const xpu_kernel_arg args[] = {{8, &src}, {8, &src_ld}, {4, &rows}, {4, &cols}, {8, &dst}, {4, &dst_cols}};
+  return rt->launch(*k, std::max(grid, 1u), 1, 256, 0, args, 6);
+}
+
+}  // namespace
 
 extern "C" int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
                         uint32_t M, uint32_t N, uint32_t K) {
@@ -16,15 +36,43 @@ extern "C" int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B
   if (dtype != XPU_DTYPE_BF16 && dtype != XPU_DTYPE_FP16)
     return set_error(XPU_ERR_INVALID, "xpu_gemm: dtype must be bf16 (0) or fp16 (1)");
   if (M == 0 || N == 0 || K == 0) return set_error(XPU_ERR_INVALID, "xpu_gemm: M, N, K must be positive");
-  const bool vec = reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0 &&
-                   K % 8 == 0 && N % 8 == 0;
-  const std::string name = std::string("xpu_gemm_") + (dtype ? "fp16" : "bf16") + (vec ? "_vec" : "_any");
+  // 32-bit buffer offsets: 256 rows of A and 64 rows of B per K-slice
+  const uint64_t kp = round_up8(K), np = round_up8(N);
+  if (kp * 256 * 2 >= (1ull << 31) || np * 64 * 2 >= (1ull << 31))
+    return set_error(XPU_ERR_INVALID, "xpu_gemm: K must be below 4M and N below 16M");
+  // A and B rows must be 16-byte aligned: otherwise the operand is copied,
+  // zero-padded to a multiple of 8 columns, into the runtime's workspace
+  const bool a_direct = reinterpret_cast<uintptr_t>(A) % 16 == 0 && K % 8 == 0;
+  const bool b_direct = reinterpret_cast<uintptr_t>(B) % 16 == 0 && N % 8 == 0;
+  const uint64_t a_bytes = a_direct ? 0 : (static_cast<uint64_t>(M) * kp * 2 + 255) & ~uint64_t{255};
+  const uint64_t b_bytes = b_direct ? 0 : static_cast<uint64_t>(K) * np * 2;
+  const void *a_use = A, *b_use = B;
+  if (a_bytes + b_bytes) {
+    void *ws = nullptr;
+    int rc = rt->scratch(a_bytes + b_bytes, &ws);
+    if (rc) return rc;
+    if (!a_direct) {
+      if ((rc = pad_rows(rt, A, K, M, K, ws, static_cast<uint32_t>(kp)))) return rc;
+      a_use = ws;
+    }
+    if (!b_direct) {
+      void *bp = static_cast<char *>(ws) + a_bytes;
+      if ((rc = pad_rows(rt, B, N, K, N, bp, static_cast<uint32_t>(np)))) return rc;
+      b_use = bp;
+    }
+  }
+  const uint32_t k_run = static_cast<uint32_t>(a_direct ? K : kp);  // reduction length seen by the kernel
+  const uint32_t n_run = static_cast<uint32_t>(b_direct ? N : np);  // columns of the B operand
+  const bool c16 = reinterpret_cast<uintptr_t>(C) % 16 == 0 && N % 8 == 0;
+  const std::string name = std::string("xpu_gemm_") + (dtype ? "fp16" : "bf16") + (c16 ? "_vec" : "_vecu");
   const xpu::KernelInfo *k = rt->find_exact(name);
   if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: " + name);
-  const uint64_t tiles = ((static_cast<uint64_t>(M) + 255) / 256) * ((static_cast<uint64_t>(N) + 255) / 256);
+  const uint64_t tiles = ((static_cast<uint64_t>(M) + 255) / 256) * ((static_cast<uint64_t>(n_run) + 255) / 256);
   if (tiles > 0x7fffffffu) return set_error(XPU_ERR_INVALID, "xpu_gemm: too many tiles");
-  const xpu_kernel_arg args[] = {{8, &A}, {8, &B}, {8, &C}, {4, &M}, {4, &N}, {4, &K}};
-  return rt->launch(*k, static_cast<uint32_t>(tiles), 1, 256, 0, args, 6);
+  const uint32_t kb = K, ldc = N, n_out = N;
+  const xpu_kernel_arg args[] = {{8, &a_use}, {8, &b_use}, {8, &C},   {4, &M},     {4, &n_run},
+                                 {4, &k_run}, {4, &kb},    {4, &ldc}, {4, &n_out}};
+  return rt->launch(*k, static_cast<uint32_t>(tiles), 1, 256, 0, args, 9);
 }
 
 namespace {

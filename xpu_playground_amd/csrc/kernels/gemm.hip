@@ -4,19 +4,20 @@
 //
 // Block tile 256 x 256 x 64 with 256 threads: four wavefronts in a 2 x 2
 // arrangement, each owning 128 x 128 of C as 4 x 4 tiles of
-// v_mfma_f32_32x32x16_{bf16,f16} (256 FP32 accumulators per lane).
-// A and B tiles are staged through LDS, double buffered: while the MFMAs
-// consume one buffer the next K-slice is in flight from global memory and is
-// written to the other buffer afterwards (one barrier per K-slice). A is
-// stored row-major [m][k]; B is transposed in registers (8 x 8 blocks of
-// 16-bit values via v_perm_b32) and stored [n][k], so both MFMA operands
-// are single 16-byte LDS reads. Rows are padded by 8 elements so the 32 rows
-// read by one ds_read_b128 fall in distinct banks.
+// v_mfma_f32_32x32x16_{bf16,f16} (256 FP32 accumulators per lane, in AGPRs).
+// A and B K-slices are loaded with buffer instructions into registers two
+// slices ahead and stored to LDS, double buffered, one barrier per slice. A
+// is stored row-major [m][k]; B is transposed in registers (8 x 8 blocks of
+// 16-bit values via v_perm_b32) and stored [n][k], so both MFMA operands are
+// single 16-byte LDS reads. Rows are padded by 8 elements so the 32 rows read
+// by one ds_read_b128 fall in distinct banks.
 //
-// Any M, N, K >= 1: out-of-range rows, columns and K are zero-filled on load
-// and masked on store (the reference pads on the host instead, gemm.cpp:75-85).
-// The _vec variants need A, B 16-byte aligned and K, N multiples of 8; the
-// _any variants load 16-bit elements.
+// The kernels need A and B rows 16-byte aligned (K and N multiples of 8);
+// the host pads other shapes into a workspace first (xpu_pad_rows below, the
+// device counterpart of the reference's host padding, gemm.cpp:75-85). Rows
+// past M, columns past N and the K tail are handled in the kernel: loads
+// past the end of A or B read zero through the buffer range check, stores
+// are masked.
 //
 // Tile order: blocks are dealt round-robin to the 8 XCDs, so when the tile
 // count is a multiple of 8 block b is renumbered to a contiguous range per
@@ -46,21 +47,6 @@ XPU_DEVICE f32x16 mfma(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// 8 consecutive elements of a row starting at column col (< cols), zero
-// beyond cols; VEC loads them as one 16-byte access.
-template <bool VEC>
-XPU_DEVICE u32x4 load8(const uint16_t *__restrict__ row, uint32_t col, uint32_t cols, bool row_ok) {
-  if (!row_ok || col >= cols) return u32x4{0, 0, 0, 0};
-  if constexpr (VEC) {
-    return *reinterpret_cast<const u32x4 *>(row + col);
-  } else {
-    uint32_t w[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) w[e] = (col + e < cols) ? row[col + e] : 0u;
-    return u32x4{w[0] | (w[1] << 16), w[2] | (w[3] << 16), w[4] | (w[5] << 16), w[6] | (w[7] << 16)};
-  }
-}
-
 struct TileCoord {
   uint32_t tm, tn;
 };
@@ -78,108 +64,7 @@ XPU_DEVICE TileCoord tile_of_block(uint32_t b, uint32_t tiles_m, uint32_t tiles_
   return {first_m + in_group % rows, in_group / rows};
 }
 
-template <int DT, bool VEC>
-XPU_DEVICE void gemm_body(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-                          uint16_t *__restrict__ C, uint32_t M, uint32_t N, uint32_t K) {
-  __shared__ __align__(16) uint16_t lds[2][2][kTileElems];  // [buffer][A | Bt][...]
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
-  const TileCoord tc = tile_of_block(blockIdx.x, tiles_m, tiles_n);
-  const uint32_t m0 = tc.tm * kBM, n0 = tc.tn * kBN;
-
-  // global -> register assignment
-  // A: thread loads chunk (tid % 8) of rows tid/8 + 32 i, i = 0..7
-  const uint32_t a_chunk = tid & 7u, a_row = tid >> 3;
-  // B: thread loads an 8 x 8 block: k rows kb*8..+7, n columns nb*8..+7
-  const uint32_t b_nb = tid & 31u, b_kb = tid >> 5;
-
-  u32x4 ra[8], rb[8];
-  auto load_tiles = [&](uint32_t k0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t row = m0 + a_row + 32u * i;
-      ra[i] = load8<VEC>(A + static_cast<uint64_t>(min(row, M - 1)) * K, k0 + a_chunk * 8u, K, row < M);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t k = k0 + b_kb * 8u + i;
-      rb[i] = load8<VEC>(B + static_cast<uint64_t>(min(k, K - 1)) * N, n0 + b_nb * 8u, N, k < K);
-    }
-  };
-  auto store_tiles = [&](uint32_t buf) {
-    uint16_t *la = lds[buf][0];
-    uint16_t *lb = lds[buf][1];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<u32x4 *>(la + (a_row + 32u * i) * kLdsPitch + a_chunk * 8u) = ra[i];
-    // transpose the 8 x 8 block: column j of rb -> row n = nb*8 + j of Bt
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-      uint32_t w[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t lo = rb[2 * q][j >> 1], hi = rb[2 * q + 1][j >> 1];
-        w[q] = __builtin_amdgcn_perm(hi, lo, sel);
-      }
-      *reinterpret_cast<u32x4 *>(lb + (b_nb * 8u + j) * kLdsPitch + b_kb * 8u) = u32x4{w[0], w[1], w[2], w[3]};
-    }
-  };
-
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-  const uint32_t wm = wave >> 1, wn = wave & 1u;
-  const uint32_t frag_row = lane & 31u, frag_k = (lane >> 5) * 8u;
-  const uint32_t nk = (K + kBK - 1) / kBK;
-
-  load_tiles(0);
-  store_tiles(0);
-  __syncthreads();
-  for (uint32_t it = 0; it < nk; ++it) {
-    const uint32_t buf = it & 1u;
-    if (it + 1 < nk) load_tiles((it + 1) * kBK);
-    const uint16_t *la = lds[buf][0] + (wm * 128u + frag_row) * kLdsPitch + frag_k;
-    const uint16_t *lb = lds[buf][1] + (wn * 128u + frag_row) * kLdsPitch + frag_k;
-#pragma unroll
-    for (uint32_t kk = 0; kk < kBK; kk += 16u) {
-      u32x4 fa[4], fb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) fa[i] = *reinterpret_cast<const u32x4 *>(la + i * 32u * kLdsPitch + kk);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) fb[j] = *reinterpret_cast<const u32x4 *>(lb + j * 32u * kLdsPitch + kk);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma<DT>(fa[i], fb[j], acc[i][j]);
-    }
-    if (it + 1 < nk) store_tiles(buf ^ 1u);
-    __syncthreads();
-  }
-
-  // D layout of v_mfma_f32_32x32x16: lane l holds column l % 32 and rows
-  // 8 (v / 4) + 4 (l / 32) + v % 4 for v = 0..15
-  const uint32_t col_in = lane & 31u, row_in = (lane >> 5) * 4u;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t col = n0 + wn * 128u + j * 32u + col_in;
-      if (col >= N) continue;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const uint32_t row = m0 + wm * 128u + i * 32u + (v / 4) * 8u + row_in + (v % 4);
-        if (row < M) C[static_cast<uint64_t>(row) * N + col] = static_cast<uint16_t>(encode<DT>(acc[i][j][v]));
-      }
-    }
-}
-
-// ------------------------------------------------------------------ vec path
+// ------------------------------------------------------------------ main path
 //
 // Rows of A and B 16-byte aligned (K, N multiples of 8): every 8-element
 // chunk is wholly inside or wholly outside the matrix. Loads go through
@@ -223,7 +108,7 @@ XPU_DEVICE u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
 
 struct Ctx {
   const uint16_t *A, *B;
-  uint32_t M, N, K, m0, n0;
+  uint32_t M, N, K, kb, m0, n0;
   uint32_t a_off;     // byte offset of this thread's first A chunk within a slice
   uint32_t b_off;     // byte offset of this thread's first B chunk (kOob + ... past N)
   uint32_t a_stride;  // bytes between the A chunks of one thread (32 rows)
@@ -239,7 +124,7 @@ XPU_DEVICE void issue(const Ctx &c, uint32_t s, u32x4 (&ra)[8], u32x4 (&rb)[8]) 
       rsrc(c.A + static_cast<uint64_t>(c.m0) * c.K + k0,
            (static_cast<int64_t>(c.M - c.m0) * c.K - static_cast<int64_t>(k0)) * 2);
   const __amdgpu_buffer_rsrc_t r_b =
-      rsrc(c.B + k0 * c.N + c.n0, (static_cast<int64_t>(c.K) - static_cast<int64_t>(k0)) * c.N * 2 -
+      rsrc(c.B + k0 * c.N + c.n0, (static_cast<int64_t>(c.kb) - static_cast<int64_t>(k0)) * c.N * 2 -
                                       static_cast<int64_t>(c.n0) * 2);
   const uint32_t a_base = k0 + c.a_col < c.K ? c.a_off : kOob;
 #pragma unroll
@@ -343,9 +228,12 @@ XPU_DEVICE void schedule_step() {
   __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
 }
 
-template <int DT>
+// K: reduction length (columns of A); kb: rows of B (<= K; rows kb..K-1
+// read as zero); N: columns of B; C has row stride ldc and n_out <= N valid
+// columns. C16: C rows 16-byte aligned and n_out % 8 == 0 (16-byte stores).
+template <int DT, bool C16>
 XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
-                     uint32_t M, uint32_t N, uint32_t K) {
+                     uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {
   __shared__ __align__(16) uint16_t lds[2][2][kTileElems];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
@@ -356,6 +244,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   c.M = M;
   c.N = N;
   c.K = K;
+  c.kb = kb;
   c.m0 = tc.tm * kBM;
   c.n0 = tc.tn * kBN;
   {
@@ -436,10 +325,18 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
       const f32x4 lo = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane);
       const f32x4 hi = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane + 4u);
       const uint32_t m = c.m0 + wm * 128u + i * 32u + r, n = c.n0 + wn * 128u + c_lane;
-      if (m < M && n < N)  // N % 8 == 0: n < N implies n + 7 < N
-        *reinterpret_cast<u32x4 *>(C + static_cast<uint64_t>(m) * N + n) =
-            u32x4{cvt_pack<DT>(lo.x, lo.y), cvt_pack<DT>(lo.z, lo.w), cvt_pack<DT>(hi.x, hi.y),
-                  cvt_pack<DT>(hi.z, hi.w)};
+      if (m >= M || n >= n_out) continue;
+      const u32x4 packed{cvt_pack<DT>(lo.x, lo.y), cvt_pack<DT>(lo.z, lo.w), cvt_pack<DT>(hi.x, hi.y),
+                         cvt_pack<DT>(hi.z, hi.w)};
+      uint16_t *dst = C + static_cast<uint64_t>(m) * ldc + n;
+      if constexpr (C16) {
+        *reinterpret_cast<u32x4 *>(dst) = packed;  // n_out % 8 == 0: n + 7 < n_out
+      } else {
+        const uint32_t w[4] = {packed.x, packed.y, packed.z, packed.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < n_out) dst[e] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+      }
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -451,21 +348,39 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 
 }  // namespace xpu
 
-#define XPU_GEMM_VARIANT(NAME, DT, VEC)                                                        \
+#define XPU_GEMM_VEC_VARIANT(NAME, DT, C16)                                                    \
   extern "C" __global__ __launch_bounds__(256, 1) void NAME(                                  \
       const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C, \
-      uint32_t M, uint32_t N, uint32_t K) {                                                    \
-    xpu::gemm_body<DT, VEC>(A, B, C, M, N, K);                                                 \
+      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {         \
+    xpu::vec::body<DT, C16>(A, B, C, M, N, K, kb, ldc, n_out);                                 \
   }
 
-#define XPU_GEMM_VEC_VARIANT(NAME, DT)                                                         \
-  extern "C" __global__ __launch_bounds__(256, 1) void NAME(                                  \
-      const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C, \
-      uint32_t M, uint32_t N, uint32_t K) {                                                    \
-    xpu::vec::body<DT>(A, B, C, M, N, K);                                                      \
-  }
+XPU_GEMM_VEC_VARIANT(xpu_gemm_bf16_vec, xpu::kBf16, true)
+XPU_GEMM_VEC_VARIANT(xpu_gemm_fp16_vec, xpu::kFp16, true)
+XPU_GEMM_VEC_VARIANT(xpu_gemm_bf16_vecu, xpu::kBf16, false)
+XPU_GEMM_VEC_VARIANT(xpu_gemm_fp16_vecu, xpu::kFp16, false)
 
-XPU_GEMM_VEC_VARIANT(xpu_gemm_bf16_vec, xpu::kBf16)
-XPU_GEMM_VEC_VARIANT(xpu_gemm_fp16_vec, xpu::kFp16)
-XPU_GEMM_VARIANT(xpu_gemm_bf16_any, xpu::kBf16, false)
-XPU_GEMM_VARIANT(xpu_gemm_fp16_any, xpu::kFp16, false)
+// dst[r][c] = src[r * src_ld + c] for c < cols, 0 for cols <= c < dst_cols
+// (dst_cols % 8 == 0, dst 16-byte aligned): the zero padding of the
+// reference's host GEMM setup (gemm.cpp:75-85) done on the device, so rows
+// of the copy are 16-byte aligned. One thread per 8 destination elements.
+extern "C" __global__ __launch_bounds__(256) void xpu_pad_rows(const uint16_t *__restrict__ src, uint64_t src_ld,
+                                                               uint32_t rows, uint32_t cols,
+                                                               uint16_t *__restrict__ dst, uint32_t dst_cols) {
+  const uint64_t chunks_per_row = dst_cols / 8u;
+  const uint64_t total = static_cast<uint64_t>(rows) * chunks_per_row;
+  for (uint64_t idx = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+    const uint64_t r = idx / chunks_per_row;
+    const uint32_t c0 = static_cast<uint32_t>(idx % chunks_per_row) * 8u;
+    const uint16_t *row = src + r * src_ld;
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = c0 + 2 * q < cols ? row[c0 + 2 * q] : 0u;
+      const uint32_t hi = c0 + 2 * q + 1 < cols ? row[c0 + 2 * q + 1] : 0u;
+      w[q] = lo | (hi << 16);
+    }
+    *reinterpret_cast<xpu::u32x4 *>(dst + r * dst_cols + c0) = xpu::u32x4{w[0], w[1], w[2], w[3]};
+  }
+}

@@ -4,3 +4,4 @@
 #include "synth.hip"
 #include "qwen3_ops.hip"
 #include "gemm.hip"
+#include "peak.hip"

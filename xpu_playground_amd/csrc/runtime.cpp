@@ -99,6 +99,7 @@ xpu_runtime::~xpu_runtime() {
   if (device >= 0) (void)hipSetDevice(device);
   if (stream) (void)hipStreamSynchronize(stream);
   for (auto &entry : allocations) (void)hipFree(entry.second);
+  if (workspace) (void)hipFree(workspace);
   if (module) (void)hipModuleUnload(module);
   if (stream) (void)hipStreamDestroy(stream);
 }
@@ -107,6 +108,23 @@ const xpu::KernelInfo *xpu_runtime::find_exact(const std::string &name) const {
   for (const auto &k : kernels)
     if (k.name == name) return &k;
   return nullptr;
+}
+
+int xpu_runtime::scratch(uint64_t bytes, void **out) {
+  if (bytes > workspace_bytes) {
+    XPU_HIP_RETURN(hipSetDevice(device));
+    if (workspace) {
+      // earlier launches on the stream may still read the old block
+      XPU_HIP_RETURN(hipStreamSynchronize(stream));
+      XPU_HIP_RETURN(hipFree(workspace));
+      workspace = nullptr;
+      workspace_bytes = 0;
+    }
+    XPU_HIP_RETURN(hipMalloc(&workspace, bytes));
+    workspace_bytes = bytes;
+  }
+  *out = workspace;
+  return XPU_OK;
 }
 
 int xpu_runtime::launch(const xpu::KernelInfo &k, uint32_t gx, uint32_t gy, uint32_t bx,

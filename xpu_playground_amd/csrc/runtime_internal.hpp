@@ -55,6 +55,9 @@ struct xpu_runtime {
   hipModule_t module = nullptr;
   std::vector<xpu::KernelInfo> kernels;
   std::map<void *, void *> allocations;
+  // grow-only scratch for entry points that stage data (GEMM padding)
+  void *workspace = nullptr;
+  uint64_t workspace_bytes = 0;
 
   xpu_runtime() = default;
   xpu_runtime(const xpu_runtime &) = delete;
@@ -63,6 +66,8 @@ struct xpu_runtime {
   const xpu::KernelInfo *find_exact(const std::string &name) const;
   int launch(const xpu::KernelInfo &k, uint32_t gx, uint32_t gy, uint32_t bx, uint32_t shared,
              const xpu_kernel_arg *args, uint32_t nargs);
+  // at least `bytes` of device scratch, 256-byte aligned; contents undefined
+  int scratch(uint64_t bytes, void **out);
 };
 
 #define XPU_HIP_RETURN(expr)                                                                 \
