@@ -171,10 +171,7 @@ XPU_DEVICE float block_max(float v, float *red) {
 // bf16(bf16(lane-local 8-slot dot) * scale) (transformers eager: bf16 matmul
 // then bf16 * scaling). The 16 row loads are independent and issued
 // together.
-XPU_DEVICE float attention_score(const uint16_t *qs, const uint16_t *krow, float scale) {
-  u32x4 kv[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) kv[j] = *reinterpret_cast<const u32x4 *>(krow + j * 8);
+XPU_DEVICE float attention_score_regs(const uint16_t *qs, const u32x4 (&kv)[16], float scale) {
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
@@ -185,6 +182,17 @@ XPU_DEVICE float attention_score(const uint16_t *qs, const uint16_t *krow, float
     for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(q[e], k[e], acc[e]);
   }
   return round_bf16(round_bf16(fold8(acc)) * scale);
+}
+
+XPU_DEVICE void load_head_row(const uint16_t *row, u32x4 (&r)[16]) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) r[j] = *reinterpret_cast<const u32x4 *>(row + j * 8);
+}
+
+XPU_DEVICE float attention_score(const uint16_t *qs, const uint16_t *krow, float scale) {
+  u32x4 kv[16];
+  load_head_row(krow, kv);
+  return attention_score_regs(qs, kv, scale);
 }
 
 constexpr uint32_t kAttnTile = 256;             // positions per V tile in LDS
@@ -198,6 +206,12 @@ constexpr uint32_t kVPitch = kHeadDim + 8;      // LDS row pitch of the V tile (
 // sbuf: kAttnChunk floats of LDS; vtile: kAttnTile * kVPitch codes of LDS;
 // red: >= 4*128 floats of LDS. Position t is handled by thread t % 256 in
 // the score pass; V rows go through vtile so that the P.V pass reads LDS.
+template <bool HAS_CURRENT>
+XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const uint16_t *vbase,
+                               uint64_t stride, uint32_t n, const uint16_t *kcur,
+                               const uint16_t *vcur, float scale, uint16_t *out, float *sbuf,
+                               uint16_t *vtile, float *red, float local_max);
+
 template <bool HAS_CURRENT>
 XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const uint16_t *vbase,
                                uint64_t stride, uint32_t n, const uint16_t *kcur,
@@ -233,6 +247,34 @@ XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const 
       local_max = fmaxf(local_max, s);
     }
   }
+  attention_tail<HAS_CURRENT>(qs, kbase, vbase, stride, n, kcur, vcur, scale, out, sbuf, vtile, red, local_max);
+}
+
+// Passes 2 and 3 of attention_head, after the scores (sbuf, when one chunk
+// holds them), the V rows (vtile, when one tile holds them) and each
+// thread's running max are in place.
+template <bool HAS_CURRENT>
+XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const uint16_t *vbase,
+                               uint64_t stride, uint32_t n, const uint16_t *kcur,
+                               const uint16_t *vcur, float scale, uint16_t *out, float *sbuf,
+                               uint16_t *vtile, float *red, float local_max) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t nchunks = (n + kAttnChunk - 1) / kAttnChunk;
+  const bool single_tile = n <= kAttnTile;
+  auto krow_of = [&](uint32_t t) -> const uint16_t * {
+    return (HAS_CURRENT && t + 1 == n) ? kcur : kbase + static_cast<uint64_t>(t) * stride;
+  };
+  auto vrow_of = [&](uint32_t t) -> const uint16_t * {
+    return (HAS_CURRENT && t + 1 == n) ? vcur : vbase + static_cast<uint64_t>(t) * stride;
+  };
+  auto stage_v_row = [&](uint32_t t, uint32_t slot) {
+    const uint16_t *src = vrow_of(t);
+    u32x4 vv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) vv[j] = *reinterpret_cast<const u32x4 *>(src + j * 8);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) *reinterpret_cast<u32x4 *>(vtile + slot * kVPitch + j * 8) = vv[j];
+  };
   const float mx = block_max(local_max, red);
   // pass 2: exponentials and the chunked canonical sum
   float total = 0.0f;

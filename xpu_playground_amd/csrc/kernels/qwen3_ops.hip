@@ -362,18 +362,47 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   const uint16_t *qsrc = qkv + head * xpu::kHeadDim;
   const uint16_t *ksrc = qkv + (heads + kv) * xpu::kHeadDim;
   const uint16_t *vsrc = qkv + (heads + kv_heads + kv) * xpu::kHeadDim;
-  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t wave = threadIdx.x >> 6, tid = threadIdx.x;
+  const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
+  const uint32_t n = pos + 1;
+  // Up to kAttnTile positions, thread t owns position t: its cached K and V
+  // rows (t < pos; written by earlier steps) are loaded before the QK-norm /
+  // RoPE prologue so their latency overlaps it.
+  const bool short_ctx = n <= xpu::kAttnTile;
+  u32x4 krow[16], vrow[16];
+  if (short_ctx && tid < pos) {
+    xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(tid) * xpu::kHeadDim, krow);
+    xpu::load_head_row(vcache + head_base + static_cast<uint64_t>(tid) * xpu::kHeadDim, vrow);
+  }
   if (wave == 0) xpu::head_norm_rope(qsrc, qnorm_w, cos_row, sin_row, eps, nullptr, qs);
   else if (wave == 1) xpu::head_norm_rope(ksrc, knorm_w, cos_row, sin_row, eps, nullptr, ks);
   __syncthreads();
-  const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
-  if (head % group == 0 && threadIdx.x < xpu::kHeadDim) {
-    const uint64_t slot = head_base + static_cast<uint64_t>(pos) * xpu::kHeadDim + threadIdx.x;
-    kcache[slot] = ks[threadIdx.x];
-    vcache[slot] = vsrc[threadIdx.x];
+  if (head % group == 0 && tid < xpu::kHeadDim) {
+    const uint64_t slot = head_base + static_cast<uint64_t>(pos) * xpu::kHeadDim + tid;
+    kcache[slot] = ks[tid];
+    vcache[slot] = vsrc[tid];
   }
-  xpu::attention_head<true>(qs, kcache + head_base, vcache + head_base, xpu::kHeadDim, pos + 1, ks,
-                            vsrc, scale, out + head * xpu::kHeadDim, sbuf, vtile, red);
+  if (!short_ctx) {
+    xpu::attention_head<true>(qs, kcache + head_base, vcache + head_base, xpu::kHeadDim, n, ks, vsrc,
+                              scale, out + head * xpu::kHeadDim, sbuf, vtile, red);
+    return;
+  }
+  // pass 1 of attention_head for one tile, from the preloaded rows (the
+  // current position from ks / vsrc)
+  float local_max = -__builtin_inff();
+  if (tid < n) {
+    if (tid == pos) {
+      xpu::load_head_row(ks, krow);
+      xpu::load_head_row(vsrc, vrow);
+    }
+    const float sc = xpu::attention_score_regs(qs, krow, scale);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) *reinterpret_cast<u32x4 *>(vtile + tid * xpu::kVPitch + j * 8) = vrow[j];
+    sbuf[tid] = sc;
+    local_max = sc;
+  }
+  xpu::attention_tail<true>(qs, kcache + head_base, vcache + head_base, xpu::kHeadDim, n, ks, vsrc, scale,
+                            out + head * xpu::kHeadDim, sbuf, vtile, red, local_max);
 }
 
 // Reduce the per-block argmax partials; token = 0xffffffff if any logit was
