@@ -154,6 +154,49 @@ XPU_DEVICE void head_norm_rope(const uint16_t *src, const uint16_t *__restrict__
   }
 }
 
+// head_norm_rope with the lane's operands already loaded (lanes 0..15:
+// elements 8 l..8 l + 7 of the head row, the norm weight, cos and sin rows;
+// other lanes ignored), so the caller can issue those loads early. Same
+// operations in the same order; writes the roped row only.
+XPU_DEVICE void head_norm_rope_vec(const u32x4 &xv, const u32x4 &wv, const u32x4 &cv, const u32x4 &sv,
+                                   float eps, uint16_t *roped_out) {
+  const uint32_t lane = lane_id();
+  const bool active = lane < 16;
+  float x[8], wf[8];
+  unpack8<kBf16>(xv, x);
+  unpack8<kBf16>(wv, wf);
+  if (!active) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+  }
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(x[e], x[e], 0.0f);
+  const float ss = wave_butterfly(fold8(acc));
+  const float scale = 1.0f / __builtin_sqrtf(ss / static_cast<float>(kHeadDim) + eps);
+  float n[8], p[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) n[e] = active ? round_bf16(wf[e] * round_bf16(x[e] * scale)) : 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(n[e], 8, 64);
+  if (active) {
+    float cf[8], sf[8];
+    unpack8<kBf16>(cv, cf);
+    unpack8<kBf16>(sv, sf);
+    uint32_t codes[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float rot = lane < 8 ? -p[e] : p[e];
+      const float a = round_bf16(n[e] * cf[e]);
+      const float b = round_bf16(rot * sf[e]);
+      codes[e] = f32_to_bf16(a + b);
+    }
+    *reinterpret_cast<u32x4 *>(roped_out + lane * 8u) =
+        u32x4{codes[0] | (codes[1] << 16), codes[2] | (codes[3] << 16), codes[4] | (codes[5] << 16),
+              codes[6] | (codes[7] << 16)};
+  }
+}
+
 XPU_DEVICE float block_max(float v, float *red) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
@@ -358,6 +401,64 @@ XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const 
     out[tid] = static_cast<uint16_t>(f32_to_bf16(r));
   }
   __syncthreads();
+}
+
+// Passes 2 and 3 of attention_head for n <= kAttnTile positions (one
+// softmax chunk), from the scores in sbuf[0..n) and each thread's running
+// max. The V operands come preloaded in the P.V layout: lane l of wave w
+// owns residue class c = 4 w + l / 16 and dims 8 (l % 16) .. + 7, and
+// vpv[it] holds V[t][those dims] for t = 16 it + c. Same operations in the
+// same order as attention_tail (each class is one ascending FMA chain per
+// dim; classes combine as ((c0 + c1) + (c2 + c3)) within a wave, then
+// across waves).
+XPU_DEVICE void attention_tail_short(uint32_t n, uint16_t *out, float *sbuf, float *red, float local_max,
+                                     const u32x4 (&vpv)[kAttnTile / 16]) {
+  const uint32_t tid = threadIdx.x;
+  const float mx = block_max(local_max, red);
+  if (tid < n) sbuf[tid] = canonical_exp(sbuf[tid] - mx);
+  __syncthreads();
+  if (tid < 64) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t k = tid * 8u + e;
+      if (k < n) acc[e] = acc[e] + sbuf[k];
+    }
+    const float total = 0.0f + wave_butterfly(fold8(acc));
+    if (tid == 0) red[0] = 1.0f / total;
+  }
+  __syncthreads();
+  const float inv = red[0];
+  const uint32_t wave = tid >> 6, lane = lane_id(), cls = wave * 4u + (lane >> 4);
+  float part[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int it = 0; it < static_cast<int>(kAttnTile / 16); ++it) {
+    const uint32_t t = it * 16u + cls;
+    if (t < n) {
+      const float pt = round_bf16(sbuf[t] * inv);
+      float v[8];
+      unpack8<kBf16>(vpv[it], v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[e] = __builtin_fmaf(pt, v[e], part[e]);
+    }
+  }
+  float sum[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float tot = 0.0f + part[e];
+    const float pair = tot + __shfl_xor(tot, 16, 64);   // (c0 + c1), (c2 + c3)
+    sum[e] = pair + __shfl_xor(pair, 32, 64);           // (c0 + c1) + (c2 + c3)
+  }
+  __syncthreads();  // everyone has read red[0]
+  if (lane < 16) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[wave * kHeadDim + lane * 8u + e] = sum[e];
+  }
+  __syncthreads();
+  if (tid < kHeadDim) {
+    const float r = (red[tid] + red[kHeadDim + tid]) + (red[2 * kHeadDim + tid] + red[3 * kHeadDim + tid]);
+    out[tid] = static_cast<uint16_t>(f32_to_bf16(r));
+  }
 }
 
 // (value, index) argmax step with the reference's tie rule (strict >, so the

@@ -369,13 +369,33 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   // rows (t < pos; written by earlier steps) are loaded before the QK-norm /
   // RoPE prologue so their latency overlaps it.
   const bool short_ctx = n <= xpu::kAttnTile;
-  u32x4 krow[16], vrow[16];
-  if (short_ctx && tid < pos) {
-    xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(tid) * xpu::kHeadDim, krow);
-    xpu::load_head_row(vcache + head_base + static_cast<uint64_t>(tid) * xpu::kHeadDim, vrow);
+  // QK-norm / RoPE operands of waves 0 (q) and 1 (k), lanes 0..15
+  const uint32_t lane = xpu::lane_id();
+  u32x4 hx = {0, 0, 0, 0}, hw = {0, 0, 0, 0}, hc = {0, 0, 0, 0}, hs = {0, 0, 0, 0};
+  if (wave < 2 && lane < 16) {
+    hx = *reinterpret_cast<const u32x4 *>((wave == 0 ? qsrc : ksrc) + lane * 8u);
+    hw = *reinterpret_cast<const u32x4 *>((wave == 0 ? qnorm_w : knorm_w) + lane * 8u);
+    hc = *reinterpret_cast<const u32x4 *>(cos_row + lane * 8u);
+    hs = *reinterpret_cast<const u32x4 *>(sin_row + lane * 8u);
   }
-  if (wave == 0) xpu::head_norm_rope(qsrc, qnorm_w, cos_row, sin_row, eps, nullptr, qs);
-  else if (wave == 1) xpu::head_norm_rope(ksrc, knorm_w, cos_row, sin_row, eps, nullptr, ks);
+  // K rows for the scores (thread t, position t) and V pieces in the P.V
+  // layout of attention_tail_short (the current position's v from qkv)
+  u32x4 krow[16], vpv[xpu::kAttnTile / 16];
+  if (short_ctx) {
+    if (tid < pos) xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(tid) * xpu::kHeadDim, krow);
+    const uint32_t cls = wave * 4u + (lane >> 4), dim0 = (lane & 15u) * 8u;
+#pragma unroll
+    for (int it = 0; it < static_cast<int>(xpu::kAttnTile / 16); ++it) {
+      const uint32_t t = it * 16u + cls;
+      if (t < pos)
+        vpv[it] = *reinterpret_cast<const u32x4 *>(vcache + head_base + static_cast<uint64_t>(t) * xpu::kHeadDim + dim0);
+      else if (t == pos)
+        vpv[it] = *reinterpret_cast<const u32x4 *>(vsrc + dim0);
+      else
+        vpv[it] = u32x4{0, 0, 0, 0};
+    }
+  }
+  if (wave < 2) xpu::head_norm_rope_vec(hx, hw, hc, hs, eps, wave == 0 ? qs : ks);
   __syncthreads();
   if (head % group == 0 && tid < xpu::kHeadDim) {
     const uint64_t slot = head_base + static_cast<uint64_t>(pos) * xpu::kHeadDim + tid;
@@ -387,22 +407,16 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
                               scale, out + head * xpu::kHeadDim, sbuf, vtile, red);
     return;
   }
-  // pass 1 of attention_head for one tile, from the preloaded rows (the
-  // current position from ks / vsrc)
+  // pass 1 of attention_head for one tile, from the preloaded K rows (the
+  // current position from ks)
   float local_max = -__builtin_inff();
   if (tid < n) {
-    if (tid == pos) {
-      xpu::load_head_row(ks, krow);
-      xpu::load_head_row(vsrc, vrow);
-    }
+    if (tid == pos) xpu::load_head_row(ks, krow);
     const float sc = xpu::attention_score_regs(qs, krow, scale);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) *reinterpret_cast<u32x4 *>(vtile + tid * xpu::kVPitch + j * 8) = vrow[j];
     sbuf[tid] = sc;
     local_max = sc;
   }
-  xpu::attention_tail<true>(qs, kcache + head_base, vcache + head_base, xpu::kHeadDim, n, ks, vsrc, scale,
-                            out + head * xpu::kHeadDim, sbuf, vtile, red, local_max);
+  xpu::attention_tail_short(n, out + head * xpu::kHeadDim, sbuf, red, local_max, vpv);
 }
 
 // Reduce the per-block argmax partials; token = 0xffffffff if any logit was
