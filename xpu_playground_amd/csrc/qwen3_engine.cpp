@@ -161,7 +161,7 @@ int allocate_buffers(xpu_qwen3 &e) {
   const uint64_t qd = uint64_t{c.heads} * c.head_dim, kvd = uint64_t{c.kv_heads} * c.head_dim;
   const uint64_t cache = uint64_t{c.layers} * c.kv_heads * e.max_seq * c.head_dim * 2;
   const uint64_t rope = uint64_t{e.max_seq} * c.head_dim * 2;
-  e.nparts = e.rt->compute_units * 4;
+  e.nparts = e.rt->compute_units * 8;
   std::vector<std::pair<void **, uint64_t>> parts = {
       {reinterpret_cast<void **>(&e.x), c.hidden * 2ull},
       {reinterpret_cast<void **>(&e.qkv), (qd + 2 * kvd) * 2},
@@ -272,17 +272,24 @@ int setup_launches(xpu_qwen3 &e) {
   e.qkv_l.shared = kpad_bytes(c.hidden);
   if ((rc = find("xpu_q3_attention", e.attn_l))) return rc;
   e.attn_l.grid = c.heads;
-  if ((rc = find("xpu_q3_gemv_residual_r1", e.o_l))) return rc;
+  // residual GEMVs: the whole row in one batch of loads when K is 2048,
+  // 3072 or 4096 (U = K / 512)
+  auto residual_kernel = [](uint32_t K) {
+    return K == 2048 ? "xpu_q3_gemv_residual_r1u4"
+                     : K == 3072 ? "xpu_q3_gemv_residual_r1u6"
+                                 : K == 4096 ? "xpu_q3_gemv_residual_r1u8" : "xpu_q3_gemv_residual_r1";
+  };
+  if ((rc = find(residual_kernel(qd), e.o_l))) return rc;
   e.o_l.grid = std::min(cap, (c.hidden + 3) / 4);
   e.o_l.shared = kpad_bytes(qd);
   if ((rc = find("xpu_q3_norm_gemv_swiglu_r2", e.gu_l))) return rc;
   e.gu_l.grid = std::min(cap, (c.intermediate + 3) / 4);
   e.gu_l.shared = kpad_bytes(c.hidden);
-  if ((rc = find("xpu_q3_gemv_residual_r1", e.down_l))) return rc;
+  if ((rc = find(residual_kernel(c.intermediate), e.down_l))) return rc;
   e.down_l.grid = std::min(cap, (c.hidden + 3) / 4);
   e.down_l.shared = kpad_bytes(c.intermediate);
-  if ((rc = find("xpu_q3_norm_gemv_logits_r4", e.logits_l))) return rc;
-  e.logits_l.grid = std::min(std::min(cap, e.nparts), (c.vocab + 15) / 16);
+  if ((rc = find("xpu_q3_norm_gemv_logits_r2", e.logits_l))) return rc;
+  e.logits_l.grid = std::min(e.nparts, (c.vocab + 7) / 8);
   e.logits_l.shared = kpad_bytes(c.hidden);
   if ((rc = find("xpu_q3_argmax_finish", e.finish_l))) return rc;
   e.finish_l.grid = 1;
