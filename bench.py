@@ -76,6 +76,51 @@ def timed_gemm(rt, dtype, m, n, k, steps, warmup):
     return ms / steps
 
 
+def measured_peaks(rt):
+    """The device's measured ceilings: bf16 MFMA issue rate (8 independent
+    v_mfma_f32_32x32x16_bf16 chains per wavefront, 2 wavefronts per SIMD)
+    and streaming HBM read bandwidth (4 GiB surface)."""
+    import numpy as np
+    from xpu_playground_amd import Args  # noqa: F401
+
+    lib = rt.lib
+    blocks, rounds = rt.compute_units * 2, 4096
+    operand, sink, clock = rt.alloc(16), rt.alloc(blocks * 256 * 4), rt.alloc(32)
+    rt.copy_to(operand, np.full(8, 0x3F00, np.uint16))
+    for _ in range(3):
+        xpu_check(lib.xpu_peak_mfma(rt.handle, operand, sink, clock, blocks, rounds))
+    rt.synchronize()
+    start, stop = rt.event(), rt.event()
+    start.record()
+    for _ in range(10):
+        xpu_check(lib.xpu_peak_mfma(rt.handle, operand, sink, clock, blocks, rounds))
+    stop.record()
+    rt.synchronize()
+    flops = blocks * 4 * rounds * 8 * 32768.0
+    mfma_tflops = flops / (start.elapsed_ms(stop) / 10 * 1e-3) / 1e12
+    nbytes = 4 << 30
+    surface, rsink = rt.alloc(nbytes), rt.alloc(rt.compute_units * 8 * 1024)
+    rt.fill_uniform(0, surface, nbytes // 2, 7)
+    for _ in range(3):
+        xpu_check(lib.xpu_peak_read(rt.handle, surface, nbytes, rsink, rt.compute_units * 8))
+    rt.synchronize()
+    start.record()
+    for _ in range(10):
+        xpu_check(lib.xpu_peak_read(rt.handle, surface, nbytes, rsink, rt.compute_units * 8))
+    stop.record()
+    rt.synchronize()
+    read_gbs = nbytes / (start.elapsed_ms(stop) / 10 * 1e-3) / 1e9
+    for p in (operand, sink, clock, surface, rsink):
+        rt.free(p)
+    return {"mfma_bf16_tflops": round(mfma_tflops, 1), "hbm_read_gbs": round(read_gbs, 1)}
+
+
+def xpu_check(code):
+    import xpu_playground_amd as xpu
+
+    xpu.check(code)
+
+
 def qwen3_decode(xpu):
     """Qwen3-0.6B shape, random N(0, 0.02^2) bf16 weights, 128-token seeded
     prompt, 128 greedy steps; returns (decode tok/s, prompt tok/s)."""
@@ -220,8 +265,14 @@ def main() -> int:
                 "roofline_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
             log(f"GEMM {gms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
             gms2 = timed_gemm(rt, xpu.FP16, 3000, 4097, 2050, 10, 3)
+            tf2 = 2.0 * 3000 * 4097 * 2050 / (gms2 * 1e-3) / 1e12
             secondary["gemm_fp16_3000x4097x2050"] = {
-                "value": round(2.0 * 3000 * 4097 * 2050 / (gms2 * 1e-3) / 1e12, 1), "unit": "TFLOP/s"}
+                "value": round(tf2, 1), "unit": "TFLOP/s", "ms": round(gms2, 4),
+                "roofline_frac": round(tf2 / MFMA_BF16_PEAK_TFLOPS, 4)}
+            log(f"GEMM ragged {gms2 * 1e3:.1f} us, {tf2:.1f} TFLOP/s")
+        if hasattr(xpu.library(), "xpu_peak_mfma"):
+            secondary["measured_peaks"] = measured_peaks(rt)
+            log(f"peaks {secondary['measured_peaks']}")
     rt.close()
     if not args.no_secondary:
         log("Qwen3-0.6B decode: 128 prompt + 128 greedy steps")

@@ -132,6 +132,10 @@ def _declare(lib):
         "xpu_synth_tokens": (c_int, [c_void_p, c_uint64, c_uint64, c_uint32]),
         "run_gemv": (c_int, [c_int, POINTER(c_char_p)]),
         "run_gemm": (c_int, [c_int, POINTER(c_char_p)]),
+        "xpu_peak_mfma": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]),
+        "xpu_peak_read": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_uint32]),
+        "run_peak_compute": (c_int, [c_int, POINTER(c_char_p)]),
+        "run_peak_mem": (c_int, [c_int, POINTER(c_char_p)]),
         "run_qwen3": (c_int, [c_int, POINTER(c_char_p)]),
     }
     for name, (res, args) in sig.items():

@@ -364,6 +364,11 @@ XPU_GEMM_VEC_VARIANT(xpu_gemm_fp16_vecu, xpu::kFp16, false)
 // (dst_cols % 8 == 0, dst 16-byte aligned): the zero padding of the
 // reference's host GEMM setup (gemm.cpp:75-85) done on the device, so rows
 // of the copy are 16-byte aligned. One thread per 8 destination elements.
+// src only needs 2-byte alignment: a chunk that starts on a 4-byte boundary
+// is one 16-byte load; one that starts 2 bytes past it is the 16-byte load
+// one element earlier plus the chunk's last element, shifted into place.
+// The chunk holding the row's end is read element by element, so no load
+// reaches past the last element of a row.
 extern "C" __global__ __launch_bounds__(256) void xpu_pad_rows(const uint16_t *__restrict__ src, uint64_t src_ld,
                                                                uint32_t rows, uint32_t cols,
                                                                uint16_t *__restrict__ dst, uint32_t dst_cols) {
@@ -373,14 +378,27 @@ extern "C" __global__ __launch_bounds__(256) void xpu_pad_rows(const uint16_t *_
        idx += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
     const uint64_t r = idx / chunks_per_row;
     const uint32_t c0 = static_cast<uint32_t>(idx % chunks_per_row) * 8u;
-    const uint16_t *row = src + r * src_ld;
-    uint32_t w[4];
+    const uint16_t *p = src + r * src_ld + c0;
+    xpu::u32x4 v;
+    if (c0 + 8u <= cols) {
+      if ((reinterpret_cast<uintptr_t>(p) & 3u) == 0) {
+        v = *reinterpret_cast<const xpu::u32x4 *>(p);
+      } else {
+        const xpu::u32x4 d = *reinterpret_cast<const xpu::u32x4 *>(p - 1);  // elements -1..6
+        const uint32_t last = p[7];
+        v = xpu::u32x4{__builtin_amdgcn_alignbit(d.y, d.x, 16), __builtin_amdgcn_alignbit(d.z, d.y, 16),
+                       __builtin_amdgcn_alignbit(d.w, d.z, 16), __builtin_amdgcn_alignbit(last, d.w, 16)};
+      }
+    } else {
+      uint32_t w[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t lo = c0 + 2 * q < cols ? row[c0 + 2 * q] : 0u;
-      const uint32_t hi = c0 + 2 * q + 1 < cols ? row[c0 + 2 * q + 1] : 0u;
-      w[q] = lo | (hi << 16);
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t lo = c0 + 2 * q < cols ? p[2 * q] : 0u;
+        const uint32_t hi = c0 + 2 * q + 1 < cols ? p[2 * q + 1] : 0u;
+        w[q] = lo | (hi << 16);
+      }
+      v = xpu::u32x4{w[0], w[1], w[2], w[3]};
     }
-    *reinterpret_cast<xpu::u32x4 *>(dst + r * dst_cols + c0) = xpu::u32x4{w[0], w[1], w[2], w[3]};
+    *reinterpret_cast<xpu::u32x4 *>(dst + r * dst_cols + c0) = v;
   }
 }

@@ -428,12 +428,12 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
 // the prompt lasts (state[3] = prompt length), else the argmax; the argmax
 // after position p >= prompt length - 1 is stored at gen[p + 1 - length].
 // state: [0] position, [1] input token, [2] last argmax, [3] prompt length.
-extern "C" __global__ __launch_bounds__(256) void xpu_q3_argmax_finish(
+extern "C" __global__ __launch_bounds__(1024) void xpu_q3_argmax_finish(
     const float *__restrict__ part_val, const uint32_t *__restrict__ part_idx,
     const uint32_t *__restrict__ part_bad, uint32_t nparts, uint32_t *state,
     const uint32_t *__restrict__ prompt, uint32_t *__restrict__ gen, uint32_t gen_capacity) {
-  __shared__ float redv[4];
-  __shared__ uint32_t redi[4], redb[4];
+  __shared__ float redv[16];
+  __shared__ uint32_t redi[16], redb[16];
   float best = -__builtin_inff();
   uint32_t best_index = 0xffffffffu, bad = 0;
   for (uint32_t i = threadIdx.x; i < nparts; i += blockDim.x) {

@@ -336,7 +336,7 @@ int enqueue_fused_step(xpu_qwen3 &e) {
                     {8, &e.part_val}, {8, &e.part_idx}, {8, &e.part_bad}})))
     return rc;
   const uint32_t nparts = e.logits_l.grid;
-  return launch(e, e.finish_l, 256,
+  return launch(e, e.finish_l, 1024,
                 {{8, &e.part_val}, {8, &e.part_idx}, {8, &e.part_bad}, {4, &nparts}, {8, &e.state},
                  {8, &e.prompt}, {8, &e.gen}, {4, &max_seq}});
 }
