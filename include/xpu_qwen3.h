@@ -98,6 +98,15 @@ int xpu_qwen3_get_config(const xpu_qwen3 *eng, xpu_qwen3_config *out);
 
 int xpu_qwen3_set_mode(xpu_qwen3 *eng, int mode);
 
+/* Prompt processing in xpu_qwen3_generate (graph and eager modes): batched
+ * (default when the module has kernels for the shape) runs the prompt
+ * positions before the last as one batch per layer with the same arithmetic
+ * as the decode step, so the KV caches, tokens and logits are bit-identical
+ * to the stepwise path, which feeds the prompt through decode one position
+ * at a time as the reference does (main.cpp:343-344). XPU_ERR_INVALID when
+ * batched is requested for an unsupported shape. */
+int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int batched);
+
 /* One forward step at `position` for input `token`; *next = greedy token
  * (Engine::decode, main.cpp:159-226). A non-finite logit fails with
  * XPU_ERR_VERIFY ("model produced a NaN or infinity", main.cpp:223-224). */
@@ -119,7 +128,7 @@ int xpu_qwen3_generate(xpu_qwen3 *eng, const uint32_t *prompt, uint32_t n_prompt
 /* Command line with the reference's flags (main.cpp:17-72):
  *   --model-dir DIR | --synthetic PRESET [--seed N] [--gain-std X]
  *   --input-ids FILE|- --max-new-tokens N [--max-seq-len N]
- *   [--mode graph|eager|reference] [--no-eos-stop]
+ *   [--mode graph|eager|reference] [--prefill batched|stepwise] [--no-eos-stop]
  * prints {"generated_ids":[...]} on stdout, diagnostics on stderr. */
 int run_qwen3(int argc, char **argv);
 

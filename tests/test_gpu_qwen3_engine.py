@@ -197,3 +197,52 @@ def test_command_line_matches_oracle(tmp_path):
     bad = subprocess.run([exe, "--synthetic", "tiny", "--input-ids", str(ids), "--max-new-tokens", "60",
                           "--max-seq-len", "64"], capture_output=True, text=True, timeout=120)
     assert bad.returncode == 1 and "exceeds --max-seq-len" in bad.stderr
+
+
+@pytest.mark.parametrize("preset,n_prompt,max_seq", [("small", 40, 96), ("small", 2, 16), ("small", 1, 16),
+                                                      ("small", 300, 320)])
+def test_batched_prefill_bit_identical(rt, preset, n_prompt, max_seq):
+    # the prompt positions before the last in one batch per layer (chunks
+    # of 256 positions): same tokens, logits and hidden state as feeding the
+    # prompt through decode one position at a time, and as the oracle
+    cfg = orc.config(preset)
+    new = min(16, max_seq - n_prompt)
+    prompt = orc.tokens(n_prompt, 12, cfg.vocab)
+    m = orc.Model(cfg, seed=4, gain_std=0.1, max_seq=max_seq)
+    ref, ref_logits = m.generate(prompt, new, logit_steps=new)
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=max_seq, seed=4, gain_std=0.1, runtime=rt)
+    results = {}
+    for batched in (True, False):
+        eng.set_prefill(batched)
+        for mode in (qwen3.GRAPH, qwen3.EAGER):
+            print(f"{preset} n_prompt={n_prompt} batched={batched} mode={mode}", flush=True)
+            eng.set_mode(mode)
+            out, pm, dm = eng.generate(prompt, new, stop_on_eos=False)
+            results[(batched, mode)] = (out.tolist(), eng.logits().copy(), eng.hidden().copy(), pm)
+    for key, (toks, logits, hidden, pm) in results.items():
+        assert toks == ref.tolist(), key
+        assert np.array_equal(logits, ref_logits[new - 1]), key
+        assert np.array_equal(hidden, m.hidden()), key
+    print({k: round(v[3], 3) for k, v in results.items()})
+    eng.close()
+
+
+def test_batched_prefill_needs_kernels_for_the_shape(rt):
+    # hidden 256 is not a multiple of 512: no batched kernels, stepwise prompt
+    cfg = orc.config("tiny")
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=32, seed=1, gain_std=0.1, runtime=rt)
+    with pytest.raises(xpu.XpuError, match="batched prefill"):
+        eng.set_prefill(True)
+    prompt = orc.tokens(10, 3, cfg.vocab)
+    m = orc.Model(cfg, seed=1, gain_std=0.1, max_seq=32)
+    ref, _ = m.generate(prompt, 6)
+    out, _, _ = eng.generate(prompt, 6, stop_on_eos=False)
+    assert out.tolist() == ref.tolist()
+    eng.close()
+
+
+def test_prefill_cli_flag():
+    exe = os.path.join(xpu.BUILD_DIR, "qwen3_hip")
+    bad = subprocess.run([exe, "--synthetic", "tiny", "--input-ids", "-", "--max-new-tokens", "1", "--prefill", "x"],
+                         input="1 2 3\n", capture_output=True, text=True, timeout=120)
+    assert bad.returncode == 1 and "--prefill must be" in bad.stderr

@@ -454,3 +454,192 @@ extern "C" __global__ __launch_bounds__(1024) void xpu_q3_argmax_finish(
     }
   }
 }
+
+// ------------------------------------------------------------ batched prefill
+//
+// Part 3: the prompt positions before the last one go through the model as
+// one batch per layer (only their K/V cache entries are needed; the last
+// prompt position runs through the decode step, which produces the first
+// generated token). Every value is computed with the same operations in the
+// same order as the decode kernels, so the cache contents are bit-identical
+// to decoding the prompt one position at a time (qwen3/main.cpp:343-344).
+// Buffers hold T tokens of a chunk: X, Xn [T][H], QKV [T][(Hq+2Hkv)*128],
+// Q and A [T][Hq*128], Hb [T][I].
+
+// X[t] = embed[prompt[p0 + t]]
+extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_embed(const uint16_t *__restrict__ embed,
+                                                                  const uint32_t *__restrict__ prompt, uint32_t p0,
+                                                                  uint16_t *__restrict__ X, uint32_t H, uint32_t vocab) {
+  const uint32_t t = blockIdx.x;
+  uint32_t token = prompt[p0 + t];
+  if (token >= vocab) token = 0;
+  const uint16_t *src = embed + static_cast<uint64_t>(token) * H;
+  for (uint32_t i = threadIdx.x; i < H; i += blockDim.x) X[static_cast<uint64_t>(t) * H + i] = src[i];
+}
+
+// Xn[t] = rmsnorm(X[t]) * w (the decode kernels' prologue, block_rmsnorm_vec)
+extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_rmsnorm(const uint16_t *__restrict__ X,
+                                                                    const uint16_t *__restrict__ w,
+                                                                    uint16_t *__restrict__ Xn, uint32_t H, float eps) {
+  extern __shared__ __align__(16) uint16_t xs[];
+  __shared__ float red[1];
+  const uint64_t row = static_cast<uint64_t>(blockIdx.x) * H;
+  xpu::block_rmsnorm_vec(xs, X + row, w, H, eps, red);
+  for (uint32_t i = threadIdx.x * 8u; i < H; i += blockDim.x * 8u)
+    *reinterpret_cast<u32x4 *>(Xn + row + i) = *reinterpret_cast<const u32x4 *>(xs + i);
+}
+
+namespace {
+
+// Batched canonical GEMV: Out[t][row] for rows of W (M x K, K = 512 NC) and
+// token rows In[t] (T x K). A wavefront holds R rows (PAIRED: rows i and
+// I + i of a [gate; up] matrix, M = I) in registers for the whole token
+// loop; the block stages TT token rows at a time in LDS. Each (row, token)
+// dot product is the decode GEMV's: lane l, slot s accumulate elements
+// c*512 + 8 l + s over chunks c in order (FMA), then fold8 and the xor
+// butterfly. EPI 0: Out = bf16(y); 1: Out = bf16(Out + bf16(y)) (residual);
+// 2 (PAIRED): Out[t][i] = bf16(bf16(silu(bf16(g))) * bf16(u)).
+template <int R, int NC, int TT, int EPI>
+XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restrict__ In, uint16_t *Out, uint32_t M,
+                        uint32_t T) {
+  constexpr uint32_t K = 512u * NC;
+  constexpr bool kPaired = EPI == 2;
+  constexpr int kOuts = kPaired ? R / 2 : R;  // outputs per wavefront
+  __shared__ __align__(16) uint16_t xt[TT * K];
+  const uint32_t wave = threadIdx.x >> 6, lane = xpu::lane_id();
+  const uint32_t o0 = (blockIdx.x * 4u + wave) * kOuts;  // first output of this wavefront
+  const uint32_t rows_total = kPaired ? 2u * M : M;
+  // the wavefront's rows, chunk c at columns c*512 + 8 lane
+  u32x4 a[R][NC];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t want = kPaired ? (r < R / 2 ? o0 + r : M + o0 + (r - R / 2)) : o0 + r;
+    const uint32_t row = want < rows_total ? want : rows_total - 1;
+    const uint16_t *p = W + static_cast<uint64_t>(row) * K + lane * 8u;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) a[r][c] = xpu::load_nt16(p + c * 512u);
+  }
+  for (uint32_t t0 = 0; t0 < T; t0 += TT) {
+    __syncthreads();  // the previous tile is consumed
+    for (uint32_t i = threadIdx.x * 8u; i < TT * K; i += blockDim.x * 8u) {
+      const uint32_t tt = i / K, col = i % K;
+      *reinterpret_cast<u32x4 *>(xt + i) =
+          t0 + tt < T ? *reinterpret_cast<const u32x4 *>(In + static_cast<uint64_t>(t0 + tt) * K + col)
+                      : u32x4{0, 0, 0, 0};
+    }
+    __syncthreads();
+    float acc[R][TT][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[r][tt][e] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        float xf[8];
+        xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const u32x4 *>(xt + tt * K + c * 512u + lane * 8u), xf);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float af[8];
+          xpu::unpack8<xpu::kBf16>(a[r][c], af);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[r][tt][e] = __builtin_fmaf(af[e], xf[e], acc[r][tt][e]);
+        }
+      }
+    }
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      float y[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) y[r] = xpu::wave_butterfly(xpu::fold8(acc[r][tt]));
+      const uint32_t t = t0 + tt;
+      if (t >= T) continue;
+      uint16_t *orow = Out + static_cast<uint64_t>(t) * M;
+#pragma unroll
+      for (int o = 0; o < kOuts; ++o) {
+        if (lane != static_cast<uint32_t>(o) || o0 + o >= M) continue;
+        if constexpr (EPI == 0) {
+          orow[o0 + o] = static_cast<uint16_t>(xpu::f32_to_bf16(y[o]));
+        } else if constexpr (EPI == 1) {
+          const float sum = xpu::bf16_to_f32(orow[o0 + o]) + xpu::round_bf16(y[o]);
+          orow[o0 + o] = static_cast<uint16_t>(xpu::f32_to_bf16(sum));
+        } else {
+          orow[o0 + o] =
+              static_cast<uint16_t>(silu_mul_code(xpu::round_bf16(y[o]), xpu::round_bf16(y[kOuts + o])));
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+#define XPU_Q3_PF_GEMV(EPI, R, NC)                                                                  \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_gemv_e##EPI##_c##NC(                 \
+      const uint16_t *__restrict__ W, const uint16_t *__restrict__ In, uint16_t *Out, uint32_t M,  \
+      uint32_t T) {                                                                                 \
+    pf_gemv<R, NC, 4, EPI>(W, In, Out, M, T);                                                       \
+  }
+XPU_Q3_PF_GEMV(0, 2, 2)
+XPU_Q3_PF_GEMV(0, 2, 4)
+XPU_Q3_PF_GEMV(0, 2, 8)
+XPU_Q3_PF_GEMV(1, 1, 2)
+XPU_Q3_PF_GEMV(1, 1, 4)
+XPU_Q3_PF_GEMV(1, 1, 6)
+XPU_Q3_PF_GEMV(1, 1, 8)
+XPU_Q3_PF_GEMV(2, 2, 2)
+XPU_Q3_PF_GEMV(2, 2, 4)
+XPU_Q3_PF_GEMV(2, 2, 8)
+
+// QK-norm + RoPE of every token of the chunk: block (h, t), one wavefront.
+// h < heads: roped q of head h into Q[t]; else kv head h - heads: roped k
+// and the v row into the head-major caches at position p0 + t.
+extern "C" __global__ __launch_bounds__(64) void xpu_q3_pf_rope_cache(
+    const uint16_t *__restrict__ QKV, const uint16_t *__restrict__ qnorm_w, const uint16_t *__restrict__ knorm_w,
+    const uint16_t *__restrict__ rope_cos, const uint16_t *__restrict__ rope_sin, uint16_t *__restrict__ kcache,
+    uint16_t *__restrict__ vcache, uint16_t *__restrict__ Q, uint32_t p0, uint32_t heads, uint32_t kv_heads,
+    uint32_t max_seq, float eps) {
+  const uint32_t h = blockIdx.x, t = blockIdx.y, pos = p0 + t, lane = xpu::lane_id();
+  const uint32_t row_len = (heads + 2 * kv_heads) * xpu::kHeadDim;
+  const uint16_t *row = QKV + static_cast<uint64_t>(t) * row_len;
+  const bool is_q = h < heads;
+  const uint32_t kvh = is_q ? 0 : h - heads;
+  const uint16_t *src = is_q ? row + h * xpu::kHeadDim : row + (heads + kvh) * xpu::kHeadDim;
+  u32x4 hx = {0, 0, 0, 0}, hw = {0, 0, 0, 0}, hc = {0, 0, 0, 0}, hs = {0, 0, 0, 0};
+  if (lane < 16) {
+    hx = *reinterpret_cast<const u32x4 *>(src + lane * 8u);
+    hw = *reinterpret_cast<const u32x4 *>((is_q ? qnorm_w : knorm_w) + lane * 8u);
+    hc = *reinterpret_cast<const u32x4 *>(rope_cos + static_cast<uint64_t>(pos) * xpu::kHeadDim + lane * 8u);
+    hs = *reinterpret_cast<const u32x4 *>(rope_sin + static_cast<uint64_t>(pos) * xpu::kHeadDim + lane * 8u);
+  }
+  const uint64_t slot = (static_cast<uint64_t>(kvh) * max_seq + pos) * xpu::kHeadDim;
+  uint16_t *dst = is_q ? Q + static_cast<uint64_t>(t) * heads * xpu::kHeadDim + h * xpu::kHeadDim : kcache + slot;
+  xpu::head_norm_rope_vec(hx, hw, hc, hs, eps, dst);
+  if (!is_q && lane < 16) {
+    const uint16_t *vsrc = row + (heads + kv_heads + kvh) * xpu::kHeadDim;
+    *reinterpret_cast<u32x4 *>(vcache + slot + lane * 8u) = *reinterpret_cast<const u32x4 *>(vsrc + lane * 8u);
+  }
+}
+
+// Attention of every token of the chunk: block (head, t) over cache
+// positions 0..p0 + t (all written by xpu_q3_pf_rope_cache and earlier
+// steps), the general attention_head of the decode path.
+extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_attention(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache,
+    uint16_t *__restrict__ A, uint32_t p0, uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float scale) {
+  __shared__ float sbuf[xpu::kAttnChunk];
+  __shared__ float red[4 * xpu::kHeadDim];
+  __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
+  __shared__ __align__(16) uint16_t vtile[xpu::kAttnTile * xpu::kVPitch];
+  const uint32_t head = blockIdx.x, t = blockIdx.y;
+  const uint32_t kv = head / (heads / kv_heads);
+  const uint64_t qoff = (static_cast<uint64_t>(t) * heads + head) * xpu::kHeadDim;
+  if (threadIdx.x < xpu::kHeadDim) qs[threadIdx.x] = Q[qoff + threadIdx.x];
+  __syncthreads();
+  const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
+  xpu::attention_head<false>(qs, kcache + head_base, vcache + head_base, xpu::kHeadDim, p0 + t + 1, nullptr,
+                             nullptr, scale, A + qoff, sbuf, vtile, red);
+}

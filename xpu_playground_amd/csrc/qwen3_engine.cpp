@@ -141,12 +141,21 @@ struct xpu_qwen3 {
     const xpu::KernelInfo *k = nullptr;
     uint32_t grid = 0, shared = 0;
   } qkv_l, attn_l, o_l, gu_l, down_l, logits_l, finish_l;
+  // batched prefill (kernels/qwen3_ops.hip part 3): chunk buffers of
+  // pf_chunk tokens; pf_ok when the shape has kernels for every projection
+  bool pf_ok = false, batched_prefill = false;
+  uint32_t pf_chunk = 0;
+  void *pf_block = nullptr;
+  uint16_t *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_a = nullptr,
+           *pf_h = nullptr;
+  const xpu::KernelInfo *pf_embed_k = nullptr, *pf_norm_k = nullptr, *pf_rope_k = nullptr, *pf_attn_k = nullptr,
+                        *pf_qkv_k = nullptr, *pf_o_k = nullptr, *pf_gu_k = nullptr, *pf_down_k = nullptr;
 
   ~xpu_qwen3() {
     if (graph) xpu_rt_graph_destroy(graph);
     if (rt) {
       for (void *p : {static_cast<void *>(arena), static_cast<void *>(kcache), static_cast<void *>(vcache),
-                      static_cast<void *>(cos_t), static_cast<void *>(sin_t), static_cast<void *>(x)})
+                      static_cast<void *>(cos_t), static_cast<void *>(sin_t), static_cast<void *>(x), pf_block})
         if (p) xpu_rt_free(rt, p);
       if (owns_rt) xpu_rt_destroy(rt);
     }
@@ -298,6 +307,43 @@ int setup_launches(xpu_qwen3 &e) {
   return XPU_OK;
 }
 
+// Batched prefill needs every projection's K to be 512 times a chunk count
+// the module has kernels for (xpu_q3_pf_gemv_e<epi>_c<K/512>).
+int setup_prefill(xpu_qwen3 &e) {
+  const xpu_qwen3_config &c = e.c;
+  const uint32_t qd = c.heads * c.head_dim;
+  auto gemv = [&](int epi, uint32_t K) -> const xpu::KernelInfo * {
+    if (K % 512u) return nullptr;
+    return e.rt->find_exact("xpu_q3_pf_gemv_e" + std::to_string(epi) + "_c" + std::to_string(K / 512u));
+  };
+  e.pf_qkv_k = gemv(0, c.hidden);
+  e.pf_o_k = gemv(1, qd);
+  e.pf_gu_k = gemv(2, c.hidden);
+  e.pf_down_k = gemv(1, c.intermediate);
+  e.pf_embed_k = e.rt->find_exact("xpu_q3_pf_embed");
+  e.pf_norm_k = e.rt->find_exact("xpu_q3_pf_rmsnorm");
+  e.pf_rope_k = e.rt->find_exact("xpu_q3_pf_rope_cache");
+  e.pf_attn_k = e.rt->find_exact("xpu_q3_pf_attention");
+  e.pf_ok = e.pf_qkv_k && e.pf_o_k && e.pf_gu_k && e.pf_down_k && e.pf_embed_k && e.pf_norm_k && e.pf_rope_k &&
+            e.pf_attn_k && c.hidden % 8 == 0 && kpad_bytes(c.hidden) <= e.rt->max_shared;
+  if (!e.pf_ok) return XPU_OK;
+  e.pf_chunk = std::min<uint32_t>(e.max_seq, 256);
+  const uint64_t T = e.pf_chunk, qkv_rows = uint64_t{c.heads + 2 * c.kv_heads} * c.head_dim;
+  const uint64_t sizes[6] = {T * c.hidden, T * c.hidden, T * qkv_rows, T * qd, T * qd, T * c.intermediate};
+  uint64_t total = 0;
+  for (uint64_t n : sizes) total += (n * 2 + 255) & ~uint64_t{255};
+  int rc = xpu_rt_alloc(e.rt, total, 4096, &e.pf_block);
+  if (rc) return rc;
+  uint16_t **dst[6] = {&e.pf_x, &e.pf_xn, &e.pf_qkv, &e.pf_q, &e.pf_a, &e.pf_h};
+  uint8_t *p = static_cast<uint8_t *>(e.pf_block);
+  for (int i = 0; i < 6; ++i) {
+    *dst[i] = reinterpret_cast<uint16_t *>(p);
+    p += (sizes[i] * 2 + 255) & ~uint64_t{255};
+  }
+  e.batched_prefill = true;
+  return XPU_OK;
+}
+
 int launch(xpu_qwen3 &e, const xpu_qwen3::Launch &l, uint32_t block, std::initializer_list<xpu_kernel_arg> args) {
   return e.rt->launch(*l.k, l.grid, 1, block, l.shared, args.begin(), static_cast<uint32_t>(args.size()));
 }
@@ -339,6 +385,58 @@ int enqueue_fused_step(xpu_qwen3 &e) {
   return launch(e, e.finish_l, 1024,
                 {{8, &e.part_val}, {8, &e.part_idx}, {8, &e.part_bad}, {4, &nparts}, {8, &e.state},
                  {8, &e.prompt}, {8, &e.gen}, {4, &max_seq}});
+}
+
+// K/V cache entries of prompt positions [0, P) (prompt ids already in
+// e.prompt), in chunks of pf_chunk positions. The last layer's o_proj and
+// MLP are skipped: only the caches are wanted.
+int run_prefill(xpu_qwen3 &e, uint32_t P) {
+  const xpu_qwen3_config &c = e.c;
+  uint32_t H = c.hidden, I = c.intermediate, V = c.vocab, heads = c.heads, kv = c.kv_heads, max_seq = e.max_seq;
+  uint32_t qkv_rows = (heads + 2 * kv) * c.head_dim;
+  float eps = c.rms_eps;
+  float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
+  const uint64_t cache_layer = uint64_t{kv} * max_seq * c.head_dim;
+  xpu_runtime *rt = e.rt;
+  auto go = [&](const xpu::KernelInfo *k, uint32_t gx, uint32_t gy, uint32_t block, uint32_t shared,
+                std::initializer_list<xpu_kernel_arg> args) {
+    return rt->launch(*k, gx, gy, block, shared, args.begin(), static_cast<uint32_t>(args.size()));
+  };
+  int rc;
+  for (uint32_t p0 = 0; p0 < P; p0 += e.pf_chunk) {
+    uint32_t T = std::min(e.pf_chunk, P - p0);
+    if ((rc = go(e.pf_embed_k, T, 1, 256, 0, {{8, &e.embed}, {8, &e.prompt}, {4, &p0}, {8, &e.pf_x}, {4, &H}, {4, &V}})))
+      return rc;
+    for (uint32_t l = 0; l < c.layers; ++l) {
+      const Layer &L = e.layers[l];
+      uint16_t *kc = e.kcache + l * cache_layer, *vc = e.vcache + l * cache_layer;
+      if ((rc = go(e.pf_norm_k, T, 1, 256, kpad_bytes(H),
+                   {{8, &e.pf_x}, {8, &L.in_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}})))
+        return rc;
+      if ((rc = go(e.pf_qkv_k, (qkv_rows + 7) / 8, 1, 256, 0,
+                   {{8, &L.qkv}, {8, &e.pf_xn}, {8, &e.pf_qkv}, {4, &qkv_rows}, {4, &T}})))
+        return rc;
+      if ((rc = go(e.pf_rope_k, heads + kv, T, 64, 0,
+                   {{8, &e.pf_qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &kc},
+                    {8, &vc}, {8, &e.pf_q}, {4, &p0}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps}})))
+        return rc;
+      if ((rc = go(e.pf_attn_k, heads, T, 256, 0,
+                   {{8, &e.pf_q}, {8, &kc}, {8, &vc}, {8, &e.pf_a}, {4, &p0}, {4, &heads}, {4, &kv},
+                    {4, &max_seq}, {4, &scale}})))
+        return rc;
+      if (l + 1 == c.layers) break;
+      if ((rc = go(e.pf_o_k, (H + 3) / 4, 1, 256, 0, {{8, &L.o}, {8, &e.pf_a}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
+        return rc;
+      if ((rc = go(e.pf_norm_k, T, 1, 256, kpad_bytes(H),
+                   {{8, &e.pf_x}, {8, &L.post_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}})))
+        return rc;
+      if ((rc = go(e.pf_gu_k, (I + 3) / 4, 1, 256, 0, {{8, &L.gu}, {8, &e.pf_xn}, {8, &e.pf_h}, {4, &I}, {4, &T}})))
+        return rc;
+      if ((rc = go(e.pf_down_k, (H + 3) / 4, 1, 256, 0, {{8, &L.down}, {8, &e.pf_h}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
+        return rc;
+    }
+  }
+  return XPU_OK;
 }
 
 int run_fused_step(xpu_qwen3 &e) {
@@ -422,7 +520,8 @@ int init_engine(xpu_qwen3 &e, xpu_runtime *rt, const xpu_qwen3_config &cfg, uint
   plan_arena(e, nullptr);
   if ((rc = allocate_buffers(e))) return rc;
   plan_arena(e, e.arena);
-  return setup_launches(e);
+  if ((rc = setup_launches(e))) return rc;
+  return setup_prefill(e);
 }
 
 // ---------------------------------------------------------------- checkpoint
@@ -724,6 +823,14 @@ extern "C" int xpu_qwen3_set_mode(xpu_qwen3 *eng, int mode) {
   return XPU_OK;
 }
 
+extern "C" int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int batched) {
+  if (!eng) return set_error(XPU_ERR_INVALID, "null engine");
+  if (batched && !eng->pf_ok)
+    return set_error(XPU_ERR_INVALID, "batched prefill has no kernels for this model shape");
+  eng->batched_prefill = batched != 0;
+  return XPU_OK;
+}
+
 extern "C" int xpu_qwen3_decode(xpu_qwen3 *eng, uint32_t token, uint32_t position, uint32_t *next) {
   if (!eng || !next) return set_error(XPU_ERR_INVALID, "null argument");
   if (token >= eng->c.vocab) return set_error(XPU_ERR_INVALID, "input token ID is outside the vocabulary");
@@ -790,13 +897,17 @@ extern "C" int xpu_qwen3_generate(xpu_qwen3 *eng, const uint32_t *prompt, uint32
     *n_out = produced;
   } else {
     if ((rc = xpu_rt_copy_to_device(eng->rt, eng->prompt, prompt, n_prompt * 4ull))) return rc;
-    const uint32_t st[4] = {0, prompt[0], 0, n_prompt};
+    // batched prefill fills the caches of positions 0..n_prompt-2; the last
+    // prompt position runs as a decode step (it yields the first new token)
+    const uint32_t first = eng->batched_prefill ? n_prompt - 1 : 0;
+    const uint32_t st[4] = {first, prompt[first], 0, n_prompt};
     if ((rc = xpu_rt_copy_to_device(eng->rt, eng->state, st, sizeof(st)))) return rc;
     void *ev[3] = {nullptr, nullptr, nullptr};
     for (auto &v : ev)
       if ((rc = xpu_rt_event_create(eng->rt, &v))) return rc;
     rc = xpu_rt_event_record(eng->rt, ev[0]);
-    for (uint32_t s = 0; !rc && s < steps; ++s) {
+    if (!rc && first) rc = run_prefill(*eng, first);
+    for (uint32_t s = first; !rc && s < steps; ++s) {
       rc = run_fused_step(*eng);
       if (!rc && s + 1 == n_prompt) rc = xpu_rt_event_record(eng->rt, ev[1]);
     }
@@ -834,6 +945,7 @@ struct QwenOptions {
   uint64_t seed = 0;
   float gain_std = 0.0f;
   int mode = XPU_QWEN3_GRAPH;
+  int prefill = -1;  // -1: the engine's default
 };
 
 [[noreturn]] void qwen_usage_error(const std::string &message) {
@@ -864,7 +976,7 @@ QwenOptions parse_qwen(int argc, char **argv) {
       std::cout << "Usage: " << argv[0]
                 << " --model-dir DIR | --synthetic qwen3-0.6b|qwen3-8b|tiny|small [--seed N] [--gain-std X]\n"
                    "       --input-ids FILE|- --max-new-tokens N [--max-seq-len N]\n"
-                   "       [--mode graph|eager|reference] [--no-eos-stop]\n";
+                   "       [--mode graph|eager|reference] [--prefill batched|stepwise] [--no-eos-stop]\n";
       std::exit(0);
     }
     if (opt == "--no-eos-stop") { o.stop_on_eos = false; continue; }
@@ -882,6 +994,10 @@ QwenOptions parse_qwen(int argc, char **argv) {
       else if (v == "eager") o.mode = XPU_QWEN3_EAGER;
       else if (v == "reference") o.mode = XPU_QWEN3_REFERENCE;
       else qwen_usage_error("--mode must be graph, eager or reference");
+    } else if (opt == "--prefill") {
+      if (v == "batched") o.prefill = 1;
+      else if (v == "stepwise") o.prefill = 0;
+      else qwen_usage_error("--prefill must be batched or stepwise");
     } else {
       qwen_usage_error("unknown option: " + opt);
     }
@@ -943,6 +1059,7 @@ extern "C" int run_qwen3(int argc, char **argv) {
     if (rc) throw std::runtime_error(xpu_last_error());
     const double load_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     if (xpu_qwen3_set_mode(eng, o.mode)) throw std::runtime_error(xpu_last_error());
+    if (o.prefill >= 0 && xpu_qwen3_set_prefill(eng, o.prefill)) throw std::runtime_error(xpu_last_error());
     std::cerr << "qwen3_hip: " << eng->rt->name << " (" << eng->rt->arch << "), " << cfg.layers << " layers, hidden "
               << cfg.hidden << ", weights " << (eng->arena_bytes >> 20) << " MiB loaded in " << load_s << " s\n";
     std::vector<uint32_t> out(std::max(o.max_new_tokens, 1u));

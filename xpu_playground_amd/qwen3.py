@@ -101,6 +101,10 @@ class Engine:
     def set_mode(self, mode: int) -> None:
         check(self.lib.xpu_qwen3_set_mode(self.handle, mode))
 
+    def set_prefill(self, batched: bool) -> None:
+        """Batched (default) or stepwise prompt processing in generate."""
+        check(self.lib.xpu_qwen3_set_prefill(self.handle, 1 if batched else 0))
+
     def decode(self, token: int, position: int) -> int:
         nxt = c_uint32()
         check(self.lib.xpu_qwen3_decode(self.handle, token, position, ctypes.byref(nxt)))
