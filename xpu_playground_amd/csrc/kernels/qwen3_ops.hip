@@ -504,8 +504,11 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
                         uint32_t T) {
   constexpr uint32_t K = 512u * NC;
   constexpr bool kPaired = EPI == 2;
-  constexpr int kOuts = kPaired ? R / 2 : R;  // outputs per wavefront
-  __shared__ __align__(16) uint16_t xt[TT * K];
+  constexpr int kOuts = kPaired ? R / 2 : R;         // outputs per wavefront
+  constexpr uint32_t kTile = TT * K;                 // codes per token tile
+  constexpr int kLoads = kTile / (256 * 8);          // 16-byte staging loads per thread
+  static_assert(kTile % (256 * 8) == 0, "tile must split evenly over the block");
+  extern __shared__ __align__(16) uint16_t xt[];     // two tiles
   const uint32_t wave = threadIdx.x >> 6, lane = xpu::lane_id();
   const uint32_t o0 = (blockIdx.x * 4u + wave) * kOuts;  // first output of this wavefront
   const uint32_t rows_total = kPaired ? 2u * M : M;
@@ -519,15 +522,29 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
 #pragma unroll
     for (int c = 0; c < NC; ++c) a[r][c] = xpu::load_nt16(p + c * 512u);
   }
-  for (uint32_t t0 = 0; t0 < T; t0 += TT) {
-    __syncthreads();  // the previous tile is consumed
-    for (uint32_t i = threadIdx.x * 8u; i < TT * K; i += blockDim.x * 8u) {
-      const uint32_t tt = i / K, col = i % K;
-      *reinterpret_cast<u32x4 *>(xt + i) =
-          t0 + tt < T ? *reinterpret_cast<const u32x4 *>(In + static_cast<uint64_t>(t0 + tt) * K + col)
-                      : u32x4{0, 0, 0, 0};
+  // token tiles are double buffered: the loads of tile i + 1 are issued
+  // before the FMAs of tile i and stored to the other buffer after them
+  u32x4 stage[kLoads];
+  auto load_tile = [&](uint32_t t0) {
+#pragma unroll
+    for (int q = 0; q < kLoads; ++q) {
+      const uint32_t i = (threadIdx.x + q * 256u) * 8u, tt = i / K, col = i % K;
+      stage[q] = t0 + tt < T ? *reinterpret_cast<const u32x4 *>(In + static_cast<uint64_t>(t0 + tt) * K + col)
+                             : u32x4{0, 0, 0, 0};
     }
-    __syncthreads();
+  };
+  auto store_tile = [&](uint16_t *buf) {
+#pragma unroll
+    for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4 *>(buf + (threadIdx.x + q * 256u) * 8u) = stage[q];
+  };
+  load_tile(0);
+  store_tile(xt);
+  __syncthreads();
+  uint32_t cur = 0;
+  for (uint32_t t0 = 0; t0 < T; t0 += TT) {
+    const bool more = t0 + TT < T;
+    if (more) load_tile(t0 + TT);
+    const uint16_t *tile = xt + cur * kTile;
     float acc[R][TT][8];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -540,7 +557,7 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
         float xf[8];
-        xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const u32x4 *>(xt + tt * K + c * 512u + lane * 8u), xf);
+        xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const u32x4 *>(tile + tt * K + c * 512u + lane * 8u), xf);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           float af[8];
@@ -572,6 +589,11 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
         }
       }
     }
+    if (more) {
+      store_tile(xt + (cur ^ 1u) * kTile);
+      __syncthreads();
+      cur ^= 1u;
+    }
   }
 }
 
@@ -581,7 +603,7 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
   extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_gemv_e##EPI##_c##NC(                 \
       const uint16_t *__restrict__ W, const uint16_t *__restrict__ In, uint16_t *Out, uint32_t M,  \
       uint32_t T) {                                                                                 \
-    pf_gemv<R, NC, 4, EPI>(W, In, Out, M, T);                                                       \
+    pf_gemv<R, NC, 8, EPI>(W, In, Out, M, T);                                                       \
   }
 XPU_Q3_PF_GEMV(0, 2, 2)
 XPU_Q3_PF_GEMV(0, 2, 4)

@@ -325,7 +325,8 @@ int setup_prefill(xpu_qwen3 &e) {
   e.pf_rope_k = e.rt->find_exact("xpu_q3_pf_rope_cache");
   e.pf_attn_k = e.rt->find_exact("xpu_q3_pf_attention");
   e.pf_ok = e.pf_qkv_k && e.pf_o_k && e.pf_gu_k && e.pf_down_k && e.pf_embed_k && e.pf_norm_k && e.pf_rope_k &&
-            e.pf_attn_k && c.hidden % 8 == 0 && kpad_bytes(c.hidden) <= e.rt->max_shared;
+            e.pf_attn_k && c.hidden % 8 == 0 && kpad_bytes(c.hidden) <= e.rt->max_shared &&
+            32u * std::max({c.hidden, qd, c.intermediate}) <= e.rt->max_shared;
   if (!e.pf_ok) return XPU_OK;
   e.pf_chunk = std::min<uint32_t>(e.max_seq, 256);
   const uint64_t T = e.pf_chunk, qkv_rows = uint64_t{c.heads + 2 * c.kv_heads} * c.head_dim;
@@ -393,8 +394,10 @@ int enqueue_fused_step(xpu_qwen3 &e) {
 int run_prefill(xpu_qwen3 &e, uint32_t P) {
   const xpu_qwen3_config &c = e.c;
   uint32_t H = c.hidden, I = c.intermediate, V = c.vocab, heads = c.heads, kv = c.kv_heads, max_seq = e.max_seq;
-  uint32_t qkv_rows = (heads + 2 * kv) * c.head_dim;
+  uint32_t qkv_rows = (heads + 2 * kv) * c.head_dim, qd = heads * c.head_dim;
   float eps = c.rms_eps;
+  // two tiles of 8 token rows of K codes (xpu_q3_pf_gemv_*)
+  auto pf_lds = [](uint32_t K) { return 2u * 8u * K * 2u; };
   float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
   const uint64_t cache_layer = uint64_t{kv} * max_seq * c.head_dim;
   xpu_runtime *rt = e.rt;
@@ -413,7 +416,7 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
       if ((rc = go(e.pf_norm_k, T, 1, 256, kpad_bytes(H),
                    {{8, &e.pf_x}, {8, &L.in_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}})))
         return rc;
-      if ((rc = go(e.pf_qkv_k, (qkv_rows + 7) / 8, 1, 256, 0,
+      if ((rc = go(e.pf_qkv_k, (qkv_rows + 7) / 8, 1, 256, pf_lds(H),
                    {{8, &L.qkv}, {8, &e.pf_xn}, {8, &e.pf_qkv}, {4, &qkv_rows}, {4, &T}})))
         return rc;
       if ((rc = go(e.pf_rope_k, heads + kv, T, 64, 0,
@@ -425,14 +428,14 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
                     {4, &max_seq}, {4, &scale}})))
         return rc;
       if (l + 1 == c.layers) break;
-      if ((rc = go(e.pf_o_k, (H + 3) / 4, 1, 256, 0, {{8, &L.o}, {8, &e.pf_a}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
+      if ((rc = go(e.pf_o_k, (H + 3) / 4, 1, 256, pf_lds(qd), {{8, &L.o}, {8, &e.pf_a}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
         return rc;
       if ((rc = go(e.pf_norm_k, T, 1, 256, kpad_bytes(H),
                    {{8, &e.pf_x}, {8, &L.post_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}})))
         return rc;
-      if ((rc = go(e.pf_gu_k, (I + 3) / 4, 1, 256, 0, {{8, &L.gu}, {8, &e.pf_xn}, {8, &e.pf_h}, {4, &I}, {4, &T}})))
+      if ((rc = go(e.pf_gu_k, (I + 3) / 4, 1, 256, pf_lds(H), {{8, &L.gu}, {8, &e.pf_xn}, {8, &e.pf_h}, {4, &I}, {4, &T}})))
         return rc;
-      if ((rc = go(e.pf_down_k, (H + 3) / 4, 1, 256, 0, {{8, &L.down}, {8, &e.pf_h}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
+      if ((rc = go(e.pf_down_k, (H + 3) / 4, 1, 256, pf_lds(I), {{8, &L.down}, {8, &e.pf_h}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
         return rc;
     }
   }
