@@ -297,34 +297,38 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     it += 2;
   } while (it < nk);
 
-  // Epilogue through LDS (free after the loop's last barrier), one 32-row
-  // band per round: each wave writes its 32 x 128 FP32 band (D layout of
+  // Epilogue through LDS (free after the loop's last barrier), one 64-row
+  // band per round: each wave writes its 64 x 128 FP32 band (D layout of
   // v_mfma_f32_32x32x16 with C^T tiles: lane l holds row l % 32, columns
   // 8 g + 4 (l / 32) + 0..3 in accumulators 4 g..4 g + 3) as 16-byte rows
   // into its own region (pitch 132 floats: the 8 rows written by 8
   // consecutive lanes fall in distinct banks), then reads it back 8
   // consecutive columns per lane and stores 16 bytes of C per lane.
   constexpr uint32_t kEpPitch = 132;
-  float *ep = reinterpret_cast<float *>(&lds[0][0][0]) + wave * 32u * kEpPitch;
+  float *ep = reinterpret_cast<float *>(&lds[0][0][0]) + wave * 64u * kEpPitch;
   const uint32_t m_lane = lane & 31u, n_lane = (lane >> 5) * 4u;
   const uint32_t r_lane = lane >> 4, c_lane = (lane & 15u) * 8u;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int band = 0; band < 2; ++band) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<f32x4 *>(ep + m_lane * kEpPitch + j * 32u + 8u * g + n_lane) =
-            f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int i = band * 2 + ii;
+          *reinterpret_cast<f32x4 *>(ep + (ii * 32u + m_lane) * kEpPitch + j * 32u + 8u * g + n_lane) =
+              f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int rr = 0; rr < 8; ++rr) {
+    for (int rr = 0; rr < 16; ++rr) {
       const uint32_t r = rr * 4u + r_lane;
       const f32x4 lo = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane);
       const f32x4 hi = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane + 4u);
-      const uint32_t m = c.m0 + wm * 128u + i * 32u + r, n = c.n0 + wn * 128u + c_lane;
+      const uint32_t m = c.m0 + wm * 128u + band * 64u + r, n = c.n0 + wn * 128u + c_lane;
       if (m >= M || n >= n_out) continue;
       const u32x4 packed{cvt_pack<DT>(lo.x, lo.y), cvt_pack<DT>(lo.z, lo.w), cvt_pack<DT>(hi.x, hi.y),
                          cvt_pack<DT>(hi.z, hi.w)};
