@@ -64,7 +64,7 @@ extern "C" int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B
   const uint32_t k_run = static_cast<uint32_t>(a_direct ? K : kp);  // reduction length seen by the kernel
   const uint32_t n_run = static_cast<uint32_t>(b_direct ? N : np);  // columns of the B operand
   const bool c16 = reinterpret_cast<uintptr_t>(C) % 16 == 0 && N % 8 == 0;
-  const std::string name = std::string("xpu_gemm_") + (dtype ? "fp16" : "bf16") + (c16 ? "_vec" : "_vecu");
+  const std::string name = std::string("xpu_gemm_") + (dtype ? "fp16" : "bf16") + (c16 ? "_dma" : "_dmau");
   const xpu::KernelInfo *k = rt->find_exact(name);
   if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: " + name);
   const uint64_t tiles = ((static_cast<uint64_t>(M) + 255) / 256) * ((static_cast<uint64_t>(n_run) + 255) / 256);

@@ -1,41 +1,56 @@
-// GEMM C[M x N] = A[M x K] . B[K x N] on gfx950 MFMA, bf16 or fp16 storage,
-// FP32 accumulation (reference: gemm_kernel.hpp:25-143 with argument order
-// (a, b, c, m, n, k), level_zero/gem_spv_entry.cpp:28-60).
+// GEMM C[M x N] = A[M x K] . B[K x N] on gfx950 MFMA with LDS-DMA operand
+// staging, bf16 or fp16 storage, FP32 accumulation (reference:
+// gemm_kernel.hpp:25-143, argument order (a, b, c, m, n, k) of
+// level_zero/gem_spv_entry.cpp:28-60).
 //
-// Block tile 256 x 256 x 64 with 256 threads: four wavefronts in a 2 x 2
-// arrangement, each owning 128 x 128 of C as 4 x 4 tiles of
-// v_mfma_f32_32x32x16_{bf16,f16} (256 FP32 accumulators per lane, in AGPRs).
-// A and B K-slices are loaded with buffer instructions into registers two
-// slices ahead and stored to LDS, double buffered, one barrier per slice. A
-// is stored row-major [m][k]; B is transposed in registers (8 x 8 blocks of
-// 16-bit values via v_perm_b32) and stored [n][k], so both MFMA operands are
-// single 16-byte LDS reads. Rows are padded by 8 elements so the 32 rows read
-// by one ds_read_b128 fall in distinct banks.
+// Block tile 256 x 256, K-slice BK (64 or 32), S LDS stages, 256 threads:
+// four wavefronts in a 2 x 2 arrangement, each owning 128 x 128 of C as
+// 4 x 4 tiles of v_mfma_f32_32x32x16_{bf16,f16} (256 FP32 accumulators per
+// lane).
 //
-// The kernels need A and B rows 16-byte aligned (K and N multiples of 8);
-// the host pads other shapes into a workspace first (xpu_pad_rows below, the
-// device counterpart of the reference's host padding, gemm.cpp:75-85). Rows
-// past M, columns past N and the K tail are handled in the kernel: loads
-// past the end of A or B read zero through the buffer range check, stores
-// are masked.
+// Operands go from global memory straight into LDS with buffer_load_dwordx4
+// ... lds (the LDS-DMA form: lane t's 16 bytes land at M0 + 16 t), so no
+// VGPR staging and no LDS store instructions. Both tiles keep the global
+// row-major orientation: A as [m][k] (2 BK bytes per row), B as [k][n]
+// (512 bytes per row). 16-byte chunks are XOR-swizzled within a row so the
+// fragment reads hit distinct banks. A fragments are single ds_read_b128
+// (lane l: row l % 32, 8 consecutive k); B fragments are two
+// ds_read_b64_tr_b16 (the gfx950 transposing read: within each 16-lane
+// group, lane j receives element (j & 3) of the 4-element rows addressed by
+// lanes (j >> 2) + 4 e, e = 0..3), which hand each lane 8 consecutive k of
+// one column n - the MFMA operand layout - out of the [k][n] tile.
 //
-// Tile order: blocks are dealt round-robin to the 8 XCDs, so when the tile
-// count is a multiple of 8 block b is renumbered to a contiguous range per
-// XCD; tiles are then walked in groups of 4 tile-rows so the blocks of one
-// XCD share A and B panels in that XCD's L2 (the reference snakes the
-// tile order, gemm_kernel.hpp:79-83, for its L3).
+// Pipeline (slice s in stage s % S): the DMA of slice s + S is issued right
+// after the barrier that publishes slice s + 1, into the stage slice s just
+// vacated; that barrier sits in slice s's last k-step after the first P of
+// its 16 MFMAs (P = 0 in the kernels built here: the slice's DMA and the
+// next slice's first fragment reads then spread over all 16), and is
+// preceded by a vmcnt wait that leaves the DMA of slices s + 2 .. s + S - 1
+// in flight. Fragments of the next k-step are read while the current one's
+// MFMAs run.
+//
+// Edges: loads past row M of A and past row K of B read zero through the
+// buffer range check; 16-byte chunks past column K of A or N of B are sent
+// beyond the descriptor range, so K and N must be multiples of 8 with A and
+// B 16-byte aligned; the host pads other shapes into a workspace first
+// (xpu_pad_rows below, the device counterpart of the reference's host
+// padding, gemm.cpp:75-85). Stores are masked to M x n_out; the _dmau
+// variants store C element by element (C rows not 16-byte aligned).
 #include "device_common.hpp"
 
 namespace xpu {
+namespace dma {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-constexpr uint32_t kBM = 256, kBN = 256, kBK = 64;
-constexpr uint32_t kLdsPitch = kBK + 8;  // elements per staged row
-constexpr uint32_t kTileElems = kBM * kLdsPitch;
+constexpr uint32_t kBM = 256, kBN = 256;
+constexpr uint32_t kOob = 0x80000000u;  // any offset >= the descriptor range reads 0
 
 template <int DT>
 XPU_DEVICE f32x16 mfma(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
@@ -47,10 +62,57 @@ XPU_DEVICE f32x16 mfma(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// Raw buffer descriptor: 48-bit base, stride 0, num_records bytes, 32-bit
+// data format. Offsets at or past num_records read as zero.
+XPU_DEVICE i32x4 rsrc(const void *base, int64_t records) {
+  records = records < 0 ? 0 : (records > 0x7fffffff ? 0x7fffffff : records);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4{static_cast<int>(a & 0xffffffffu), static_cast<int>((a >> 32) & 0xffffu),
+               static_cast<int>(records), 0x00020000};
+}
+
+// 16 bytes per lane from the buffer at voff into LDS at m0 + 16 * lane.
+// Written as asm so that the compiler's wait-count pass, which cannot tell
+// the stages apart, does not wait for every DMA before each LDS read; the
+// loop below issues the waits itself.
+XPU_DEVICE void dma16(uint32_t m0, const i32x4 &r, uint32_t voff) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(r), "{m0}"(m0)
+               : "memory");
+}
+
+template <int N> XPU_DEVICE void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  // gfx9 s_waitcnt: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14; expcnt and
+  // lgkmcnt at their maxima (no wait)
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// XOR swizzles of 16-byte chunks. A: row r of the tile (2 BK bytes), B:
+// row k (512 bytes). With them the rows read by one ds_read_b128 (32 rows,
+// one chunk column) and the 4 x 4 (row, chunk) blocks read by one
+// ds_read_b64_tr_b16 group pair fall into distinct 16-byte bank groups
+// whether the LDS serves 128 or 256 bytes per clock.
+template <int BK> XPU_DEVICE uint32_t a_swz(uint32_t r) {
+  if constexpr (BK == 64) return (r & 7u) ^ ((r >> 3) & 1u);
+  else return ((r >> 1) & 3u) ^ ((r >> 3) & 1u);
+}
+XPU_DEVICE uint32_t b_swz(uint32_t k) { return ((k & 1u) ? 10u : 0u) ^ ((k & 2u) ? 4u : 0u); }
+
+XPU_DEVICE uint32_t lds_addr(const void *p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)p));
+}
+
 struct TileCoord {
   uint32_t tm, tn;
 };
 
+// Blocks are dealt round-robin to the 8 XCDs; when the tile count is a
+// multiple of 8, block b is renumbered to a contiguous range per XCD, and
+// tiles are walked in groups of 4 tile-rows so the blocks of one XCD share
+// A and B panels in that XCD's L2.
 XPU_DEVICE TileCoord tile_of_block(uint32_t b, uint32_t tiles_m, uint32_t tiles_n) {
   const uint32_t total = tiles_m * tiles_n;
   uint32_t logical = b;
@@ -64,35 +126,6 @@ XPU_DEVICE TileCoord tile_of_block(uint32_t b, uint32_t tiles_m, uint32_t tiles_
   return {first_m + in_group % rows, in_group / rows};
 }
 
-// ------------------------------------------------------------------ main path
-//
-// Rows of A and B 16-byte aligned (K, N multiples of 8): every 8-element
-// chunk is wholly inside or wholly outside the matrix. Loads go through
-// buffer descriptors rebased per K-slice, so rows past M (A) and past K (B)
-// read as zero from the hardware range check, and chunks past K (A) or N (B)
-// are sent to an offset beyond the descriptor's range (no branches in the
-// main loop; slices past the end load zeros).
-//
-// Schedule per K-slice it (two register sets, two LDS buffers):
-//   issue global loads of slice it + 2 into register set it % 2
-//   MFMAs of slice it from LDS buffer it % 2
-//   transpose + store slice it + 1 (register set (it + 1) % 2) to buffer (it + 1) % 2
-//   barrier
-// The loop is unrolled by two so register sets and LDS buffers are
-// compile-time indices.
-namespace vec {
-
-constexpr uint32_t kOob = 0x80000000u;  // any offset >= the descriptor range reads 0
-
-XPU_DEVICE __amdgpu_buffer_rsrc_t rsrc(const uint16_t *base, int64_t records) {
-  records = records < 0 ? 0 : (records > 0x7fffffff ? 0x7fffffff : records);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), static_cast<short>(0),
-                                           static_cast<int>(records), 0x00020000);
-}
-
-// Two FP32 values to packed 16-bit codes with the hardware conversion
-// (round to nearest even, as the reference's esimd::convert<T> store,
-// gemm_kernel.hpp:40-48); branch-free, unlike the integer codec.
 template <int DT> XPU_DEVICE uint32_t cvt_pack(float lo, float hi) {
   if constexpr (DT == kFp16)
     return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))) |
@@ -102,162 +135,127 @@ template <int DT> XPU_DEVICE uint32_t cvt_pack(float lo, float hi) {
            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
 }
 
-XPU_DEVICE u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0));
-}
-
-struct Ctx {
-  const uint16_t *A, *B;
-  uint32_t M, N, K, kb, m0, n0;
-  uint32_t a_off;     // byte offset of this thread's first A chunk within a slice
-  uint32_t b_off;     // byte offset of this thread's first B chunk (kOob + ... past N)
-  uint32_t a_stride;  // bytes between the A chunks of one thread (32 rows)
-  uint32_t b_stride;  // bytes between the B chunks of one thread (1 row)
-  uint32_t a_col;     // first column of this thread's A chunk within a slice
+template <int BK, int S> struct Cfg {
+  static constexpr uint32_t kKs = BK / 16;                  // k-steps per slice
+  static constexpr uint32_t kABytes = 512u * BK;            // 256 rows x 2 BK bytes
+  static constexpr uint32_t kStage = 2u * kABytes;          // A then B (BK rows x 512 bytes)
+  static constexpr uint32_t kCpr = BK / 8;                  // 16-byte chunks per A row
+  static constexpr uint32_t kRpi = 64 / kCpr;               // A rows per DMA instruction
+  static constexpr uint32_t kDmaA = 256 / kRpi / 4;         // A DMA instructions per wave per slice
+  static constexpr uint32_t kDmaB = BK / 2 / 4;             // B DMA instructions per wave per slice
+  static constexpr uint32_t kDma = kDmaA + kDmaB;
+  static constexpr uint32_t kEpPitch = 132;                  // epilogue staging pitch (floats)
+  static constexpr uint32_t kEpBytes = 4u * 64u * kEpPitch * 4u;
+  static constexpr uint32_t kLds = S * kStage > kEpBytes ? S * kStage : kEpBytes;
+  static_assert(kLds <= 160u * 1024u, "LDS");
 };
 
-// Loads of K-slice s: A rows a_row + 32 i, columns s*64 + a_chunk*8 .. +7;
-// B rows s*64 + b_kb*8 + i, columns n0 + b_nb*8 .. +7.
-XPU_DEVICE void issue(const Ctx &c, uint32_t s, u32x4 (&ra)[8], u32x4 (&rb)[8]) {
-  const uint64_t k0 = static_cast<uint64_t>(s) * kBK;
-  const __amdgpu_buffer_rsrc_t r_a =
-      rsrc(c.A + static_cast<uint64_t>(c.m0) * c.K + k0,
-           (static_cast<int64_t>(c.M - c.m0) * c.K - static_cast<int64_t>(k0)) * 2);
-  const __amdgpu_buffer_rsrc_t r_b =
-      rsrc(c.B + k0 * c.N + c.n0, (static_cast<int64_t>(c.kb) - static_cast<int64_t>(k0)) * c.N * 2 -
-                                      static_cast<int64_t>(c.n0) * 2);
-  const uint32_t a_base = k0 + c.a_col < c.K ? c.a_off : kOob;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ra[i] = load16(r_a, a_base + i * c.a_stride);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) rb[i] = load16(r_b, c.b_off + i * c.b_stride);
-}
-
-// A chunks as loaded ([m][k] rows); B 8 x 8 blocks transposed to [n][k].
-XPU_DEVICE void commit(uint16_t *__restrict__ la, uint16_t *__restrict__ lb, uint32_t tid,
-                       const u32x4 (&ra)[8], const u32x4 (&rb)[8]) {
-  const uint32_t a_chunk = tid & 7u, a_row = tid >> 3;
-  const uint32_t b_kb = tid & 7u, b_nb = tid >> 3;
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    *reinterpret_cast<u32x4 *>(la + (a_row + 32u * i) * kLdsPitch + a_chunk * 8u) = ra[i];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-    uint32_t w[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) w[q] = __builtin_amdgcn_perm(rb[2 * q + 1][j >> 1], rb[2 * q][j >> 1], sel);
-    *reinterpret_cast<u32x4 *>(lb + (b_nb * 8u + j) * kLdsPitch + b_kb * 8u) = u32x4{w[0], w[1], w[2], w[3]};
-  }
-}
-
-// 4 k-steps of 16 MFMAs over one LDS buffer; fragments of the next k-step
-// are read before the MFMAs of the current one.
-template <int DT>
-XPU_DEVICE void compute(const uint16_t *__restrict__ la, const uint16_t *__restrict__ lb, f32x16 (&acc)[4][4]) {
-  u32x4 fa[2][4], fb[2][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    fa[0][i] = *reinterpret_cast<const u32x4 *>(la + i * 32u * kLdsPitch);
-    fb[0][i] = *reinterpret_cast<const u32x4 *>(lb + i * 32u * kLdsPitch);
-  }
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int cur = ks & 1;
-    if (ks + 1 < 4) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        fa[cur ^ 1][i] = *reinterpret_cast<const u32x4 *>(la + i * 32u * kLdsPitch + (ks + 1) * 16);
-        fb[cur ^ 1][i] = *reinterpret_cast<const u32x4 *>(lb + i * 32u * kLdsPitch + (ks + 1) * 16);
-      }
-    }
-    // operands swapped (B^T fragment first): the accumulator tile is C^T,
-    // so each lane ends up with 4 consecutive columns of one row of C
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma<DT>(fb[cur][j], fa[cur][i], acc[i][j]);
-  }
-}
-
-// Instruction order of one K-slice step (issue + compute + commit, one
-// basic block): after the first k-step's 8 fragment reads, every MFMA is
-// paired with one other instruction - the next k-step's fragment reads,
-// the 16 global loads of slice it + 2, the 8 A-tile LDS stores and the
-// 8 transposed B stores with their v_perm_b32 - so the matrix pipe never
-// waits on an LDS round trip that could have been issued earlier.
-XPU_DEVICE void schedule_step() {
-  constexpr int kMfma = 0x008, kValu = 0x002, kVmemRead = 0x020, kDsRead = 0x100, kDsWrite = 0x200;
-  __builtin_amdgcn_sched_group_barrier(kDsRead, 8, 0);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {  // k-step 0: k-step 1 fragments, then loads 0..7
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {  // k-step 1: k-step 2 fragments, then loads 8..15
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {  // k-step 2: k-step 3 fragments, then A stores
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {  // k-step 3: B transposes and stores
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
-  }
-  __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
-}
-
-// K: reduction length (columns of A); kb: rows of B (<= K; rows kb..K-1
-// read as zero); N: columns of B; C has row stride ldc and n_out <= N valid
-// columns. C16: C rows 16-byte aligned and n_out % 8 == 0 (16-byte stores).
-template <int DT, bool C16>
+template <int DT, int BK, int S, int P, bool C16>
 XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
                      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {
-  __shared__ __align__(16) uint16_t lds[2][2][kTileElems];
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  using G = Cfg<BK, S>;
+  __shared__ __align__(1024) uint8_t lds[G::kLds];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
   const TileCoord tc = tile_of_block(blockIdx.x, tiles_m, tiles_n);
-  Ctx c;
-  c.A = A;
-  c.B = B;
-  c.M = M;
-  c.N = N;
-  c.K = K;
-  c.kb = kb;
-  c.m0 = tc.tm * kBM;
-  c.n0 = tc.tn * kBN;
+  const uint32_t m0 = tc.tm * kBM, n0 = tc.tn * kBN;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+
+  // DMA lane maps. A: instruction i of this wave fills tile rows
+  // (wave + 4 i) * kRpi .. + kRpi - 1; lane t lands in physical chunk
+  // t % kCpr of row t / kCpr and fetches the logical chunk that the swizzle
+  // puts there. B: instruction i fills rows 2 (wave + 4 i) .. + 1.
+  const uint32_t a_row = wave * G::kRpi + lane / G::kCpr;
+  const uint32_t a_chunk = (lane % G::kCpr) ^ a_swz<BK>(a_row & 15u);
+  const uint32_t a_voff = (a_row * K + a_chunk * 8u) * 2u;
+  const uint32_t a_istride = 4u * G::kRpi * K * 2u;
+  const uint32_t b_row = 2u * wave + lane / 32u;
+  const uint32_t b_chunk = (lane % 32u) ^ b_swz(b_row & 3u);
+  const uint32_t b_voff = n0 + b_chunk * 8u < N ? (b_row * N + b_chunk * 8u) * 2u : kOob;
+  const uint32_t b_istride = 8u * N * 2u;
+
+  // DMA instruction d (0 .. kDma-1) of slice s into stage st: A rows first,
+  // then B rows. Per slice the descriptors are rebased to the slice's first
+  // column (A) and row (B).
+  struct Slice {
+    i32x4 r_a, r_b;
+    uint32_t a_base, st_base;
+  };
+  auto slice_of = [&](uint32_t s, uint32_t stage) {
+    const uint64_t k0 = static_cast<uint64_t>(s) * BK;
+    Slice d;
+    d.r_a = rsrc(A + static_cast<uint64_t>(m0) * K + k0,
+                 (static_cast<int64_t>(M - m0) * K - static_cast<int64_t>(k0)) * 2);
+    d.r_b = rsrc(B + k0 * N + n0,
+                 (static_cast<int64_t>(kb) - static_cast<int64_t>(k0)) * N * 2 - static_cast<int64_t>(n0) * 2);
+    d.a_base = k0 + a_chunk * 8u < K ? a_voff : kOob;
+    d.st_base = lds0 + stage * G::kStage;
+    return d;
+  };
+  auto dma = [&](const Slice &d, uint32_t op) {
+    if (op < G::kDmaA)
+      dma16(d.st_base + (wave + 4u * op) * 1024u, d.r_a, d.a_base + op * a_istride);
+    else
+      dma16(d.st_base + G::kABytes + (wave + 4u * (op - G::kDmaA)) * 1024u, d.r_b,
+            b_voff + (op - G::kDmaA) * b_istride);
+  };
+
+  // Fragment addresses (bytes within a stage). A: row wm*128 + 32 i + l%32,
+  // logical chunk 2 ks + l/32. B: k-row 16 ks + 8 (l/32) + 4 h + (l%16)/4,
+  // column wn*128 + 32 j + 16 ((l/16) % 2) + 4 (l % 4): the 4-element row
+  // that lane l contributes to its group's transposing read.
+  const uint32_t wm = wave >> 1, wn = wave & 1u;
+  // The ds_read offset field holds 16 bits, so the stages are addressed from
+  // one base per 64 KiB group; the bases are made opaque to the compiler so
+  // that it keeps them in registers instead of materialising one register per
+  // (stage, k-step, tile) combination.
+  constexpr uint32_t kGroups = (S * G::kStage + 65535u) / 65536u;
+  uint32_t fa_base[kGroups][G::kKs], fb_base[kGroups][4];
   {
-    const uint32_t a_chunk = tid & 7u, a_row = tid >> 3;
-    const uint32_t b_kb = tid & 7u, b_nb = tid >> 3;
-    c.a_col = a_chunk * 8u;
-    // kOob + i * stride stays at or above the descriptor range limit
-    // (< 2^31) and below 2^32 for the sizes the host admits
-    c.a_off = (a_row * K + a_chunk * 8u) * 2u;
-    c.b_off = c.n0 + b_nb * 8u < N ? (b_kb * 8u * N + b_nb * 8u) * 2u : kOob;
-    c.a_stride = 64u * K;
-    c.b_stride = 2u * N;
+    const uint32_t krow = 8u * (lane >> 5) + ((lane & 15u) >> 2);
+    const uint32_t x = 2u * ((lane >> 4) & 1u) + ((lane & 3u) >> 1);
+#pragma unroll
+    for (uint32_t g = 0; g < kGroups; ++g) {
+#pragma unroll
+      for (uint32_t ks = 0; ks < G::kKs; ++ks) {
+        fa_base[g][ks] = lds0 + g * 65536u + (wm * 128u + (lane & 31u)) * (2u * BK) +
+                         16u * ((2u * ks + (lane >> 5)) ^ a_swz<BK>(lane & 15u));
+        asm volatile("" : "+v"(fa_base[g][ks]));
+      }
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) {
+        fb_base[g][j] = lds0 + g * 65536u + G::kABytes + krow * 512u +
+                        16u * (16u * wn + ((4u * j + x) ^ b_swz(krow & 3u))) + 8u * (lane & 1u);
+        asm volatile("" : "+v"(fb_base[g][j]));
+      }
+    }
   }
+
+  struct Frags {
+    u32x4 a[4], b[4];
+  };
+  // Read r (0..11) of the fragments of k-step ks in a stage, in the order
+  // the MFMAs consume them: A0, B0, B1, B2, B3 (two halves each), A1, A2, A3.
+  auto read = [&](uint32_t stage, uint32_t ks, Frags &f, uint32_t r) {
+    const uint32_t g = stage * G::kStage / 65536u, in_group = stage * G::kStage % 65536u;
+    if (r == 0 || r >= 9) {
+      const uint32_t i = r == 0 ? 0 : r - 8;
+      const uint32_t addr = fa_base[g][ks] + in_group + i * 32u * 2u * BK;
+      f.a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(addr);
+    } else {
+      const uint32_t j = (r - 1) >> 1, h = (r - 1) & 1;
+      const uint32_t addr = fb_base[g][j] + in_group + (16u * ks + 4u * h) * 512u;
+      const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(addr)));
+      if (h == 0) {
+        f.b[j].x = v.x;
+        f.b[j].y = v.y;
+      } else {
+        f.b[j].z = v.x;
+        f.b[j].w = v.y;
+      }
+    }
+  };
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -267,45 +265,84 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  const uint32_t wm = wave >> 1, wn = wave & 1u;
-  const uint32_t frag = (lane & 31u) * kLdsPitch + (lane >> 5) * 8u;
-  const uint32_t fa_off = wm * 128u * kLdsPitch + frag, fb_off = wn * 128u * kLdsPitch + frag;
-  const uint32_t nk = (K + kBK - 1) / kBK;
+  // MFMA q = 4 i + j. Operands swapped (B^T fragment first): the
+  // accumulator tile is C^T, so each lane ends up with 4 consecutive
+  // columns of one row of C.
+  auto mfma_q = [&](const Frags &f, uint32_t q) {
+    acc[q >> 2][q & 3] = mfma<DT>(f.b[q & 3], f.a[q >> 2], acc[q >> 2][q & 3]);
+  };
 
-  u32x4 ra0[8], rb0[8], ra1[8], rb1[8];
-  issue(c, 0, ra0, rb0);
-  issue(c, 1, ra1, rb1);
-  commit(lds[0][0], lds[0][1], tid, ra0, rb0);
+  const uint32_t nk = (K + BK - 1) / BK;
+  Frags frag[2];
+#pragma unroll
+  for (uint32_t p = 0; p < S; ++p) {
+    const Slice d = slice_of(p, p);
+#pragma unroll
+    for (uint32_t op = 0; op < G::kDma; ++op) dma(d, op);
+  }
+  wait_vmcnt<(S - 1) * G::kDma>();
   __syncthreads();
-  uint32_t it = 0;
-  do {  // nk >= 1 (K >= 1)
-    issue(c, it + 2, ra0, rb0);
-    compute<DT>(lds[0][0] + fa_off, lds[0][1] + fb_off, acc);
-    commit(lds[1][0], lds[1][1], tid, ra1, rb1);
-    schedule_step();
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-    // for odd nk this step runs slice nk, which loaded as zeros
-    issue(c, it + 3, ra1, rb1);
-    compute<DT>(lds[1][0] + fa_off, lds[1][1] + fb_off, acc);
-    commit(lds[0][0], lds[0][1], tid, ra0, rb0);
-    schedule_step();
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-    it += 2;
-  } while (it < nk);
+#pragma unroll
+  for (uint32_t r = 0; r < 12; ++r) read(0, 0, frag[0], r);
 
-  // Epilogue through LDS (free after the loop's last barrier), one 64-row
-  // band per round: each wave writes its 64 x 128 FP32 band (D layout of
-  // v_mfma_f32_32x32x16 with C^T tiles: lane l holds row l % 32, columns
-  // 8 g + 4 (l / 32) + 0..3 in accumulators 4 g..4 g + 3) as 16-byte rows
-  // into its own region (pitch 132 floats: the 8 rows written by 8
-  // consecutive lanes fall in distinct banks), then reads it back 8
-  // consecutive columns per lane and stores 16 bytes of C per lane.
-  constexpr uint32_t kEpPitch = 132;
-  float *ep = reinterpret_cast<float *>(&lds[0][0][0]) + wave * 64u * kEpPitch;
+  // Instruction order is fixed with sched_barrier: in an ordinary k-step
+  // each of the first 12 MFMAs is followed by one fragment read of the next
+  // k-step; in the last k-step of a slice, 8 MFMAs, then the wait and the
+  // barrier, then the 8 remaining MFMAs each followed by its share of the
+  // slice's DMA and of the next slice's first fragment reads.
+  // Whole groups of S slices (one exit keeps the accumulators in place);
+  // slices past nk read zeros and add nothing.
+  for (uint32_t s0 = 0; s0 < nk; s0 += S) {
+#pragma unroll
+    for (uint32_t st = 0; st < S; ++st) {
+#pragma unroll
+      for (uint32_t ks = 0; ks < G::kKs; ++ks) {
+        const int cur = (st * G::kKs + ks) & 1;
+        if (ks + 1 < G::kKs) {
+#pragma unroll
+          for (uint32_t q = 0; q < 16; ++q) {
+            mfma_q(frag[cur], q);
+            if (q < 12) read(st, ks + 1, frag[cur ^ 1], q);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        } else {
+#pragma unroll
+          for (uint32_t q = 0; q < P; ++q) {
+            mfma_q(frag[cur], q);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          wait_vmcnt<(S - 2) * G::kDma>();
+          __syncthreads();
+          __builtin_amdgcn_sched_barrier(0);
+          const Slice d = slice_of(s0 + st + S, st);
+          constexpr uint32_t kAfter = 16 - P;
+#pragma unroll
+          for (uint32_t q = P; q < 16; ++q) {
+            mfma_q(frag[cur], q);
+            const uint32_t x = q - P;
+#pragma unroll
+            for (uint32_t op = x * G::kDma / kAfter; op < (x + 1) * G::kDma / kAfter; ++op) dma(d, op);
+#pragma unroll
+            for (uint32_t r = x * 12 / kAfter; r < (x + 1) * 12 / kAfter; ++r) read((st + 1) % S, 0, frag[cur ^ 1], r);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+    }
+  }
+  // drain the DMA of slices past the end (they read zeros) before the
+  // epilogue reuses the LDS
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  // Epilogue through LDS, one 64-row band per round: each wave writes its
+  // 64 x 128 FP32 band (D layout of v_mfma_f32_32x32x16 with C^T tiles: lane
+  // l holds row l % 32, columns 8 g + 4 (l / 32) + 0..3 in accumulators
+  // 4 g..4 g + 3) as 16-byte rows into its own region (pitch 132 floats),
+  // then reads it back 8 consecutive columns per lane and stores 16 bytes of
+  // C per lane.
+  constexpr uint32_t kEpPitch = G::kEpPitch;
+  float *ep = reinterpret_cast<float *>(lds) + wave * 64u * kEpPitch;
   const uint32_t m_lane = lane & 31u, n_lane = (lane >> 5) * 4u;
   const uint32_t r_lane = lane >> 4, c_lane = (lane & 15u) * 8u;
 #pragma unroll
@@ -328,7 +365,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
       const uint32_t r = rr * 4u + r_lane;
       const f32x4 lo = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane);
       const f32x4 hi = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane + 4u);
-      const uint32_t m = c.m0 + wm * 128u + band * 64u + r, n = c.n0 + wn * 128u + c_lane;
+      const uint32_t m = m0 + wm * 128u + band * 64u + r, n = n0 + wn * 128u + c_lane;
       if (m >= M || n >= n_out) continue;
       const u32x4 packed{cvt_pack<DT>(lo.x, lo.y), cvt_pack<DT>(lo.z, lo.w), cvt_pack<DT>(hi.x, hi.y),
                          cvt_pack<DT>(hi.z, hi.w)};
@@ -348,21 +385,21 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   }
 }
 
-}  // namespace vec
-
+}  // namespace dma
 }  // namespace xpu
 
-#define XPU_GEMM_VEC_VARIANT(NAME, DT, C16)                                                    \
+#define XPU_GEMM_DMA_VARIANT(NAME, DT, BK, S, P, C16)                                             \
   extern "C" __global__ __launch_bounds__(256, 1) void NAME(                                  \
       const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C, \
       uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {         \
-    xpu::vec::body<DT, C16>(A, B, C, M, N, K, kb, ldc, n_out);                                 \
+    xpu::dma::body<DT, BK, S, P, C16>(A, B, C, M, N, K, kb, ldc, n_out);                          \
   }
 
-XPU_GEMM_VEC_VARIANT(xpu_gemm_bf16_vec, xpu::kBf16, true)
-XPU_GEMM_VEC_VARIANT(xpu_gemm_fp16_vec, xpu::kFp16, true)
-XPU_GEMM_VEC_VARIANT(xpu_gemm_bf16_vecu, xpu::kBf16, false)
-XPU_GEMM_VEC_VARIANT(xpu_gemm_fp16_vecu, xpu::kFp16, false)
+// BK = 64, two stages, barrier at the start of a slice's last k-step (P = 0)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dma, xpu::kBf16, 64, 2, 0, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dma, xpu::kFp16, 64, 2, 0, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dmau, xpu::kBf16, 64, 2, 0, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dmau, xpu::kFp16, 64, 2, 0, false)
 
 // dst[r][c] = src[r * src_ld + c] for c < cols, 0 for cols <= c < dst_cols
 // (dst_cols % 8 == 0, dst 16-byte aligned): the zero padding of the
