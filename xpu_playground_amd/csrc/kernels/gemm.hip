@@ -23,11 +23,11 @@
 // Pipeline (slice s in stage s % S): the DMA of slice s + S is issued right
 // after the barrier that publishes slice s + 1, into the stage slice s just
 // vacated; that barrier sits in slice s's last k-step after the first P of
-// its 16 MFMAs (P = 0 in the kernels built here: the slice's DMA and the
-// next slice's first fragment reads then spread over all 16), and is
-// preceded by a vmcnt wait that leaves the DMA of slices s + 2 .. s + S - 1
-// in flight. Fragments of the next k-step are read while the current one's
-// MFMAs run.
+// its 16 MFMAs and is preceded by a vmcnt wait that leaves the DMA of slices
+// s + 2 .. s + S - 1 in flight. A slice's DMA is spread over the D k-steps
+// from its barrier on (D = 2 leaves the last of it more than two k-steps to
+// land). Fragments of the next k-step are read while the current one's MFMAs
+// run.
 //
 // Edges: loads past row M of A and past row K of B read zero through the
 // buffer range check; 16-byte chunks past column K of A or N of B are sent
@@ -150,7 +150,7 @@ template <int BK, int S> struct Cfg {
   static_assert(kLds <= 160u * 1024u, "LDS");
 };
 
-template <int DT, int BK, int S, int P, bool C16>
+template <int DT, int BK, int S, int P, int D, bool C16>
 XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
                      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {
   using G = Cfg<BK, S>;
@@ -273,23 +273,37 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   };
 
   const uint32_t nk = (K + BK - 1) / BK;
-  Frags frag[2];
+  static_assert(D >= 1 && D <= G::kKs, "a slice's DMA is issued within the k-steps before the next barrier");
+  // DMA ops of one slice issued during the e-th k-step after its barrier
+  auto dma_part = [&](const Slice &d, uint32_t e, uint32_t x, uint32_t nx) {
+    const uint32_t lo = e * G::kDma / D, hi = (e + 1) * G::kDma / D;
 #pragma unroll
-  for (uint32_t p = 0; p < S; ++p) {
+    for (uint32_t op = lo + x * (hi - lo) / nx; op < lo + (x + 1) * (hi - lo) / nx; ++op) dma(d, op);
+  };
+  Frags frag[2];
+  // Prologue: slices 0 .. S-2 whole, and the first part of slice S-1 as if
+  // its barrier had just passed; the rest of slice S-1 follows during slice
+  // 0 like any slice's DMA.
+#pragma unroll
+  for (uint32_t p = 0; p + 1 < S; ++p) {
     const Slice d = slice_of(p, p);
 #pragma unroll
     for (uint32_t op = 0; op < G::kDma; ++op) dma(d, op);
   }
-  wait_vmcnt<(S - 1) * G::kDma>();
+  Slice pend = slice_of(S - 1, S - 1);
+  dma_part(pend, 0, 0, 1);
+  wait_vmcnt<(S - 2) * G::kDma + G::kDma / D>();
   __syncthreads();
 #pragma unroll
   for (uint32_t r = 0; r < 12; ++r) read(0, 0, frag[0], r);
 
-  // Instruction order is fixed with sched_barrier: in an ordinary k-step
-  // each of the first 12 MFMAs is followed by one fragment read of the next
-  // k-step; in the last k-step of a slice, 8 MFMAs, then the wait and the
-  // barrier, then the 8 remaining MFMAs each followed by its share of the
-  // slice's DMA and of the next slice's first fragment reads.
+  // Instruction order is fixed with sched_barrier. Ordinary k-step: each of
+  // the first 12 MFMAs is followed by one fragment read of the next k-step,
+  // and the pending slice's DMA share of this k-step is spread over the 16.
+  // Last k-step of a slice: P MFMAs, the wait and the barrier, then the
+  // remaining MFMAs with the next slice's first fragment reads and the first
+  // share of the new slice's DMA (the DMA of a slice is spread over the D
+  // k-steps from its barrier on).
   // Whole groups of S slices (one exit keeps the accumulators in place);
   // slices past nk read zeros and add nothing.
   for (uint32_t s0 = 0; s0 < nk; s0 += S) {
@@ -299,10 +313,12 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
       for (uint32_t ks = 0; ks < G::kKs; ++ks) {
         const int cur = (st * G::kKs + ks) & 1;
         if (ks + 1 < G::kKs) {
+          const uint32_t e = ks + 1;  // k-steps since the pending slice's barrier
 #pragma unroll
           for (uint32_t q = 0; q < 16; ++q) {
             mfma_q(frag[cur], q);
             if (q < 12) read(st, ks + 1, frag[cur ^ 1], q);
+            if (e < D) dma_part(pend, e, q, 16);
             __builtin_amdgcn_sched_barrier(0);
           }
         } else {
@@ -314,14 +330,13 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
           wait_vmcnt<(S - 2) * G::kDma>();
           __syncthreads();
           __builtin_amdgcn_sched_barrier(0);
-          const Slice d = slice_of(s0 + st + S, st);
+          pend = slice_of(s0 + st + S, st);
           constexpr uint32_t kAfter = 16 - P;
 #pragma unroll
           for (uint32_t q = P; q < 16; ++q) {
             mfma_q(frag[cur], q);
             const uint32_t x = q - P;
-#pragma unroll
-            for (uint32_t op = x * G::kDma / kAfter; op < (x + 1) * G::kDma / kAfter; ++op) dma(d, op);
+            dma_part(pend, 0, x, kAfter);
 #pragma unroll
             for (uint32_t r = x * 12 / kAfter; r < (x + 1) * 12 / kAfter; ++r) read((st + 1) % S, 0, frag[cur ^ 1], r);
             __builtin_amdgcn_sched_barrier(0);
@@ -388,18 +403,19 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 }  // namespace dma
 }  // namespace xpu
 
-#define XPU_GEMM_DMA_VARIANT(NAME, DT, BK, S, P, C16)                                             \
+#define XPU_GEMM_DMA_VARIANT(NAME, DT, BK, S, P, D, C16)                                             \
   extern "C" __global__ __launch_bounds__(256, 1) void NAME(                                  \
       const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C, \
       uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {         \
-    xpu::dma::body<DT, BK, S, P, C16>(A, B, C, M, N, K, kb, ldc, n_out);                          \
+    xpu::dma::body<DT, BK, S, P, D, C16>(A, B, C, M, N, K, kb, ldc, n_out);                          \
   }
 
-// BK = 64, two stages, barrier at the start of a slice's last k-step (P = 0)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dma, xpu::kBf16, 64, 2, 0, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dma, xpu::kFp16, 64, 2, 0, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dmau, xpu::kBf16, 64, 2, 0, false)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dmau, xpu::kFp16, 64, 2, 0, false)
+// BK = 64, two stages, barrier after 4 MFMAs of a slice's last k-step, each
+// slice's DMA spread over two k-steps
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dma, xpu::kBf16, 64, 2, 4, 2, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dma, xpu::kFp16, 64, 2, 4, 2, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dmau, xpu::kBf16, 64, 2, 4, 2, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dmau, xpu::kFp16, 64, 2, 4, 2, false)
 
 // dst[r][c] = src[r * src_ld + c] for c < cols, 0 for cols <= c < dst_cols
 // (dst_cols % 8 == 0, dst 16-byte aligned): the zero padding of the
