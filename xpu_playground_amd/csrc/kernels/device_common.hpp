@@ -86,12 +86,50 @@ XPU_DEVICE float fold8(const float (&a)[8]) {
   return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
 }
 
-// xor-butterfly over the 64 lanes of a wavefront; every lane ends with the
-// same value because IEEE addition is commutative.
-XPU_DEVICE float wave_butterfly(float s) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) s = s + __shfl_xor(s, m, 64);
+XPU_DEVICE uint32_t lane_id() { return threadIdx.x & 63u; }
+
+// Cross-lane exchanges for a full wavefront (all 64 lanes active), without
+// LDS round trips. DPP row_ror:8 moves the value of lane l ^ 8 (rotation by
+// 8 within each 16-lane row); quad_perm [2,3,0,1] and [1,0,3,2] move lanes
+// l ^ 2 and l ^ 1. gfx950 v_permlane32_swap / v_permlane16_swap of a value
+// with itself return (own, partner of lane l ^ 32) in the lower half and
+// (partner, own) in the upper half (likewise for rows of 16 with l ^ 16).
+template <int CTRL> XPU_DEVICE uint32_t dpp_u(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL> XPU_DEVICE float dpp_f(float v) {
+  return __builtin_bit_cast(float, dpp_u<CTRL>(__builtin_bit_cast(uint32_t, v)));
+}
+XPU_DEVICE uint32_t xor32_u(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (lane_id() & 32u) ? r[0] : r[1];
+}
+XPU_DEVICE uint32_t xor16_u(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (lane_id() & 16u) ? r[0] : r[1];
+}
+XPU_DEVICE float xor32_f(float v) { return __builtin_bit_cast(float, xor32_u(__builtin_bit_cast(uint32_t, v))); }
+XPU_DEVICE float xor16_f(float v) { return __builtin_bit_cast(float, xor16_u(__builtin_bit_cast(uint32_t, v))); }
+XPU_DEVICE float xor8_f(float v) { return dpp_f<0x128>(v); }  // row_ror:8
+
+// Butterfly reduction op(own, partner) with partners l ^ 32, 16, 8, 4, 2, 1
+// in that order; every lane ends with the same value. At the l ^ 4 step the
+// values depend on l % 8 only, so row_ror:4 (lane (l + 4) % 16 of the row)
+// supplies the l ^ 4 value.
+template <typename Op> XPU_DEVICE float wave_reduce(float s, Op op) {
+  s = op(s, xor32_f(s));
+  s = op(s, xor16_f(s));
+  s = op(s, xor8_f(s));
+  s = op(s, dpp_f<0x124>(s));  // row_ror:4
+  s = op(s, dpp_f<0x4E>(s));   // quad_perm [2,3,0,1]
+  s = op(s, dpp_f<0xB1>(s));   // quad_perm [1,0,3,2]
   return s;
+}
+
+// xor-butterfly sum over the 64 lanes of a wavefront (s + partner for
+// partners l ^ 32, 16, 8, 4, 2, 1); every lane ends with the same value.
+XPU_DEVICE float wave_butterfly(float s) {
+  return wave_reduce(s, [](float a, float b) { return a + b; });
 }
 
 // exp: Cody-Waite reduction and degree-7 Taylor polynomial, the same
@@ -122,7 +160,5 @@ XPU_DEVICE float canonical_exp(float x) {
 XPU_DEVICE u32x4 load_nt16(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 }
-
-XPU_DEVICE uint32_t lane_id() { return threadIdx.x & 63u; }
 
 }  // namespace xpu

@@ -132,7 +132,7 @@ XPU_DEVICE void head_norm_rope(const uint16_t *src, const uint16_t *__restrict__
     n[e] = active ? round_bf16(bf16_to_f32(w[i]) * round_bf16(x[e] * scale)) : 0.0f;
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(n[e], 8, 64);
+  for (int e = 0; e < 8; ++e) p[e] = xor8_f(n[e]);
   if (active) {
     uint32_t codes[8], ncodes[8];
 #pragma unroll
@@ -157,9 +157,10 @@ XPU_DEVICE void head_norm_rope(const uint16_t *src, const uint16_t *__restrict__
 // head_norm_rope with the lane's operands already loaded (lanes 0..15:
 // elements 8 l..8 l + 7 of the head row, the norm weight, cos and sin rows;
 // other lanes ignored), so the caller can issue those loads early. Same
-// operations in the same order; writes the roped row only.
+// operations in the same order; writes the roped row only, lane l's eight
+// codes at roped_out + l * out_chunk.
 XPU_DEVICE void head_norm_rope_vec(const u32x4 &xv, const u32x4 &wv, const u32x4 &cv, const u32x4 &sv,
-                                   float eps, uint16_t *roped_out) {
+                                   float eps, uint16_t *roped_out, uint64_t out_chunk = 8) {
   const uint32_t lane = lane_id();
   const bool active = lane < 16;
   float x[8], wf[8];
@@ -178,7 +179,7 @@ XPU_DEVICE void head_norm_rope_vec(const u32x4 &xv, const u32x4 &wv, const u32x4
 #pragma unroll
   for (int e = 0; e < 8; ++e) n[e] = active ? round_bf16(wf[e] * round_bf16(x[e] * scale)) : 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(n[e], 8, 64);
+  for (int e = 0; e < 8; ++e) p[e] = xor8_f(n[e]);
   if (active) {
     float cf[8], sf[8];
     unpack8<kBf16>(cv, cf);
@@ -191,15 +192,14 @@ XPU_DEVICE void head_norm_rope_vec(const u32x4 &xv, const u32x4 &wv, const u32x4
       const float b = round_bf16(rot * sf[e]);
       codes[e] = f32_to_bf16(a + b);
     }
-    *reinterpret_cast<u32x4 *>(roped_out + lane * 8u) =
+    *reinterpret_cast<u32x4 *>(roped_out + lane * out_chunk) =
         u32x4{codes[0] | (codes[1] << 16), codes[2] | (codes[3] << 16), codes[4] | (codes[5] << 16),
               codes[6] | (codes[7] << 16)};
   }
 }
 
 XPU_DEVICE float block_max(float v, float *red) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  v = wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
   const uint32_t wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
   __syncthreads();
   if (lane_id() == 0) red[wave] = v;
@@ -227,47 +227,62 @@ XPU_DEVICE float attention_score_regs(const uint16_t *qs, const u32x4 (&kv)[16],
   return round_bf16(round_bf16(fold8(acc)) * scale);
 }
 
-XPU_DEVICE void load_head_row(const uint16_t *row, u32x4 (&r)[16]) {
+// The 16 eight-element chunks of a 128-wide head row; chunk j at row + j * chunk
+// (8 for a contiguous row).
+XPU_DEVICE void load_head_row(const uint16_t *row, u32x4 (&r)[16], uint64_t chunk = 8) {
 #pragma unroll
-  for (int j = 0; j < 16; ++j) r[j] = *reinterpret_cast<const u32x4 *>(row + j * 8);
+  for (int j = 0; j < 16; ++j) r[j] = *reinterpret_cast<const u32x4 *>(row + j * chunk);
 }
 
-XPU_DEVICE float attention_score(const uint16_t *qs, const uint16_t *krow, float scale) {
+XPU_DEVICE float attention_score(const uint16_t *qs, const uint16_t *krow, float scale, uint64_t chunk = 8) {
   u32x4 kv[16];
-  load_head_row(krow, kv);
+  load_head_row(krow, kv, chunk);
   return attention_score_regs(qs, kv, scale);
 }
+
+// Cache addressing of one kv head: K row t chunk j at kbase + t * kstride +
+// j * kchunk, V row t at vbase + t * vstride (contiguous). The reference
+// layout [position][kv_head][128] has kstride = vstride = kv_heads * 128,
+// kchunk = 8; the engine's K cache is chunk-major [kv_head][16][max_seq][8]
+// (kstride = 8, kchunk = max_seq * 8: the chunk j of consecutive positions
+// is contiguous, so a lane-per-position read is coalesced) and its V cache
+// head-major [kv_head][max_seq][128] (vstride = 128).
+struct KvLayout {
+  uint64_t kstride, kchunk, vstride;
+};
 
 constexpr uint32_t kAttnTile = 256;             // positions per V tile in LDS
 constexpr uint32_t kVPitch = kHeadDim + 8;      // LDS row pitch of the V tile (bank spread)
 
 // Single-query attention of one head with a 256-thread block
-// (qwen3/kernels.hpp:157-192): positions 0..n-1, row t of K/V at
-// kbase/vbase + t * stride, except that when HAS_CURRENT the last position
-// reads kcur/vcur (the new token, not yet visible in the cache).
+// (qwen3/kernels.hpp:157-192): positions 0..n-1, rows of K/V addressed by
+// kbase/vbase and the layout lay, except that when HAS_CURRENT the last
+// position reads kcur/vcur (the new token, contiguous rows not yet visible in
+// the cache).
 // p_t = bf16(exp(s_t - max) * (1 / sum_t exp)), out = bf16(sum_t p_t v_t).
 // sbuf: kAttnChunk floats of LDS; vtile: kAttnTile * kVPitch codes of LDS;
 // red: >= 4*128 floats of LDS. Position t is handled by thread t % 256 in
 // the score pass; V rows go through vtile so that the P.V pass reads LDS.
 template <bool HAS_CURRENT>
 XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const uint16_t *vbase,
-                               uint64_t stride, uint32_t n, const uint16_t *kcur,
+                               KvLayout lay, uint32_t n, const uint16_t *kcur,
                                const uint16_t *vcur, float scale, uint16_t *out, float *sbuf,
                                uint16_t *vtile, float *red, float local_max);
 
 template <bool HAS_CURRENT>
 XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const uint16_t *vbase,
-                               uint64_t stride, uint32_t n, const uint16_t *kcur,
+                               KvLayout lay, uint32_t n, const uint16_t *kcur,
                                const uint16_t *vcur, float scale, uint16_t *out, float *sbuf,
                                uint16_t *vtile, float *red) {
   const uint32_t tid = threadIdx.x;
   const uint32_t nchunks = (n + kAttnChunk - 1) / kAttnChunk;
   const bool single_tile = n <= kAttnTile;
-  auto krow_of = [&](uint32_t t) -> const uint16_t * {
-    return (HAS_CURRENT && t + 1 == n) ? kcur : kbase + static_cast<uint64_t>(t) * stride;
+  auto score_of = [&](uint32_t t) -> float {
+    if (HAS_CURRENT && t + 1 == n) return attention_score(qs, kcur, scale);
+    return attention_score(qs, kbase + static_cast<uint64_t>(t) * lay.kstride, scale, lay.kchunk);
   };
   auto vrow_of = [&](uint32_t t) -> const uint16_t * {
-    return (HAS_CURRENT && t + 1 == n) ? vcur : vbase + static_cast<uint64_t>(t) * stride;
+    return (HAS_CURRENT && t + 1 == n) ? vcur : vbase + static_cast<uint64_t>(t) * lay.vstride;
   };
   auto stage_v_row = [&](uint32_t t, uint32_t slot) {
     const uint16_t *src = vrow_of(t);
@@ -284,13 +299,13 @@ XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const 
     const uint32_t base = c * kAttnChunk;
     const uint32_t len = min(kAttnChunk, n - base);
     for (uint32_t i = tid; i < len; i += blockDim.x) {
-      const float s = attention_score(qs, krow_of(base + i), scale);
+      const float s = score_of(base + i);
       if (single_tile) stage_v_row(base + i, i);
       sbuf[i] = s;
       local_max = fmaxf(local_max, s);
     }
   }
-  attention_tail<HAS_CURRENT>(qs, kbase, vbase, stride, n, kcur, vcur, scale, out, sbuf, vtile, red, local_max);
+  attention_tail<HAS_CURRENT>(qs, kbase, vbase, lay, n, kcur, vcur, scale, out, sbuf, vtile, red, local_max);
 }
 
 // Passes 2 and 3 of attention_head, after the scores (sbuf, when one chunk
@@ -298,17 +313,18 @@ XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const 
 // thread's running max are in place.
 template <bool HAS_CURRENT>
 XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const uint16_t *vbase,
-                               uint64_t stride, uint32_t n, const uint16_t *kcur,
+                               KvLayout lay, uint32_t n, const uint16_t *kcur,
                                const uint16_t *vcur, float scale, uint16_t *out, float *sbuf,
                                uint16_t *vtile, float *red, float local_max) {
   const uint32_t tid = threadIdx.x;
   const uint32_t nchunks = (n + kAttnChunk - 1) / kAttnChunk;
   const bool single_tile = n <= kAttnTile;
-  auto krow_of = [&](uint32_t t) -> const uint16_t * {
-    return (HAS_CURRENT && t + 1 == n) ? kcur : kbase + static_cast<uint64_t>(t) * stride;
+  auto score_of = [&](uint32_t t) -> float {
+    if (HAS_CURRENT && t + 1 == n) return attention_score(qs, kcur, scale);
+    return attention_score(qs, kbase + static_cast<uint64_t>(t) * lay.kstride, scale, lay.kchunk);
   };
   auto vrow_of = [&](uint32_t t) -> const uint16_t * {
-    return (HAS_CURRENT && t + 1 == n) ? vcur : vbase + static_cast<uint64_t>(t) * stride;
+    return (HAS_CURRENT && t + 1 == n) ? vcur : vbase + static_cast<uint64_t>(t) * lay.vstride;
   };
   auto stage_v_row = [&](uint32_t t, uint32_t slot) {
     const uint16_t *src = vrow_of(t);
@@ -325,7 +341,7 @@ XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const 
     const uint32_t base = c * kAttnChunk;
     const uint32_t len = min(kAttnChunk, n - base);
     for (uint32_t i = tid; i < len; i += blockDim.x) {
-      const float s = nchunks == 1 ? sbuf[i] : attention_score(qs, krow_of(base + i), scale);
+      const float s = nchunks == 1 ? sbuf[i] : score_of(base + i);
       sbuf[i] = canonical_exp(s - mx);
     }
     __syncthreads();
@@ -355,7 +371,7 @@ XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const 
     const uint32_t len = min(kAttnChunk, n - base);
     for (uint32_t i = tid; i < len; i += blockDim.x) {
       const float e = nchunks == 1 ? sbuf[i]
-                                   : canonical_exp(attention_score(qs, krow_of(base + i), scale) - mx);
+                                   : canonical_exp(score_of(base + i) - mx);
       sbuf[i] = round_bf16(e * inv);
     }
     __syncthreads();
@@ -446,8 +462,8 @@ XPU_DEVICE void attention_tail_short(uint32_t n, uint16_t *out, float *sbuf, flo
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float tot = 0.0f + part[e];
-    const float pair = tot + __shfl_xor(tot, 16, 64);   // (c0 + c1), (c2 + c3)
-    sum[e] = pair + __shfl_xor(pair, 32, 64);           // (c0 + c1) + (c2 + c3)
+    const float pair = tot + xor16_f(tot);   // (c0 + c1), (c2 + c3)
+    sum[e] = pair + xor32_f(pair);           // (c0 + c1) + (c2 + c3)
   }
   __syncthreads();  // everyone has read red[0]
   if (lane < 16) {
@@ -476,13 +492,19 @@ XPU_DEVICE bool finite_f(float v) { return v == v && v != __builtin_inff() && v 
 // thread 0. red needs 3 * (blockDim/64) words of LDS.
 XPU_DEVICE void block_argmax(float &v, uint32_t &i, uint32_t &bad, float *redv, uint32_t *redi,
                              uint32_t *redb) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const float ov = __shfl_xor(v, m, 64);
-    const uint32_t oi = __shfl_xor(i, m, 64);
-    bad |= __shfl_xor(bad, m, 64);
+  // partners l ^ 32, 16, 8, then lanes with equal l % 8 hold equal pairs, so
+  // row_ror:4 and the quad permutations complete the butterfly (the merge
+  // is symmetric)
+  auto step = [&](float ov, uint32_t oi, uint32_t ob) {
+    bad |= ob;
     argmax_merge(v, i, ov, oi);
-  }
+  };
+  step(xor32_f(v), xor32_u(i), xor32_u(bad));
+  step(xor16_f(v), xor16_u(i), xor16_u(bad));
+  step(xor8_f(v), dpp_u<0x128>(i), dpp_u<0x128>(bad));
+  step(dpp_f<0x124>(v), dpp_u<0x124>(i), dpp_u<0x124>(bad));
+  step(dpp_f<0x4E>(v), dpp_u<0x4E>(i), dpp_u<0x4E>(bad));
+  step(dpp_f<0xB1>(v), dpp_u<0xB1>(i), dpp_u<0xB1>(bad));
   const uint32_t wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
   __syncthreads();
   if (lane_id() == 0) {

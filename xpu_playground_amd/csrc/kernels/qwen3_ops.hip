@@ -16,8 +16,9 @@
 //   xpu_q3_norm_gemv_logits final RMSNorm + tied lm_head + per-block argmax
 //   xpu_q3_argmax_finish    argmax, next token, position advance
 // The decode position and token live in device memory (state[0], state[1])
-// so one captured graph serves every step. Engine KV caches are head-major
-// [kv_head][max_seq][128].
+// so one captured graph serves every step. Engine caches: K chunk-major
+// [kv_head][16][max_seq][8] (eight-element chunk j of every position
+// contiguous), V head-major [kv_head][max_seq][128].
 #include "qwen3_core.hpp"
 
 using xpu::u32x4;
@@ -111,7 +112,7 @@ extern "C" __global__ __launch_bounds__(256) void QwenAttention(
   __syncthreads();
   const uint64_t stride = static_cast<uint64_t>(kv_heads) * xpu::kHeadDim;
   xpu::attention_head<false>(qs, key_cache + kv * xpu::kHeadDim, value_cache + kv * xpu::kHeadDim,
-                             stride, position + 1, nullptr, nullptr, 0.08838834764831845f,
+                             xpu::KvLayout{stride, 8, stride}, position + 1, nullptr, nullptr, 0.08838834764831845f,
                              output + head * xpu::kHeadDim, sbuf, vtile, red);
 }
 
@@ -343,7 +344,7 @@ XPU_Q3_LOGITS(_r2, 2, 2)
 XPU_Q3_LOGITS(_r4, 4, 2)
 
 // One block per query head: QK-norm + RoPE of q and of its kv head's k; the
-// first query head of each group writes k and v into the head-major cache at
+// first query head of each group writes k and v into the engine caches at
 // position state[0]; then attention over positions 0..state[0].
 extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
     const uint16_t *__restrict__ qkv, const uint16_t *__restrict__ qnorm_w,
@@ -368,6 +369,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   const uint16_t *vsrc = qkv + (heads + kv_heads + kv) * xpu::kHeadDim;
   const uint32_t wave = threadIdx.x >> 6, tid = threadIdx.x;
   const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
+  const uint64_t kchunk = static_cast<uint64_t>(max_seq) * 8u;  // chunk-major K cache
   const uint32_t n = pos + 1;
   // Up to kAttnTile positions, thread t owns position t: its cached K and V
   // rows (t < pos; written by earlier steps) are loaded before the QK-norm /
@@ -386,7 +388,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   // layout of attention_tail_short (the current position's v from qkv)
   u32x4 krow[16], vpv[xpu::kAttnTile / 16];
   if (short_ctx) {
-    if (tid < pos) xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(tid) * xpu::kHeadDim, krow);
+    if (tid < pos) xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(tid) * 8u, krow, kchunk);
     const uint32_t cls = wave * 4u + (lane >> 4), dim0 = (lane & 15u) * 8u;
 #pragma unroll
     for (int it = 0; it < static_cast<int>(xpu::kAttnTile / 16); ++it) {
@@ -402,12 +404,12 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   if (wave < 2) xpu::head_norm_rope_vec(hx, hw, hc, hs, eps, wave == 0 ? qs : ks);
   __syncthreads();
   if (head % group == 0 && tid < xpu::kHeadDim) {
-    const uint64_t slot = head_base + static_cast<uint64_t>(pos) * xpu::kHeadDim + tid;
-    kcache[slot] = ks[tid];
-    vcache[slot] = vsrc[tid];
+    kcache[head_base + (tid >> 3) * kchunk + static_cast<uint64_t>(pos) * 8u + (tid & 7u)] = ks[tid];
+    vcache[head_base + static_cast<uint64_t>(pos) * xpu::kHeadDim + tid] = vsrc[tid];
   }
   if (!short_ctx) {
-    xpu::attention_head<true>(qs, kcache + head_base, vcache + head_base, xpu::kHeadDim, n, ks, vsrc,
+    xpu::attention_head<true>(qs, kcache + head_base, vcache + head_base,
+                              xpu::KvLayout{8u, kchunk, xpu::kHeadDim}, n, ks, vsrc,
                               scale, out + head * xpu::kHeadDim, sbuf, vtile, red);
     return;
   }
@@ -618,7 +620,7 @@ XPU_Q3_PF_GEMV(2, 2, 8)
 
 // QK-norm + RoPE of every token of the chunk: block (h, t), one wavefront.
 // h < heads: roped q of head h into Q[t]; else kv head h - heads: roped k
-// and the v row into the head-major caches at position p0 + t.
+// and the v row into the engine caches at position p0 + t.
 extern "C" __global__ __launch_bounds__(64) void xpu_q3_pf_rope_cache(
     const uint16_t *__restrict__ QKV, const uint16_t *__restrict__ qnorm_w, const uint16_t *__restrict__ knorm_w,
     const uint16_t *__restrict__ rope_cos, const uint16_t *__restrict__ rope_sin, uint16_t *__restrict__ kcache,
@@ -638,8 +640,10 @@ extern "C" __global__ __launch_bounds__(64) void xpu_q3_pf_rope_cache(
     hs = *reinterpret_cast<const u32x4 *>(rope_sin + static_cast<uint64_t>(pos) * xpu::kHeadDim + lane * 8u);
   }
   const uint64_t slot = (static_cast<uint64_t>(kvh) * max_seq + pos) * xpu::kHeadDim;
-  uint16_t *dst = is_q ? Q + static_cast<uint64_t>(t) * heads * xpu::kHeadDim + h * xpu::kHeadDim : kcache + slot;
-  xpu::head_norm_rope_vec(hx, hw, hc, hs, eps, dst);
+  // K: chunk-major [kv_head][16][max_seq][8]
+  const uint64_t kslot = static_cast<uint64_t>(kvh) * max_seq * xpu::kHeadDim + static_cast<uint64_t>(pos) * 8u;
+  uint16_t *dst = is_q ? Q + static_cast<uint64_t>(t) * heads * xpu::kHeadDim + h * xpu::kHeadDim : kcache + kslot;
+  xpu::head_norm_rope_vec(hx, hw, hc, hs, eps, dst, is_q ? 8u : static_cast<uint64_t>(max_seq) * 8u);
   if (!is_q && lane < 16) {
     const uint16_t *vsrc = row + (heads + kv_heads + kvh) * xpu::kHeadDim;
     *reinterpret_cast<u32x4 *>(vcache + slot + lane * 8u) = *reinterpret_cast<const u32x4 *>(vsrc + lane * 8u);
@@ -662,6 +666,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_attention(
   if (threadIdx.x < xpu::kHeadDim) qs[threadIdx.x] = Q[qoff + threadIdx.x];
   __syncthreads();
   const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
-  xpu::attention_head<false>(qs, kcache + head_base, vcache + head_base, xpu::kHeadDim, p0 + t + 1, nullptr,
+  xpu::attention_head<false>(qs, kcache + head_base, vcache + head_base,
+                             xpu::KvLayout{8u, static_cast<uint64_t>(max_seq) * 8u, xpu::kHeadDim}, p0 + t + 1, nullptr,
                              nullptr, scale, A + qoff, sbuf, vtile, red);
 }

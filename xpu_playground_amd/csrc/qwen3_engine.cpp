@@ -11,8 +11,9 @@
 // Memory layout (one arena, 4 KiB aligned tensors as in model.cpp:481-491):
 // per layer [q; k; v] projection (rows q then k then v), o_proj, [gate; up]
 // (2I x H), down_proj, the four norm gains; then embed_tokens, the final norm
-// and, when untied, lm_head. KV caches [layer][kv_head][max_seq][128] bf16
-// (the reference-mode kernels use [layer][max_seq][kv_head][128]).
+// and, when untied, lm_head. KV caches bf16: K [layer][kv_head][16][max_seq][8]
+// (chunk-major), V [layer][kv_head][max_seq][128] (the reference-mode
+// kernels use [layer][max_seq][kv_head][128] for both).
 #include "../../include/xpu_qwen3.h"
 #include "../../include/xpu_kernels.h"
 #include "host_common.hpp"
