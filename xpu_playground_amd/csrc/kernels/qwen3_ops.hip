@@ -343,6 +343,268 @@ XPU_Q3_SWIGLU(_r4, 4, 2)
 XPU_Q3_LOGITS(_r2, 2, 2)
 XPU_Q3_LOGITS(_r4, 4, 2)
 
+// ---- register-vector forms of the four fused GEMVs
+//
+// For K <= 512 NC: lane l of every wavefront holds elements 512 c + 8 l ..
+// 512 c + 8 l + 7 of the input vector in xv[c] (zeros past K), which are
+// exactly the elements it multiplies in the canonical GEMV order, and which
+// are also the canonical (lane, slot, chunk) layout of the RMSNorm sum of
+// squares. So each wavefront loads its vector slices from global memory
+// (the same addresses in every wavefront, served by the caches) and, for
+// the norm kernels, computes the RMSNorm scale and the normed codes in
+// registers: no LDS staging and no block barriers. Same operations in the
+// same order as block_rmsnorm_vec and gemv_rows_first. The vector loads are
+// issued first, then the first batch of weight rows (rows past the end are
+// clamped and discarded), so the weight latency overlaps the norm.
+namespace {
+
+template <int NC>
+XPU_DEVICE void load_slices(const uint16_t *__restrict__ v, uint32_t K, u32x4 (&xv)[NC]) {
+  const uint32_t lane = xpu::lane_id();
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const uint32_t col = c * 512u + lane * 8u;
+    xv[c] = col < K ? *reinterpret_cast<const u32x4 *>(v + col) : u32x4{0, 0, 0, 0};
+  }
+}
+
+// xv <- codes of bf16(w * bf16(x * (1 / sqrt(sum(x^2) / K + eps))))
+template <int NC>
+XPU_DEVICE void rmsnorm_slices(u32x4 (&xv)[NC], const u32x4 (&wv)[NC], uint32_t K, float eps) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float f[8];
+    xpu::unpack8<xpu::kBf16>(xv[c], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(f[e], f[e], acc[e]);
+  }
+  const float ss = xpu::wave_butterfly(xpu::fold8(acc));
+  const float scale = 1.0f / __builtin_sqrtf(ss / static_cast<float>(K) + eps);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float xf[8], wf[8];
+    xpu::unpack8<xpu::kBf16>(xv[c], xf);
+    xpu::unpack8<xpu::kBf16>(wv[c], wf);
+    uint32_t code[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) code[e] = xpu::f32_to_bf16(wf[e] * xpu::round_bf16(xf[e] * scale));
+    // slices past K stay zero (their x and w loads were zero, and so are
+    // their codes: bf16(0 * ...) = +0)
+    xv[c] = u32x4{code[0] | (code[1] << 16), code[2] | (code[3] << 16), code[4] | (code[5] << 16),
+                  code[6] | (code[7] << 16)};
+  }
+}
+
+template <int R, int NC, bool PAIRED>
+XPU_DEVICE void load_rows(const uint16_t *__restrict__ W, uint32_t K, uint32_t rows_total, uint32_t u0,
+                          uint32_t pair_offset, u32x4 (&a)[NC][R]) {
+  const uint16_t *rows[R];
+  xpu::gemv_row_ptrs<R, PAIRED>(W, K, rows_total, u0, pair_offset, rows);
+  const uint32_t lane = xpu::lane_id();
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      a[c][r] = c * 512u + lane * 8u < K ? xpu::load_nt16(rows[r] + c * 512u) : u32x4{0, 0, 0, 0};
+}
+
+template <int R, int NC>
+XPU_DEVICE void dot_rows(const u32x4 (&a)[NC][R], const u32x4 (&xv)[NC], float (&out)[R]) {
+  float acc[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) xpu::fma_chunk<xpu::kBf16, R>(acc, a[c], xv[c]);
+#pragma unroll
+  for (int r = 0; r < R; ++r) out[r] = xpu::wave_butterfly(xpu::fold8(acc[r]));
+}
+
+// Grid-stride loop over output units (rows, or row pairs when PAIRED), one
+// unit group of R rows per wavefront per step. vec_load issues the vector
+// loads, vec_finish turns them into xv; body(unit0, out[R]).
+template <int R, int NC, bool PAIRED, typename VecLoad, typename VecFinish, typename Body>
+XPU_DEVICE void reg_gemv(const uint16_t *__restrict__ W, uint32_t units, uint32_t K, VecLoad vec_load,
+                         VecFinish vec_finish, Body body) {
+  constexpr uint32_t per_wave = PAIRED ? R / 2 : R;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t waves = blockDim.x >> 6;
+  const uint32_t rows_total = PAIRED ? 2 * units : units;
+  const uint32_t pair_offset = PAIRED ? units : 0;
+  const uint32_t stride = gridDim.x * waves * per_wave;
+  uint32_t u0 = (blockIdx.x * waves + wave) * per_wave;
+  vec_load();
+  u32x4 a[NC][R];
+  load_rows<R, NC, PAIRED>(W, K, rows_total, u0 < units ? u0 : 0, pair_offset, a);
+  u32x4 xv[NC];
+  vec_finish(xv);
+  for (; u0 < units; u0 += stride) {
+    float out[R];
+    dot_rows<R, NC>(a, xv, out);
+    body(u0, out);
+    if (u0 + stride < units) load_rows<R, NC, PAIRED>(W, K, rows_total, u0 + stride, pair_offset, a);
+  }
+}
+
+}  // namespace
+
+template <int R, int NC>
+XPU_DEVICE void q3_norm_gemv_reg(const uint16_t *__restrict__ W, uint16_t *x, const uint16_t *__restrict__ norm_w,
+                                 uint16_t *__restrict__ out, uint32_t M, uint32_t K, float eps,
+                                 const uint16_t *__restrict__ embed, const uint32_t *__restrict__ state,
+                                 uint32_t vocab) {
+  const uint16_t *src = x;
+  if (embed) {
+    uint32_t token = state[1];
+    if (token >= vocab) token = 0;
+    src = embed + static_cast<uint64_t>(token) * K;
+  }
+  const uint32_t lane = xpu::lane_id();
+  u32x4 xr[NC], wr[NC];
+  reg_gemv<R, NC, false>(
+      W, M, K,
+      [&] {
+        load_slices<NC>(src, K, xr);
+        load_slices<NC>(norm_w, K, wr);
+      },
+      [&](u32x4 (&xv)[NC]) {
+        if (embed && blockIdx.x == 0 && threadIdx.x < 64) {  // the residual stream starts as the embedding row
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+            if (c * 512u + lane * 8u < K) *reinterpret_cast<u32x4 *>(x + c * 512u + lane * 8u) = xr[c];
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) xv[c] = xr[c];
+        rmsnorm_slices<NC>(xv, wr, K, eps);
+      },
+      [&](uint32_t row0, const float (&o)[R]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (lane == static_cast<uint32_t>(r) && row0 + r < M)
+            out[row0 + r] = static_cast<uint16_t>(xpu::f32_to_bf16(o[r]));
+      });
+}
+
+template <int R, int NC>
+XPU_DEVICE void q3_gemv_residual_reg(const uint16_t *__restrict__ W, const uint16_t *__restrict__ v, uint16_t *x,
+                                     uint32_t M, uint32_t K) {
+  const uint32_t lane = xpu::lane_id();
+  u32x4 vr[NC];
+  reg_gemv<R, NC, false>(
+      W, M, K, [&] { load_slices<NC>(v, K, vr); },
+      [&](u32x4 (&xv)[NC]) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) xv[c] = vr[c];
+      },
+      [&](uint32_t row0, const float (&o)[R]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (lane == static_cast<uint32_t>(r) && row0 + r < M) {
+            const float sum = xpu::bf16_to_f32(x[row0 + r]) + xpu::round_bf16(o[r]);
+            x[row0 + r] = static_cast<uint16_t>(xpu::f32_to_bf16(sum));
+          }
+      });
+}
+
+template <int R, int NC>
+XPU_DEVICE void q3_norm_gemv_swiglu_reg(const uint16_t *__restrict__ Wgu, const uint16_t *__restrict__ x,
+                                        const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ h, uint32_t I,
+                                        uint32_t K, float eps) {
+  static_assert(R % 2 == 0, "gate/up rows come in pairs");
+  constexpr int P = R / 2;
+  const uint32_t lane = xpu::lane_id();
+  u32x4 xr[NC], wr[NC];
+  reg_gemv<R, NC, true>(
+      Wgu, I, K,
+      [&] {
+        load_slices<NC>(x, K, xr);
+        load_slices<NC>(norm_w, K, wr);
+      },
+      [&](u32x4 (&xv)[NC]) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) xv[c] = xr[c];
+        rmsnorm_slices<NC>(xv, wr, K, eps);
+      },
+      [&](uint32_t i0, const float (&o)[R]) {
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+          if (lane == static_cast<uint32_t>(p) && i0 + p < I)
+            h[i0 + p] = static_cast<uint16_t>(silu_mul_code(xpu::round_bf16(o[p]), xpu::round_bf16(o[P + p])));
+      });
+}
+
+template <int R, int NC>
+XPU_DEVICE void q3_norm_gemv_logits_reg(const uint16_t *__restrict__ E, const uint16_t *__restrict__ x,
+                                        const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ logits,
+                                        uint32_t V, uint32_t K, float eps, float *__restrict__ part_val,
+                                        uint32_t *__restrict__ part_idx, uint32_t *__restrict__ part_bad) {
+  __shared__ float redv[4];
+  __shared__ uint32_t redi[4], redb[4];
+  const uint32_t lane = xpu::lane_id();
+  float best = -__builtin_inff();
+  uint32_t best_index = 0xffffffffu, bad = 0;
+  u32x4 xr[NC], wr[NC];
+  reg_gemv<R, NC, false>(
+      E, V, K,
+      [&] {
+        load_slices<NC>(x, K, xr);
+        load_slices<NC>(norm_w, K, wr);
+      },
+      [&](u32x4 (&xv)[NC]) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) xv[c] = xr[c];
+        rmsnorm_slices<NC>(xv, wr, K, eps);
+      },
+      [&](uint32_t row0, const float (&o)[R]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (row0 + r >= V) break;
+          const uint32_t code = xpu::f32_to_bf16(o[r]);
+          if (lane == static_cast<uint32_t>(r)) logits[row0 + r] = static_cast<uint16_t>(code);
+          const float v = xpu::bf16_to_f32(code);
+          if (!xpu::finite_f(v)) bad = 1;
+          xpu::argmax_merge(best, best_index, v, row0 + r);
+        }
+      });
+  xpu::block_argmax(best, best_index, bad, redv, redi, redb);
+  if (threadIdx.x == 0) {
+    part_val[blockIdx.x] = best;
+    part_idx[blockIdx.x] = best_index;
+    part_bad[blockIdx.x] = bad;
+  }
+}
+
+#define XPU_Q3_REG_SET(NC)                                                                                     \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_norm_gemv_r2_v##NC(                                \
+      const uint16_t *__restrict__ W, uint16_t *x, const uint16_t *__restrict__ norm_w,                       \
+      uint16_t *__restrict__ out, uint32_t M, uint32_t K, float eps, const uint16_t *__restrict__ embed,      \
+      const uint32_t *__restrict__ state, uint32_t vocab) {                                                   \
+    q3_norm_gemv_reg<2, NC>(W, x, norm_w, out, M, K, eps, embed, state, vocab);                               \
+  }                                                                                                           \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_gemv_residual_r1_v##NC(                            \
+      const uint16_t *__restrict__ W, const uint16_t *__restrict__ v, uint16_t *x, uint32_t M, uint32_t K) {  \
+    q3_gemv_residual_reg<1, NC>(W, v, x, M, K);                                                               \
+  }                                                                                                           \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_norm_gemv_swiglu_r2_v##NC(                         \
+      const uint16_t *__restrict__ Wgu, const uint16_t *__restrict__ x, const uint16_t *__restrict__ norm_w,  \
+      uint16_t *__restrict__ h, uint32_t I, uint32_t K, float eps) {                                          \
+    q3_norm_gemv_swiglu_reg<2, NC>(Wgu, x, norm_w, h, I, K, eps);                                             \
+  }                                                                                                           \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_norm_gemv_logits_r2_v##NC(                         \
+      const uint16_t *__restrict__ E, const uint16_t *__restrict__ x, const uint16_t *__restrict__ norm_w,    \
+      uint16_t *__restrict__ logits, uint32_t V, uint32_t K, float eps, float *__restrict__ part_val,         \
+      uint32_t *__restrict__ part_idx, uint32_t *__restrict__ part_bad) {                                     \
+    q3_norm_gemv_logits_reg<2, NC>(E, x, norm_w, logits, V, K, eps, part_val, part_idx, part_bad);            \
+  }
+
+XPU_Q3_REG_SET(1)
+XPU_Q3_REG_SET(2)
+XPU_Q3_REG_SET(4)
+XPU_Q3_REG_SET(6)
+XPU_Q3_REG_SET(8)
+
 // One block per query head: QK-norm + RoPE of q and of its kv head's k; the
 // first query head of each group writes k and v into the engine caches at
 // position state[0]; then attention over positions 0..state[0].

@@ -277,30 +277,43 @@ int setup_launches(xpu_qwen3 &e) {
   };
   const uint32_t qkv_rows = (c.heads + 2 * c.kv_heads) * c.head_dim, qd = c.heads * c.head_dim;
   int rc;
-  if ((rc = find("xpu_q3_norm_gemv_r2", e.qkv_l))) return rc;
+  // Register-vector kernels (_v<NC>: vector slices and RMSNorm in lane
+  // registers, no LDS) when K <= 512 NC for a built NC; else the LDS-staged
+  // kernels.
+  auto reg_nc = [](uint32_t K) -> uint32_t {
+    for (uint32_t nc : {1u, 2u, 4u, 6u, 8u})
+      if (K <= 512u * nc) return nc;
+    return 0;
+  };
+  auto pick = [&](const std::string &reg_base, uint32_t K, const char *lds_name, xpu_qwen3::Launch &l) -> int {
+    const uint32_t nc = reg_nc(K);
+    if (nc) {
+      l.k = e.rt->find_exact(reg_base + "_v" + std::to_string(nc));
+      l.shared = 0;
+      if (l.k) return XPU_OK;
+    }
+    l.shared = kpad_bytes(K);
+    return find(lds_name, l);
+  };
+  if ((rc = pick("xpu_q3_norm_gemv_r2", c.hidden, "xpu_q3_norm_gemv_r2", e.qkv_l))) return rc;
   e.qkv_l.grid = std::min(cap, (qkv_rows + 7) / 8);
-  e.qkv_l.shared = kpad_bytes(c.hidden);
   if ((rc = find("xpu_q3_attention", e.attn_l))) return rc;
   e.attn_l.grid = c.heads;
-  // residual GEMVs: the whole row in one batch of loads when K is 2048,
-  // 3072 or 4096 (U = K / 512)
+  // LDS-staged residual GEMVs: the whole row in one batch of loads when K is
+  // 2048, 3072 or 4096 (U = K / 512)
   auto residual_kernel = [](uint32_t K) {
     return K == 2048 ? "xpu_q3_gemv_residual_r1u4"
                      : K == 3072 ? "xpu_q3_gemv_residual_r1u6"
                                  : K == 4096 ? "xpu_q3_gemv_residual_r1u8" : "xpu_q3_gemv_residual_r1";
   };
-  if ((rc = find(residual_kernel(qd), e.o_l))) return rc;
+  if ((rc = pick("xpu_q3_gemv_residual_r1", qd, residual_kernel(qd), e.o_l))) return rc;
   e.o_l.grid = std::min(cap, (c.hidden + 3) / 4);
-  e.o_l.shared = kpad_bytes(qd);
-  if ((rc = find("xpu_q3_norm_gemv_swiglu_r2", e.gu_l))) return rc;
+  if ((rc = pick("xpu_q3_norm_gemv_swiglu_r2", c.hidden, "xpu_q3_norm_gemv_swiglu_r2", e.gu_l))) return rc;
   e.gu_l.grid = std::min(cap, (c.intermediate + 3) / 4);
-  e.gu_l.shared = kpad_bytes(c.hidden);
-  if ((rc = find(residual_kernel(c.intermediate), e.down_l))) return rc;
+  if ((rc = pick("xpu_q3_gemv_residual_r1", c.intermediate, residual_kernel(c.intermediate), e.down_l))) return rc;
   e.down_l.grid = std::min(cap, (c.hidden + 3) / 4);
-  e.down_l.shared = kpad_bytes(c.intermediate);
-  if ((rc = find("xpu_q3_norm_gemv_logits_r2", e.logits_l))) return rc;
+  if ((rc = pick("xpu_q3_norm_gemv_logits_r2", c.hidden, "xpu_q3_norm_gemv_logits_r2", e.logits_l))) return rc;
   e.logits_l.grid = std::min(e.nparts, (c.vocab + 7) / 8);
-  e.logits_l.shared = kpad_bytes(c.hidden);
   if ((rc = find("xpu_q3_argmax_finish", e.finish_l))) return rc;
   e.finish_l.grid = 1;
   for (auto *l : {&e.qkv_l, &e.o_l, &e.gu_l, &e.down_l, &e.logits_l})
