@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_size_t, c_uint32, c_uint64, c_void_p
 
 PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -214,12 +215,21 @@ class Runtime:
 
     def __init__(self, module_path: str | None = None, device: int = -1):
         self.lib = library()
+        self._dependents = weakref.WeakSet()
         handle = c_void_p()
         check(self.lib.xpu_rt_create(module_path.encode() if module_path else None, device, ctypes.byref(handle)))
         self.handle = handle
 
+    def add_dependent(self, obj) -> None:
+        """Register an object holding allocations of this runtime (an engine);
+        close() closes it first, so it never frees through a destroyed
+        runtime."""
+        self._dependents.add(obj)
+
     def close(self):
         if self.handle:
+            for dep in list(self._dependents):
+                dep.close()
             self.lib.xpu_rt_destroy(self.handle)
             self.handle = None
 

@@ -608,6 +608,18 @@ XPU_Q3_REG_SET(8)
 // One block per query head: QK-norm + RoPE of q and of its kv head's k; the
 // first query head of each group writes k and v into the engine caches at
 // position state[0]; then attention over positions 0..state[0].
+//
+// Contexts of up to kAttnTile positions (thread t <-> position t) take four
+// block barriers: every load is issued at entry without branches (q/k rows,
+// norm gains and cos/sin first, so the QK-norm / RoPE of waves 0 and 1 only
+// waits for those; then the thread's K row from the chunk-major cache and
+// its V pieces in the P.V layout); the softmax maximum goes through one LDS
+// exchange; the canonical denominator is folded in registers (the 8 slots
+// of canonical lane L are the exponentials of positions 8 L .. 8 L + 7,
+// held by 8 consecutive lanes, folded with quad permutations and a half-row
+// mirror) and its 64-lane butterfly is evaluated by every wave from LDS;
+// then P.V and the fixed class tree. Same operations in the same order as
+// attention_tail_short. Longer contexts use attention_head.
 extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
     const uint16_t *__restrict__ qkv, const uint16_t *__restrict__ qnorm_w,
     const uint16_t *__restrict__ knorm_w, const uint16_t *__restrict__ rope_cos,
@@ -618,6 +630,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   __shared__ float red[4 * xpu::kHeadDim];
   __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
   __shared__ __align__(16) uint16_t ks[xpu::kHeadDim];
+  __shared__ __align__(16) uint16_t junk[2 * xpu::kHeadDim];
   __shared__ __align__(16) uint16_t vtile[xpu::kAttnTile * xpu::kVPitch];
   const uint32_t head = blockIdx.x;
   const uint32_t pos = state[0];
@@ -629,62 +642,100 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   const uint16_t *qsrc = qkv + head * xpu::kHeadDim;
   const uint16_t *ksrc = qkv + (heads + kv) * xpu::kHeadDim;
   const uint16_t *vsrc = qkv + (heads + kv_heads + kv) * xpu::kHeadDim;
-  const uint32_t wave = threadIdx.x >> 6, tid = threadIdx.x;
+  const uint32_t tid = threadIdx.x, lane = xpu::lane_id();
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
   const uint64_t kchunk = static_cast<uint64_t>(max_seq) * 8u;  // chunk-major K cache
   const uint32_t n = pos + 1;
-  // Up to kAttnTile positions, thread t owns position t: its cached K and V
-  // rows (t < pos; written by earlier steps) are loaded before the QK-norm /
-  // RoPE prologue so their latency overlaps it.
   const bool short_ctx = n <= xpu::kAttnTile;
-  // QK-norm / RoPE operands of waves 0 (q) and 1 (k), lanes 0..15
-  const uint32_t lane = xpu::lane_id();
-  u32x4 hx = {0, 0, 0, 0}, hw = {0, 0, 0, 0}, hc = {0, 0, 0, 0}, hs = {0, 0, 0, 0};
-  if (wave < 2 && lane < 16) {
-    hx = *reinterpret_cast<const u32x4 *>((wave == 0 ? qsrc : ksrc) + lane * 8u);
-    hw = *reinterpret_cast<const u32x4 *>((wave == 0 ? qnorm_w : knorm_w) + lane * 8u);
-    hc = *reinterpret_cast<const u32x4 *>(cos_row + lane * 8u);
-    hs = *reinterpret_cast<const u32x4 *>(sin_row + lane * 8u);
-  }
-  // K rows for the scores (thread t, position t) and V pieces in the P.V
-  // layout of attention_tail_short (the current position's v from qkv)
+  // QK-norm / RoPE operands (waves 0: q, 1: k; lanes 0..15 used)
+  const uint32_t l16 = lane & 15u;
+  const u32x4 hx = *reinterpret_cast<const u32x4 *>((wave == 0 ? qsrc : ksrc) + l16 * 8u);
+  const u32x4 hw = *reinterpret_cast<const u32x4 *>((wave == 0 ? qnorm_w : knorm_w) + l16 * 8u);
+  const u32x4 hc = *reinterpret_cast<const u32x4 *>(cos_row + l16 * 8u);
+  const u32x4 hs = *reinterpret_cast<const u32x4 *>(sin_row + l16 * 8u);
+  const u32x4 hv = *reinterpret_cast<const u32x4 *>(vsrc + l16 * 8u);  // the new v row
+  __builtin_amdgcn_sched_barrier(0);  // these five loads go out first
+  // K row of position tid (clamped into the cache; positions >= pos are
+  // replaced below) and V pieces: lane l of wave w owns residue class
+  // cls = 4 w + l / 16 and dims 8 (l % 16) .. + 7; vpv[it] = V[16 it + cls]
+  // (the current position's v from qkv; entries past pos are not used)
   u32x4 krow[16], vpv[xpu::kAttnTile / 16];
-  if (short_ctx) {
-    if (tid < pos) xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(tid) * 8u, krow, kchunk);
-    const uint32_t cls = wave * 4u + (lane >> 4), dim0 = (lane & 15u) * 8u;
+  xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(min(tid, max_seq - 1)) * 8u, krow, kchunk);
+  const uint32_t cls = wave * 4u + (lane >> 4), dim0 = l16 * 8u;
 #pragma unroll
-    for (int it = 0; it < static_cast<int>(xpu::kAttnTile / 16); ++it) {
-      const uint32_t t = it * 16u + cls;
-      if (t < pos)
-        vpv[it] = *reinterpret_cast<const u32x4 *>(vcache + head_base + static_cast<uint64_t>(t) * xpu::kHeadDim + dim0);
-      else if (t == pos)
-        vpv[it] = *reinterpret_cast<const u32x4 *>(vsrc + dim0);
-      else
-        vpv[it] = u32x4{0, 0, 0, 0};
-    }
+  for (int it = 0; it < static_cast<int>(xpu::kAttnTile / 16); ++it) {
+    const uint32_t t = it * 16u + cls;
+    const uint16_t *src = t < pos ? vcache + head_base + static_cast<uint64_t>(t) * xpu::kHeadDim : vsrc;
+    vpv[it] = *reinterpret_cast<const u32x4 *>(src + dim0);  // unused past pos
   }
-  if (wave < 2) xpu::head_norm_rope_vec(hx, hw, hc, hs, eps, wave == 0 ? qs : ks);
-  __syncthreads();
-  if (head % group == 0 && tid < xpu::kHeadDim) {
-    kcache[head_base + (tid >> 3) * kchunk + static_cast<uint64_t>(pos) * 8u + (tid & 7u)] = ks[tid];
-    vcache[head_base + static_cast<uint64_t>(pos) * xpu::kHeadDim + tid] = vsrc[tid];
+  {
+    // every wave evaluates a QK-norm / RoPE (waves 2 and 3 into scratch) so
+    // that the four operand loads stay ahead of the K / V loads
+    const bool active = lane < 16;
+    const u32x4 zero{0, 0, 0, 0};
+    xpu::head_norm_rope_vec(active ? hx : zero, active ? hw : zero, hc, hs, eps,
+                            wave == 0 ? qs : wave == 1 ? ks : junk + (wave - 2) * xpu::kHeadDim);
+  }
+  __syncthreads();  // 1: qs, ks
+  if (head % group == 0 && tid < 16) {
+    // the new k (chunk-major) and v (head-major) at position pos
+    *reinterpret_cast<u32x4 *>(kcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) =
+        *reinterpret_cast<const u32x4 *>(ks + tid * 8u);
+    *reinterpret_cast<u32x4 *>(vcache + head_base + static_cast<uint64_t>(pos) * xpu::kHeadDim + tid * 8u) = hv;
   }
   if (!short_ctx) {
     xpu::attention_head<true>(qs, kcache + head_base, vcache + head_base,
-                              xpu::KvLayout{8u, kchunk, xpu::kHeadDim}, n, ks, vsrc,
-                              scale, out + head * xpu::kHeadDim, sbuf, vtile, red);
+                              xpu::KvLayout{8u, kchunk, xpu::kHeadDim}, n, ks, vsrc, scale,
+                              out + head * xpu::kHeadDim, sbuf, vtile, red);
     return;
   }
-  // pass 1 of attention_head for one tile, from the preloaded K rows (the
-  // current position from ks)
-  float local_max = -__builtin_inff();
-  if (tid < n) {
-    if (tid == pos) xpu::load_head_row(ks, krow);
-    const float sc = xpu::attention_score_regs(qs, krow, scale);
-    sbuf[tid] = sc;
-    local_max = sc;
+  // scores (the current position from ks) and the block maximum
+  if (tid == pos) xpu::load_head_row(ks, krow);
+  const float sc = tid < n ? xpu::attention_score_regs(qs, krow, scale) : -__builtin_inff();
+  const float wmax = xpu::wave_reduce(sc, [](float x, float y) { return fmaxf(x, y); });
+  if (lane == 0) red[wave] = wmax;
+  __syncthreads();  // 2: wave maxima
+  const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // exponentials; canonical lane L = tid / 8 folds its 8 slots
+  const float ex = tid < n ? xpu::canonical_exp(sc - mx) : 0.0f;
+  sbuf[tid] = ex;
+  float f = ex + xpu::dpp_f<0xB1>(ex);  // (a0 + a1), (a2 + a3), ...
+  f = f + xpu::dpp_f<0x4E>(f);          // (a0 + a1) + (a2 + a3)
+  f = f + xpu::dpp_f<0x141>(f);         // row_half_mirror: the other quad of the eight
+  float *lane_sum = red + 4;            // 32 canonical lane sums (n <= 256)
+  if ((tid & 7u) == 0) lane_sum[tid >> 3] = f;
+  __syncthreads();  // 3: exponentials and lane sums
+  const float total = xpu::wave_butterfly(lane < 32 ? lane_sum[lane] : 0.0f);
+  const float inv = 1.0f / total;
+  float part[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int it = 0; it < static_cast<int>(xpu::kAttnTile / 16); ++it) {
+    const uint32_t t = it * 16u + cls;
+    if (t < n) {
+      const float pt = xpu::round_bf16(sbuf[t] * inv);
+      float v[8];
+      xpu::unpack8<xpu::kBf16>(vpv[it], v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[e] = __builtin_fmaf(pt, v[e], part[e]);
+    }
   }
-  xpu::attention_tail_short(n, out + head * xpu::kHeadDim, sbuf, red, local_max, vpv);
+  float sum[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float pair = part[e] + xpu::xor16_f(part[e]);  // (c0 + c1), (c2 + c3)
+    sum[e] = pair + xpu::xor32_f(pair);                   // (c0 + c1) + (c2 + c3)
+  }
+  float *wsum = sbuf + xpu::kAttnTile;  // 4 x 128 wave partials, past the exponentials
+  if (lane < 16) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wsum[wave * xpu::kHeadDim + lane * 8u + e] = sum[e];
+  }
+  __syncthreads();  // 4: wave partials
+  if (tid < xpu::kHeadDim) {
+    const float r = (wsum[tid] + wsum[xpu::kHeadDim + tid]) + (wsum[2 * xpu::kHeadDim + tid] + wsum[3 * xpu::kHeadDim + tid]);
+    out[head * xpu::kHeadDim + tid] = static_cast<uint16_t>(xpu::f32_to_bf16(r));
+  }
 }
 
 // Reduce the per-block argmax partials; token = 0xffffffff if any logit was

@@ -68,6 +68,8 @@ class Engine:
                  runtime: Runtime | None = None, model_dir: str | None = None):
         self.lib = library()
         self.runtime = runtime
+        if runtime is not None:
+            runtime.add_dependent(self)  # closed before the runtime it allocates from
         handle = c_void_p()
         rt = runtime.handle if runtime else None
         if model_dir is not None:
