@@ -358,14 +358,22 @@ XPU_Q3_LOGITS(_r4, 4, 2)
 // clamped and discarded), so the weight latency overlaps the norm.
 namespace {
 
+constexpr uint32_t kRegBlock = 256;  // block size of the register-vector kernels
+
+// Branch-free masked loads (K % 8 == 0, K >= 8): a slice past K reads the
+// last in-range slice and is replaced by zeros, so every load is issued
+// unconditionally and the wait counts stay exact.
+XPU_DEVICE u32x4 masked16(const uint16_t *__restrict__ base, uint32_t col, uint32_t K, bool nt) {
+  const uint32_t c = col < K ? col : K - 8u;
+  const u32x4 v = nt ? xpu::load_nt16(base + c) : *reinterpret_cast<const u32x4 *>(base + c);
+  return col < K ? v : u32x4{0, 0, 0, 0};
+}
+
 template <int NC>
 XPU_DEVICE void load_slices(const uint16_t *__restrict__ v, uint32_t K, u32x4 (&xv)[NC]) {
   const uint32_t lane = xpu::lane_id();
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const uint32_t col = c * 512u + lane * 8u;
-    xv[c] = col < K ? *reinterpret_cast<const u32x4 *>(v + col) : u32x4{0, 0, 0, 0};
-  }
+  for (int c = 0; c < NC; ++c) xv[c] = masked16(v, c * 512u + lane * 8u, K, false);
 }
 
 // xv <- codes of bf16(w * bf16(x * (1 / sqrt(sum(x^2) / K + eps))))
@@ -399,14 +407,14 @@ XPU_DEVICE void rmsnorm_slices(u32x4 (&xv)[NC], const u32x4 (&wv)[NC], uint32_t 
 template <int R, int NC, bool PAIRED>
 XPU_DEVICE void load_rows(const uint16_t *__restrict__ W, uint32_t K, uint32_t rows_total, uint32_t u0,
                           uint32_t pair_offset, u32x4 (&a)[NC][R]) {
-  const uint16_t *rows[R];
-  xpu::gemv_row_ptrs<R, PAIRED>(W, K, rows_total, u0, pair_offset, rows);
   const uint32_t lane = xpu::lane_id();
 #pragma unroll
-  for (int c = 0; c < NC; ++c)
+  for (int r = 0; r < R; ++r) {
+    const uint32_t want = PAIRED ? (r < R / 2 ? u0 + r : u0 + pair_offset + (r - R / 2)) : u0 + r;
+    const uint16_t *row = W + static_cast<uint64_t>(want < rows_total ? want : rows_total - 1) * K;
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      a[c][r] = c * 512u + lane * 8u < K ? xpu::load_nt16(rows[r] + c * 512u) : u32x4{0, 0, 0, 0};
+    for (int c = 0; c < NC; ++c) a[c][r] = masked16(row, c * 512u + lane * 8u, K, true);
+  }
 }
 
 template <int R, int NC>
@@ -423,19 +431,20 @@ XPU_DEVICE void dot_rows(const u32x4 (&a)[NC][R], const u32x4 (&xv)[NC], float (
 }
 
 // Grid-stride loop over output units (rows, or row pairs when PAIRED), one
-// unit group of R rows per wavefront per step. vec_load issues the vector
-// loads, vec_finish turns them into xv; body(unit0, out[R]).
+// unit group of R rows per wavefront per step. vec_load(first unit) issues
+// the vector loads (and any other early load), vec_finish turns them into
+// xv; body(unit0, out[R]).
 template <int R, int NC, bool PAIRED, typename VecLoad, typename VecFinish, typename Body>
 XPU_DEVICE void reg_gemv(const uint16_t *__restrict__ W, uint32_t units, uint32_t K, VecLoad vec_load,
                          VecFinish vec_finish, Body body) {
   constexpr uint32_t per_wave = PAIRED ? R / 2 : R;
+  constexpr uint32_t waves = kRegBlock / 64;  // launched with kRegBlock threads
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t waves = blockDim.x >> 6;
   const uint32_t rows_total = PAIRED ? 2 * units : units;
   const uint32_t pair_offset = PAIRED ? units : 0;
   const uint32_t stride = gridDim.x * waves * per_wave;
   uint32_t u0 = (blockIdx.x * waves + wave) * per_wave;
-  vec_load();
+  vec_load(u0);
   u32x4 a[NC][R];
   load_rows<R, NC, PAIRED>(W, K, rows_total, u0 < units ? u0 : 0, pair_offset, a);
   u32x4 xv[NC];
@@ -465,7 +474,7 @@ XPU_DEVICE void q3_norm_gemv_reg(const uint16_t *__restrict__ W, uint16_t *x, co
   u32x4 xr[NC], wr[NC];
   reg_gemv<R, NC, false>(
       W, M, K,
-      [&] {
+      [&](uint32_t) {
         load_slices<NC>(src, K, xr);
         load_slices<NC>(norm_w, K, wr);
       },
@@ -492,8 +501,16 @@ XPU_DEVICE void q3_gemv_residual_reg(const uint16_t *__restrict__ W, const uint1
                                      uint32_t M, uint32_t K) {
   const uint32_t lane = xpu::lane_id();
   u32x4 vr[NC];
+  // residual input of the first unit's rows (lane r: row u0 + r), loaded
+  // with the vector so the read-modify-write does not wait on memory
+  uint32_t first = 0xffffffffu, xres = 0;
   reg_gemv<R, NC, false>(
-      W, M, K, [&] { load_slices<NC>(v, K, vr); },
+      W, M, K,
+      [&](uint32_t u0) {
+        load_slices<NC>(v, K, vr);
+        first = u0;
+        if (lane < static_cast<uint32_t>(R) && u0 + lane < M) xres = x[u0 + lane];
+      },
       [&](u32x4 (&xv)[NC]) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) xv[c] = vr[c];
@@ -502,7 +519,8 @@ XPU_DEVICE void q3_gemv_residual_reg(const uint16_t *__restrict__ W, const uint1
 #pragma unroll
         for (int r = 0; r < R; ++r)
           if (lane == static_cast<uint32_t>(r) && row0 + r < M) {
-            const float sum = xpu::bf16_to_f32(x[row0 + r]) + xpu::round_bf16(o[r]);
+            const uint32_t old = row0 == first ? xres : x[row0 + r];
+            const float sum = xpu::bf16_to_f32(old) + xpu::round_bf16(o[r]);
             x[row0 + r] = static_cast<uint16_t>(xpu::f32_to_bf16(sum));
           }
       });
@@ -518,7 +536,7 @@ XPU_DEVICE void q3_norm_gemv_swiglu_reg(const uint16_t *__restrict__ Wgu, const 
   u32x4 xr[NC], wr[NC];
   reg_gemv<R, NC, true>(
       Wgu, I, K,
-      [&] {
+      [&](uint32_t) {
         load_slices<NC>(x, K, xr);
         load_slices<NC>(norm_w, K, wr);
       },
@@ -548,7 +566,7 @@ XPU_DEVICE void q3_norm_gemv_logits_reg(const uint16_t *__restrict__ E, const ui
   u32x4 xr[NC], wr[NC];
   reg_gemv<R, NC, false>(
       E, V, K,
-      [&] {
+      [&](uint32_t) {
         load_slices<NC>(x, K, xr);
         load_slices<NC>(norm_w, K, wr);
       },
