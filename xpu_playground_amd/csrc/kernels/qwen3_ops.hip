@@ -643,7 +643,8 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
     const uint16_t *__restrict__ knorm_w, const uint16_t *__restrict__ rope_cos,
     const uint16_t *__restrict__ rope_sin, uint16_t *__restrict__ kcache,
     uint16_t *__restrict__ vcache, uint16_t *__restrict__ out, const uint32_t *__restrict__ state,
-    uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float eps, float scale) {
+    uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float eps, float scale,
+    const uint16_t *__restrict__ prefetch, uint64_t prefetch_bytes, uint32_t prefetch_delay) {
   __shared__ float sbuf[xpu::kAttnChunk];
   __shared__ float red[4 * xpu::kHeadDim];
   __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
@@ -651,8 +652,30 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   __shared__ __align__(16) uint16_t junk[2 * xpu::kHeadDim];
   __shared__ __align__(16) uint16_t vtile[xpu::kAttnTile * xpu::kVPitch];
   const uint32_t head = blockIdx.x;
+  if (head >= heads) {
+    // Blocks past the query heads read [prefetch, prefetch + prefetch_bytes)
+    // (the weights of the kernels that follow) so that they come from the
+    // Infinity Cache, not HBM, when those kernels run; the attention itself
+    // occupies only `heads` compute units for its latency-bound duration.
+    // start after prefetch_delay x 64 x 16 cycles, behind the attention's
+    // own loads
+    for (uint32_t d = 0; d < prefetch_delay; ++d) __builtin_amdgcn_s_sleep(16);
+    const uint64_t n16 = prefetch_bytes / 16u;
+    const u32x4 *p = reinterpret_cast<const u32x4 *>(prefetch);
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x - heads) * blockDim.x;
+    uint32_t acc = 0;
+    for (uint64_t i = static_cast<uint64_t>(head - heads) * blockDim.x + threadIdx.x; i < n16; i += 4 * stride) {
+      u32x4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = i + u * stride < n16 ? p[i + u * stride] : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].w;
+    }
+    asm volatile("" : : "v"(acc));  // keeps the loads
+    return;
+  }
   const uint32_t pos = state[0];
-  if (head >= heads || pos >= max_seq) return;
+  if (pos >= max_seq) return;
   const uint32_t group = heads / kv_heads;
   const uint32_t kv = head / group;
   const uint16_t *cos_row = rope_cos + static_cast<uint64_t>(pos) * xpu::kHeadDim;

@@ -21,6 +21,7 @@
 #include "runtime_internal.hpp"
 
 #include <chrono>
+#include <cstdlib>
 #include <cstdio>
 #include <fstream>
 #include <iostream>
@@ -137,6 +138,11 @@ struct xpu_qwen3 {
   uint32_t *ref_token = nullptr;
   uint32_t nparts = 0;
   void *graph = nullptr;
+  // weight prefetch by the attention kernel's spare blocks: byte cap and
+  // start delay (XPU_Q3_PREFETCH_MB, XPU_Q3_PREFETCH_DELAY)
+  uint64_t pf_cap = ~uint64_t{0};
+  uint32_t pf_delay = 2;
+  bool pf_next = false;
   // fused-path geometry
   struct Launch {
     const xpu::KernelInfo *k = nullptr;
@@ -298,7 +304,15 @@ int setup_launches(xpu_qwen3 &e) {
   if ((rc = pick("xpu_q3_norm_gemv_r2", c.hidden, "xpu_q3_norm_gemv_r2", e.qkv_l))) return rc;
   e.qkv_l.grid = std::min(cap, (qkv_rows + 7) / 8);
   if ((rc = find("xpu_q3_attention", e.attn_l))) return rc;
-  e.attn_l.grid = c.heads;
+  // one block per query head, the other compute units prefetch weights
+  e.attn_l.grid = std::max(c.heads, e.rt->compute_units);
+  {
+    const char *cap = std::getenv("XPU_Q3_PREFETCH_MB"), *delay = std::getenv("XPU_Q3_PREFETCH_DELAY");
+    const char *next = std::getenv("XPU_Q3_PREFETCH_NEXT");
+    e.pf_cap = cap && *cap ? std::strtoull(cap, nullptr, 10) << 20 : ~uint64_t{0};
+    e.pf_delay = delay && *delay ? static_cast<uint32_t>(std::strtoul(delay, nullptr, 10)) : 2u;
+    e.pf_next = next && *next == '1';
+  }
   // LDS-staged residual GEMVs: the whole row in one batch of loads when K is
   // 2048, 3072 or 4096 (U = K / 512)
   auto residual_kernel = [](uint32_t K) {
@@ -381,10 +395,19 @@ int enqueue_fused_step(xpu_qwen3 &e) {
                      {{8, &L.qkv}, {8, &e.x}, {8, &L.in_norm}, {8, &e.qkv}, {4, &qkv_rows}, {4, &H}, {4, &eps},
                       {8, &embed}, {8, &e.state}, {4, &V}})))
       return rc;
+    // the attention kernel's spare blocks prefetch this layer's o_proj,
+    // [gate; up] and down_proj (contiguous in the arena)
+    const uint16_t *pf = L.o;
+    const uint8_t *pf_end = reinterpret_cast<const uint8_t *>(L.down) + uint64_t{H} * I * 2;
+    if (e.pf_next && l + 1 < c.layers)  // and the next layer's [q; k; v]
+      pf_end = reinterpret_cast<const uint8_t *>(e.layers[l + 1].qkv) + uint64_t{qkv_rows} * H * 2;
+    const uint64_t pf_bytes =
+        std::min<uint64_t>(e.pf_cap, static_cast<uint64_t>(pf_end - reinterpret_cast<const uint8_t *>(L.o)));
+    const uint32_t pf_delay = e.pf_delay;
     if ((rc = launch(e, e.attn_l, 256,
                      {{8, &e.qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &kc},
                       {8, &vc}, {8, &e.attn}, {8, &e.state}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps},
-                      {4, &scale}})))
+                      {4, &scale}, {8, &pf}, {8, &pf_bytes}, {4, &pf_delay}})))
       return rc;
     if ((rc = launch(e, e.o_l, 256, {{8, &L.o}, {8, &e.attn}, {8, &e.x}, {4, &H}, {4, &qd}}))) return rc;
     if ((rc = launch(e, e.gu_l, 256,
