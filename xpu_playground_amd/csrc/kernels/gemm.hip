@@ -49,7 +49,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-constexpr uint32_t kBM = 256, kBN = 256;
+constexpr uint32_t kBM = 256;
 constexpr uint32_t kOob = 0x80000000u;  // any offset >= the descriptor range reads 0
 
 template <int DT>
@@ -135,45 +135,55 @@ template <int DT> XPU_DEVICE uint32_t cvt_pack(float lo, float hi) {
            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
 }
 
-template <int BK, int S> struct Cfg {
-  static constexpr uint32_t kKs = BK / 16;                  // k-steps per slice
-  static constexpr uint32_t kABytes = 512u * BK;            // 256 rows x 2 BK bytes
-  static constexpr uint32_t kStage = 2u * kABytes;          // A then B (BK rows x 512 bytes)
-  static constexpr uint32_t kCpr = BK / 8;                  // 16-byte chunks per A row
-  static constexpr uint32_t kRpi = 64 / kCpr;               // A rows per DMA instruction
-  static constexpr uint32_t kDmaA = 256 / kRpi / 4;         // A DMA instructions per wave per slice
-  static constexpr uint32_t kDmaB = BK / 2 / 4;             // B DMA instructions per wave per slice
+// NJ: 32 x 32 MFMA tiles per wavefront along N (wavefront tile 128 x 32 NJ,
+// block tile 256 x 64 NJ); BK: K-slice; S: LDS stages.
+template <int NJ, int BK, int S> struct Cfg {
+  static constexpr uint32_t kBNW = 32u * NJ;                 // columns per wavefront
+  static constexpr uint32_t kBN = 2u * kBNW;                 // block tile columns
+  static constexpr uint32_t kKs = BK / 16;                   // k-steps per slice
+  static constexpr uint32_t kABytes = 512u * BK;             // 256 rows x 2 BK bytes
+  static constexpr uint32_t kBRow = 2u * kBN;                // bytes per B row in LDS
+  static constexpr uint32_t kStage = kABytes + BK * kBRow;   // A then B
+  static constexpr uint32_t kCpr = BK / 8;                   // 16-byte chunks per A row
+  static constexpr uint32_t kRpi = 64 / kCpr;                // A rows per DMA instruction
+  static constexpr uint32_t kBCpr = kBN / 8;                 // 16-byte chunks per B row
+  static constexpr uint32_t kBRpi = 64 / kBCpr;              // B rows per DMA instruction
+  static constexpr uint32_t kDmaA = 256 / kRpi / 4;          // A DMA instructions per wave per slice
+  static constexpr uint32_t kDmaB = BK / kBRpi / 4;          // B DMA instructions per wave per slice
   static constexpr uint32_t kDma = kDmaA + kDmaB;
-  static constexpr uint32_t kEpPitch = 132;                  // epilogue staging pitch (floats)
+  static constexpr uint32_t kMf = 4u * NJ;                   // MFMAs per k-step
+  static constexpr uint32_t kReads = 4u + 2u * NJ;           // fragment reads per k-step
+  static constexpr uint32_t kEpPitch = kBNW + 4;             // epilogue staging pitch (floats)
   static constexpr uint32_t kEpBytes = 4u * 64u * kEpPitch * 4u;
   static constexpr uint32_t kLds = S * kStage > kEpBytes ? S * kStage : kEpBytes;
   static_assert(kLds <= 160u * 1024u, "LDS");
+  static_assert(kBCpr == 16 || kBCpr == 32, "B rows of 16 or 32 chunks (the swizzle permutes 16)");
 };
 
-template <int DT, int BK, int S, int P, int D, bool C16>
+template <int DT, int NJ, int BK, int S, int P, int D, bool C16>
 XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
                      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {
-  using G = Cfg<BK, S>;
+  using G = Cfg<NJ, BK, S>;
   __shared__ __align__(1024) uint8_t lds[G::kLds];
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  const uint32_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + G::kBN - 1) / G::kBN;
   const TileCoord tc = tile_of_block(blockIdx.x, tiles_m, tiles_n);
-  const uint32_t m0 = tc.tm * kBM, n0 = tc.tn * kBN;
+  const uint32_t m0 = tc.tm * kBM, n0 = tc.tn * G::kBN;
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
 
   // DMA lane maps. A: instruction i of this wave fills tile rows
   // (wave + 4 i) * kRpi .. + kRpi - 1; lane t lands in physical chunk
   // t % kCpr of row t / kCpr and fetches the logical chunk that the swizzle
-  // puts there. B: instruction i fills rows 2 (wave + 4 i) .. + 1.
+  // puts there. B: instruction i fills rows kBRpi (wave + 4 i) .. + kBRpi - 1.
   const uint32_t a_row = wave * G::kRpi + lane / G::kCpr;
   const uint32_t a_chunk = (lane % G::kCpr) ^ a_swz<BK>(a_row & 15u);
   const uint32_t a_voff = (a_row * K + a_chunk * 8u) * 2u;
   const uint32_t a_istride = 4u * G::kRpi * K * 2u;
-  const uint32_t b_row = 2u * wave + lane / 32u;
-  const uint32_t b_chunk = (lane % 32u) ^ b_swz(b_row & 3u);
+  const uint32_t b_row = G::kBRpi * wave + lane / G::kBCpr;
+  const uint32_t b_chunk = (lane % G::kBCpr) ^ b_swz(b_row & 3u);
   const uint32_t b_voff = n0 + b_chunk * 8u < N ? (b_row * N + b_chunk * 8u) * 2u : kOob;
-  const uint32_t b_istride = 8u * N * 2u;
+  const uint32_t b_istride = 4u * G::kBRpi * N * 2u;
 
   // DMA instruction d (0 .. kDma-1) of slice s into stage st: A rows first,
   // then B rows. Per slice the descriptors are rebased to the slice's first
@@ -203,7 +213,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 
   // Fragment addresses (bytes within a stage). A: row wm*128 + 32 i + l%32,
   // logical chunk 2 ks + l/32. B: k-row 16 ks + 8 (l/32) + 4 h + (l%16)/4,
-  // column wn*128 + 32 j + 16 ((l/16) % 2) + 4 (l % 4): the 4-element row
+  // column wn*kBNW + 32 j + 16 ((l/16) % 2) + 4 (l % 4): the 4-element row
   // that lane l contributes to its group's transposing read.
   const uint32_t wm = wave >> 1, wn = wave & 1u;
   // The ds_read offset field holds 16 bits, so the stages are addressed from
@@ -211,7 +221,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   // that it keeps them in registers instead of materialising one register per
   // (stage, k-step, tile) combination.
   constexpr uint32_t kGroups = (S * G::kStage + 65535u) / 65536u;
-  uint32_t fa_base[kGroups][G::kKs], fb_base[kGroups][4];
+  uint32_t fa_base[kGroups][G::kKs], fb_base[kGroups][NJ];
   {
     const uint32_t krow = 8u * (lane >> 5) + ((lane & 15u) >> 2);
     const uint32_t x = 2u * ((lane >> 4) & 1u) + ((lane & 3u) >> 1);
@@ -224,28 +234,29 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
         asm volatile("" : "+v"(fa_base[g][ks]));
       }
 #pragma unroll
-      for (uint32_t j = 0; j < 4; ++j) {
-        fb_base[g][j] = lds0 + g * 65536u + G::kABytes + krow * 512u +
-                        16u * (16u * wn + ((4u * j + x) ^ b_swz(krow & 3u))) + 8u * (lane & 1u);
+      for (uint32_t j = 0; j < NJ; ++j) {
+        fb_base[g][j] = lds0 + g * 65536u + G::kABytes + krow * G::kBRow +
+                        16u * ((wn * (G::kBNW / 8u) + 4u * j + x) ^ b_swz(krow & 3u)) + 8u * (lane & 1u);
         asm volatile("" : "+v"(fb_base[g][j]));
       }
     }
   }
 
   struct Frags {
-    u32x4 a[4], b[4];
+    u32x4 a[4], b[NJ];
   };
-  // Read r (0..11) of the fragments of k-step ks in a stage, in the order
-  // the MFMAs consume them: A0, B0, B1, B2, B3 (two halves each), A1, A2, A3.
+  // Read r (0 .. kReads-1) of the fragments of k-step ks in a stage, in the
+  // order the MFMAs consume them: A0, B0 .. B(NJ-1) (two halves each), A1,
+  // A2, A3.
   auto read = [&](uint32_t stage, uint32_t ks, Frags &f, uint32_t r) {
     const uint32_t g = stage * G::kStage / 65536u, in_group = stage * G::kStage % 65536u;
-    if (r == 0 || r >= 9) {
-      const uint32_t i = r == 0 ? 0 : r - 8;
+    if (r == 0 || r > 2u * NJ) {
+      const uint32_t i = r == 0 ? 0 : r - 2u * NJ;
       const uint32_t addr = fa_base[g][ks] + in_group + i * 32u * 2u * BK;
       f.a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(addr);
     } else {
       const uint32_t j = (r - 1) >> 1, h = (r - 1) & 1;
-      const uint32_t addr = fb_base[g][j] + in_group + (16u * ks + 4u * h) * 512u;
+      const uint32_t addr = fb_base[g][j] + in_group + (16u * ks + 4u * h) * G::kBRow;
       const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(addr)));
       if (h == 0) {
         f.b[j].x = v.x;
@@ -257,23 +268,24 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     }
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[4][NJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // MFMA q = 4 i + j. Operands swapped (B^T fragment first): the
+  // MFMA q = NJ i + j. Operands swapped (B^T fragment first): the
   // accumulator tile is C^T, so each lane ends up with 4 consecutive
   // columns of one row of C.
   auto mfma_q = [&](const Frags &f, uint32_t q) {
-    acc[q >> 2][q & 3] = mfma<DT>(f.b[q & 3], f.a[q >> 2], acc[q >> 2][q & 3]);
+    acc[q / NJ][q % NJ] = mfma<DT>(f.b[q % NJ], f.a[q / NJ], acc[q / NJ][q % NJ]);
   };
 
   const uint32_t nk = (K + BK - 1) / BK;
   static_assert(D >= 1 && D <= G::kKs, "a slice's DMA is issued within the k-steps before the next barrier");
+  static_assert(P <= G::kMf && G::kReads <= G::kMf, "k-step schedule");
   // DMA ops of one slice issued during the e-th k-step after its barrier
   auto dma_part = [&](const Slice &d, uint32_t e, uint32_t x, uint32_t nx) {
     const uint32_t lo = e * G::kDma / D, hi = (e + 1) * G::kDma / D;
@@ -295,15 +307,15 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   wait_vmcnt<(S - 2) * G::kDma + G::kDma / D>();
   __syncthreads();
 #pragma unroll
-  for (uint32_t r = 0; r < 12; ++r) read(0, 0, frag[0], r);
+  for (uint32_t r = 0; r < G::kReads; ++r) read(0, 0, frag[0], r);
 
   // Instruction order is fixed with sched_barrier. Ordinary k-step: each of
-  // the first 12 MFMAs is followed by one fragment read of the next k-step,
-  // and the pending slice's DMA share of this k-step is spread over the 16.
-  // Last k-step of a slice: P MFMAs, the wait and the barrier, then the
-  // remaining MFMAs with the next slice's first fragment reads and the first
-  // share of the new slice's DMA (the DMA of a slice is spread over the D
-  // k-steps from its barrier on).
+  // the first kReads MFMAs is followed by one fragment read of the next
+  // k-step, and the pending slice's DMA share of this k-step is spread over
+  // the kMf MFMAs. Last k-step of a slice: P MFMAs, the wait and the
+  // barrier, then the remaining MFMAs with the next slice's first fragment
+  // reads and the first share of the new slice's DMA (the DMA of a slice is
+  // spread over the D k-steps from its barrier on).
   // Whole groups of S slices (one exit keeps the accumulators in place);
   // slices past nk read zeros and add nothing.
   for (uint32_t s0 = 0; s0 < nk; s0 += S) {
@@ -315,10 +327,10 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
         if (ks + 1 < G::kKs) {
           const uint32_t e = ks + 1;  // k-steps since the pending slice's barrier
 #pragma unroll
-          for (uint32_t q = 0; q < 16; ++q) {
+          for (uint32_t q = 0; q < G::kMf; ++q) {
             mfma_q(frag[cur], q);
-            if (q < 12) read(st, ks + 1, frag[cur ^ 1], q);
-            if (e < D) dma_part(pend, e, q, 16);
+            if (q < G::kReads) read(st, ks + 1, frag[cur ^ 1], q);
+            if (e < D) dma_part(pend, e, q, G::kMf);
             __builtin_amdgcn_sched_barrier(0);
           }
         } else {
@@ -331,14 +343,15 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
           __syncthreads();
           __builtin_amdgcn_sched_barrier(0);
           pend = slice_of(s0 + st + S, st);
-          constexpr uint32_t kAfter = 16 - P;
+          constexpr uint32_t kAfter = G::kMf - P;
 #pragma unroll
-          for (uint32_t q = P; q < 16; ++q) {
+          for (uint32_t q = P; q < G::kMf; ++q) {
             mfma_q(frag[cur], q);
             const uint32_t x = q - P;
             dma_part(pend, 0, x, kAfter);
 #pragma unroll
-            for (uint32_t r = x * 12 / kAfter; r < (x + 1) * 12 / kAfter; ++r) read((st + 1) % S, 0, frag[cur ^ 1], r);
+            for (uint32_t r = x * G::kReads / kAfter; r < (x + 1) * G::kReads / kAfter; ++r)
+              read((st + 1) % S, 0, frag[cur ^ 1], r);
             __builtin_amdgcn_sched_barrier(0);
           }
         }
@@ -351,21 +364,23 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   __syncthreads();
 
   // Epilogue through LDS, one 64-row band per round: each wave writes its
-  // 64 x 128 FP32 band (D layout of v_mfma_f32_32x32x16 with C^T tiles: lane
+  // 64 x kBNW FP32 band (D layout of v_mfma_f32_32x32x16 with C^T tiles: lane
   // l holds row l % 32, columns 8 g + 4 (l / 32) + 0..3 in accumulators
-  // 4 g..4 g + 3) as 16-byte rows into its own region (pitch 132 floats),
-  // then reads it back 8 consecutive columns per lane and stores 16 bytes of
-  // C per lane.
+  // 4 g..4 g + 3) as 16-byte rows into its own region (pitch kBNW + 4
+  // floats), then reads it back 8 consecutive columns per lane and stores 16
+  // bytes of C per lane.
   constexpr uint32_t kEpPitch = G::kEpPitch;
+  constexpr uint32_t kLpr = G::kBNW / 8u;  // lanes per staged row on the way out
+  constexpr uint32_t kRpr = 64u / kLpr;    // rows per read instruction
   float *ep = reinterpret_cast<float *>(lds) + wave * 64u * kEpPitch;
   const uint32_t m_lane = lane & 31u, n_lane = (lane >> 5) * 4u;
-  const uint32_t r_lane = lane >> 4, c_lane = (lane & 15u) * 8u;
+  const uint32_t r_lane = lane / kLpr, c_lane = (lane % kLpr) * 8u;
 #pragma unroll
   for (int band = 0; band < 2; ++band) {
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int i = band * 2 + ii;
@@ -376,11 +391,11 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      const uint32_t r = rr * 4u + r_lane;
+    for (uint32_t rr = 0; rr < 64u / kRpr; ++rr) {
+      const uint32_t r = rr * kRpr + r_lane;
       const f32x4 lo = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane);
       const f32x4 hi = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane + 4u);
-      const uint32_t m = m0 + wm * 128u + band * 64u + r, n = n0 + wn * 128u + c_lane;
+      const uint32_t m = m0 + wm * 128u + band * 64u + r, n = n0 + wn * G::kBNW + c_lane;
       if (m >= M || n >= n_out) continue;
       const u32x4 packed{cvt_pack<DT>(lo.x, lo.y), cvt_pack<DT>(lo.z, lo.w), cvt_pack<DT>(hi.x, hi.y),
                          cvt_pack<DT>(hi.z, hi.w)};
@@ -403,19 +418,19 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 }  // namespace dma
 }  // namespace xpu
 
-#define XPU_GEMM_DMA_VARIANT(NAME, DT, BK, S, P, D, C16)                                             \
-  extern "C" __global__ __launch_bounds__(256, 1) void NAME(                                  \
+#define XPU_GEMM_DMA_VARIANT(NAME, DT, NJ, BK, S, P, D, MINB, C16)                            \
+  extern "C" __global__ __launch_bounds__(256, MINB) void NAME(                               \
       const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C, \
       uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {         \
-    xpu::dma::body<DT, BK, S, P, D, C16>(A, B, C, M, N, K, kb, ldc, n_out);                          \
+    xpu::dma::body<DT, NJ, BK, S, P, D, C16>(A, B, C, M, N, K, kb, ldc, n_out);                \
   }
 
 // BK = 64, two stages, barrier after 4 MFMAs of a slice's last k-step, each
 // slice's DMA spread over two k-steps
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dma, xpu::kBf16, 64, 2, 4, 2, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dma, xpu::kFp16, 64, 2, 4, 2, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dmau, xpu::kBf16, 64, 2, 4, 2, false)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dmau, xpu::kFp16, 64, 2, 4, 2, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dma, xpu::kBf16, 4, 64, 2, 4, 2, 1, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dma, xpu::kFp16, 4, 64, 2, 4, 2, 1, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dmau, xpu::kBf16, 4, 64, 2, 4, 2, 1, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dmau, xpu::kFp16, 4, 64, 2, 4, 2, 1, false)
 
 // dst[r][c] = src[r * src_ld + c] for c < cols, 0 for cols <= c < dst_cols
 // (dst_cols % 8 == 0, dst 16-byte aligned): the zero padding of the
