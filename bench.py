@@ -111,14 +111,14 @@ def measured_peaks(rt):
     flops = blocks * 4 * rounds * 8 * 32768.0
     mfma_tflops = flops / (start.elapsed_ms(stop) / 10 * 1e-3) / 1e12
     nbytes = 4 << 30
-    surface, rsink = rt.alloc(nbytes), rt.alloc(rt.compute_units * 8 * 1024)
+    surface, rsink = rt.alloc(nbytes), rt.alloc(rt.compute_units * 1024)
     rt.fill_uniform(0, surface, nbytes // 2, 7)
     for _ in range(3):
-        xpu_check(lib.xpu_peak_read(rt.handle, surface, nbytes, rsink, rt.compute_units * 8))
+        xpu_check(lib.xpu_peak_read(rt.handle, surface, nbytes, rsink, rt.compute_units))
     rt.synchronize()
     start.record()
     for _ in range(10):
-        xpu_check(lib.xpu_peak_read(rt.handle, surface, nbytes, rsink, rt.compute_units * 8))
+        xpu_check(lib.xpu_peak_read(rt.handle, surface, nbytes, rsink, rt.compute_units))
     stop.record()
     rt.synchronize()
     read_gbs = nbytes / (start.elapsed_ms(stop) / 10 * 1e-3) / 1e9

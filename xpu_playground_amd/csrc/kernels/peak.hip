@@ -53,21 +53,23 @@ extern "C" __global__ __launch_bounds__(256) void xpu_peak_mfma_bf16(
   sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = sum;
 }
 
-// Streaming read of `count` 16-byte words (non-temporal loads, 4 in flight
+// Streaming read of `count` 16-byte words (non-temporal loads, 8 in flight
 // per thread per step, grid-stride), one checksum word per thread written to
-// sink (so the loads cannot be removed).
+// sink (so the loads cannot be removed). One 256-thread block per compute
+// unit keeps 8 MiB in flight on 256 CUs, which measured fastest: 4 loads in
+// flight or more resident blocks per CU read 3-16% slower.
 extern "C" __global__ __launch_bounds__(256) void xpu_peak_read(const xpu::u32x4 *__restrict__ input,
                                                                 uint32_t *__restrict__ sink, uint64_t count) {
   const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
   uint32_t acc = 0;
   uint64_t i = tid;
-  for (; i + 3 * stride < count; i += 4 * stride) {
-    const xpu::u32x4 v0 = xpu::load_nt16(input + i);
-    const xpu::u32x4 v1 = xpu::load_nt16(input + i + stride);
-    const xpu::u32x4 v2 = xpu::load_nt16(input + i + 2 * stride);
-    const xpu::u32x4 v3 = xpu::load_nt16(input + i + 3 * stride);
-    acc ^= (v0.x ^ v1.y) ^ (v2.z ^ v3.w);
+  for (; i + 7 * stride < count; i += 8 * stride) {
+    xpu::u32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = xpu::load_nt16(input + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].w;
   }
   for (; i < count; i += stride) {
     const xpu::u32x4 v = xpu::load_nt16(input + i);

@@ -178,7 +178,7 @@ extern "C" int run_peak_mem(int argc, char **argv) {
     xpu_runtime *rt = guard.rt;
     std::cout << "Device: " << rt->name << " (" << rt->arch << ", " << rt->compute_units << " CUs)\n";
     const uint64_t bytes = o.size_mib << 20;
-    const uint32_t blocks = rt->compute_units * 8;
+    const uint32_t blocks = rt->compute_units;  // one block per CU (kernels/peak.hip)
     check(xpu_rt_require_device_and_memory(rt, bytes + blocks * 1024ull));
     void *input = nullptr, *sink = nullptr;
     check(xpu_rt_alloc(rt, bytes, 4096, &input));
