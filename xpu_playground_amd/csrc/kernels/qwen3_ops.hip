@@ -626,12 +626,17 @@ XPU_Q3_REG_SET(8)
 // One block per query head: QK-norm + RoPE of q and of its kv head's k; the
 // first query head of each group writes k and v into the engine caches at
 // position state[0]; then attention over positions 0..state[0].
+// cos_row / sin_row are the RoPE table rows of position state[0] (the engine
+// keeps them in a fixed buffer, rewritten whenever the position changes), so
+// that no load before the QK-norm depends on the position.
 //
 // Contexts of up to kAttnTile positions (thread t <-> position t) take four
-// block barriers: every load is issued at entry without branches (q/k rows,
-// norm gains and cos/sin first, so the QK-norm / RoPE of waves 0 and 1 only
-// waits for those; then the thread's K row from the chunk-major cache and
-// its V pieces in the P.V layout); the softmax maximum goes through one LDS
+// block barriers: the loads that do not depend on the position are issued at
+// entry without branches (q/k rows, norm gains and cos/sin first, so the
+// QK-norm / RoPE of waves 0 and 1 only waits for those; then the thread's K
+// row from the chunk-major cache), the position is first used after barrier
+// 1; the V pieces in the P.V layout are loaded after the scores, so that they
+// do not queue ahead of the K rows; the softmax maximum goes through one LDS
 // exchange; the canonical denominator is folded in registers (the 8 slots
 // of canonical lane L are the exponentials of positions 8 L .. 8 L + 7,
 // held by 8 consecutive lanes, folded with quad permutations and a half-row
@@ -640,8 +645,8 @@ XPU_Q3_REG_SET(8)
 // attention_tail_short. Longer contexts use attention_head.
 extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
     const uint16_t *__restrict__ qkv, const uint16_t *__restrict__ qnorm_w,
-    const uint16_t *__restrict__ knorm_w, const uint16_t *__restrict__ rope_cos,
-    const uint16_t *__restrict__ rope_sin, uint16_t *__restrict__ kcache,
+    const uint16_t *__restrict__ knorm_w, const uint16_t *__restrict__ cos_row,
+    const uint16_t *__restrict__ sin_row, uint16_t *__restrict__ kcache,
     uint16_t *__restrict__ vcache, uint16_t *__restrict__ out, const uint32_t *__restrict__ state,
     uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float eps, float scale,
     const uint16_t *__restrict__ prefetch, uint64_t prefetch_bytes, uint32_t prefetch_delay) {
@@ -674,12 +679,8 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
     asm volatile("" : : "v"(acc));  // keeps the loads
     return;
   }
-  const uint32_t pos = state[0];
-  if (pos >= max_seq) return;
   const uint32_t group = heads / kv_heads;
   const uint32_t kv = head / group;
-  const uint16_t *cos_row = rope_cos + static_cast<uint64_t>(pos) * xpu::kHeadDim;
-  const uint16_t *sin_row = rope_sin + static_cast<uint64_t>(pos) * xpu::kHeadDim;
   const uint16_t *qsrc = qkv + head * xpu::kHeadDim;
   const uint16_t *ksrc = qkv + (heads + kv) * xpu::kHeadDim;
   const uint16_t *vsrc = qkv + (heads + kv_heads + kv) * xpu::kHeadDim;
@@ -687,8 +688,6 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
   const uint64_t kchunk = static_cast<uint64_t>(max_seq) * 8u;  // chunk-major K cache
-  const uint32_t n = pos + 1;
-  const bool short_ctx = n <= xpu::kAttnTile;
   // QK-norm / RoPE operands (waves 0: q, 1: k; lanes 0..15 used)
   const uint32_t l16 = lane & 15u;
   const u32x4 hx = *reinterpret_cast<const u32x4 *>((wave == 0 ? qsrc : ksrc) + l16 * 8u);
@@ -698,27 +697,22 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   const u32x4 hv = *reinterpret_cast<const u32x4 *>(vsrc + l16 * 8u);  // the new v row
   __builtin_amdgcn_sched_barrier(0);  // these five loads go out first
   // K row of position tid (clamped into the cache; positions >= pos are
-  // replaced below) and V pieces: lane l of wave w owns residue class
-  // cls = 4 w + l / 16 and dims 8 (l % 16) .. + 7; vpv[it] = V[16 it + cls]
-  // (the current position's v from qkv; entries past pos are not used)
-  u32x4 krow[16], vpv[xpu::kAttnTile / 16];
+  // replaced below)
+  u32x4 krow[16];
   xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(min(tid, max_seq - 1)) * 8u, krow, kchunk);
-  const uint32_t cls = wave * 4u + (lane >> 4), dim0 = l16 * 8u;
-#pragma unroll
-  for (int it = 0; it < static_cast<int>(xpu::kAttnTile / 16); ++it) {
-    const uint32_t t = it * 16u + cls;
-    const uint16_t *src = t < pos ? vcache + head_base + static_cast<uint64_t>(t) * xpu::kHeadDim : vsrc;
-    vpv[it] = *reinterpret_cast<const u32x4 *>(src + dim0);  // unused past pos
-  }
   {
     // every wave evaluates a QK-norm / RoPE (waves 2 and 3 into scratch) so
-    // that the four operand loads stay ahead of the K / V loads
+    // that the four operand loads stay ahead of the K loads
     const bool active = lane < 16;
     const u32x4 zero{0, 0, 0, 0};
     xpu::head_norm_rope_vec(active ? hx : zero, active ? hw : zero, hc, hs, eps,
                             wave == 0 ? qs : wave == 1 ? ks : junk + (wave - 2) * xpu::kHeadDim);
   }
   __syncthreads();  // 1: qs, ks
+  const uint32_t pos = state[0];
+  if (pos >= max_seq) return;  // the reference skips the step (kernels.hpp:74-75)
+  const uint32_t n = pos + 1;
+  const bool short_ctx = n <= xpu::kAttnTile;
   if (head % group == 0 && tid < 16) {
     // the new k (chunk-major) and v (head-major) at position pos
     *reinterpret_cast<u32x4 *>(kcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) =
@@ -734,6 +728,17 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   // scores (the current position from ks) and the block maximum
   if (tid == pos) xpu::load_head_row(ks, krow);
   const float sc = tid < n ? xpu::attention_score_regs(qs, krow, scale) : -__builtin_inff();
+  // V pieces: lane l of wave w owns residue class cls = 4 w + l / 16 and
+  // dims 8 (l % 16) .. + 7; vpv[it] = V[16 it + cls] (the current position's
+  // v from qkv; entries past pos are not used)
+  u32x4 vpv[xpu::kAttnTile / 16];
+  const uint32_t cls = wave * 4u + (lane >> 4), dim0 = l16 * 8u;
+#pragma unroll
+  for (int it = 0; it < static_cast<int>(xpu::kAttnTile / 16); ++it) {
+    const uint32_t t = it * 16u + cls;
+    const uint16_t *src = t < pos ? vcache + head_base + static_cast<uint64_t>(t) * xpu::kHeadDim : vsrc;
+    vpv[it] = *reinterpret_cast<const u32x4 *>(src + dim0);
+  }
   const float wmax = xpu::wave_reduce(sc, [](float x, float y) { return fmaxf(x, y); });
   if (lane == 0) red[wave] = wmax;
   __syncthreads();  // 2: wave maxima
@@ -787,9 +792,21 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
 extern "C" __global__ __launch_bounds__(1024) void xpu_q3_argmax_finish(
     const float *__restrict__ part_val, const uint32_t *__restrict__ part_idx,
     const uint32_t *__restrict__ part_bad, uint32_t nparts, uint32_t *state,
-    const uint32_t *__restrict__ prompt, uint32_t *__restrict__ gen, uint32_t gen_capacity) {
+    const uint32_t *__restrict__ prompt, uint32_t *__restrict__ gen, uint32_t gen_capacity,
+    const uint16_t *__restrict__ rope_cos, const uint16_t *__restrict__ rope_sin,
+    uint16_t *__restrict__ rope_row, uint32_t max_seq) {
   __shared__ float redv[16];
   __shared__ uint32_t redi[16], redb[16];
+  {
+    // the RoPE rows of the next position into rope_row (cos, then sin), read
+    // by the next step's attention kernels; state[0] is read here, before the
+    // barriers of block_argmax, and advanced by thread 0 after them
+    const uint32_t next_pos = state[0] + 1;
+    const uint32_t i = threadIdx.x;
+    if (next_pos < max_seq && i < 2 * xpu::kHeadDim)
+      rope_row[i] = i < xpu::kHeadDim ? rope_cos[static_cast<uint64_t>(next_pos) * xpu::kHeadDim + i]
+                                      : rope_sin[static_cast<uint64_t>(next_pos) * xpu::kHeadDim + i - xpu::kHeadDim];
+  }
   float best = -__builtin_inff();
   uint32_t best_index = 0xffffffffu, bad = 0;
   for (uint32_t i = threadIdx.x; i < nparts; i += blockDim.x) {

@@ -133,6 +133,7 @@ struct xpu_qwen3 {
   uint16_t *kcache = nullptr, *vcache = nullptr, *cos_t = nullptr, *sin_t = nullptr;
   uint16_t *x = nullptr, *qkv = nullptr, *attn = nullptr, *h = nullptr, *up = nullptr, *logits = nullptr;
   uint16_t *norm = nullptr, *tmp = nullptr;
+  uint16_t *rope_row = nullptr;  // cos and sin rows of the decode position state[0]
   float *part_val = nullptr;
   uint32_t *part_idx = nullptr, *part_bad = nullptr, *state = nullptr, *prompt = nullptr, *gen = nullptr;
   uint32_t *ref_token = nullptr;
@@ -191,6 +192,7 @@ int allocate_buffers(xpu_qwen3 &e) {
       {reinterpret_cast<void **>(&e.part_idx), e.nparts * 4ull},
       {reinterpret_cast<void **>(&e.part_bad), e.nparts * 4ull},
       {reinterpret_cast<void **>(&e.state), 64},
+      {reinterpret_cast<void **>(&e.rope_row), 2ull * c.head_dim * 2},
       {reinterpret_cast<void **>(&e.prompt), e.max_seq * 4ull},
       {reinterpret_cast<void **>(&e.gen), e.max_seq * 4ull},
       {reinterpret_cast<void **>(&e.ref_token), 4},
@@ -386,6 +388,7 @@ int enqueue_fused_step(xpu_qwen3 &e) {
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
   const uint64_t cache_layer = uint64_t{kv} * max_seq * c.head_dim;
   const uint16_t *no_embed = nullptr;
+  const uint16_t *sin_row = e.rope_row + c.head_dim;
   int rc;
   for (uint32_t l = 0; l < c.layers; ++l) {
     const Layer &L = e.layers[l];
@@ -405,7 +408,7 @@ int enqueue_fused_step(xpu_qwen3 &e) {
         std::min<uint64_t>(e.pf_cap, static_cast<uint64_t>(pf_end - reinterpret_cast<const uint8_t *>(L.o)));
     const uint32_t pf_delay = e.pf_delay;
     if ((rc = launch(e, e.attn_l, 256,
-                     {{8, &e.qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &kc},
+                     {{8, &e.qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.rope_row}, {8, &sin_row}, {8, &kc},
                       {8, &vc}, {8, &e.attn}, {8, &e.state}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps},
                       {4, &scale}, {8, &pf}, {8, &pf_bytes}, {4, &pf_delay}})))
       return rc;
@@ -422,7 +425,8 @@ int enqueue_fused_step(xpu_qwen3 &e) {
   const uint32_t nparts = e.logits_l.grid;
   return launch(e, e.finish_l, 1024,
                 {{8, &e.part_val}, {8, &e.part_idx}, {8, &e.part_bad}, {4, &nparts}, {8, &e.state},
-                 {8, &e.prompt}, {8, &e.gen}, {4, &max_seq}});
+                 {8, &e.prompt}, {8, &e.gen}, {4, &max_seq}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &e.rope_row},
+                 {4, &max_seq}});
 }
 
 // K/V cache entries of prompt positions [0, P) (prompt ids already in
@@ -477,6 +481,16 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
     }
   }
   return XPU_OK;
+}
+
+// The fused step's attention kernels read the RoPE rows of the position in
+// e.rope_row; xpu_q3_argmax_finish advances them with the position, and this
+// sets them wherever the host writes the position.
+int set_rope_row(xpu_qwen3 &e, uint32_t position) {
+  const uint64_t hd = e.c.head_dim, at = uint64_t{position} * hd;
+  int rc = xpu_rt_copy_device(e.rt, e.rope_row, e.cos_t + at, hd * 2);
+  if (!rc) rc = xpu_rt_copy_device(e.rt, e.rope_row + hd, e.sin_t + at, hd * 2);
+  return rc;
 }
 
 int run_fused_step(xpu_qwen3 &e) {
@@ -882,6 +896,7 @@ extern "C" int xpu_qwen3_decode(xpu_qwen3 *eng, uint32_t token, uint32_t positio
   } else {
     const uint32_t st[4] = {position, token, 0, 0};
     if ((rc = xpu_rt_copy_to_device(eng->rt, eng->state, st, sizeof(st)))) return rc;
+    if ((rc = set_rope_row(*eng, position))) return rc;
     if ((rc = run_fused_step(*eng))) return rc;
     uint32_t back[4];
     if ((rc = xpu_rt_copy_from_device(eng->rt, back, eng->state, sizeof(back)))) return rc;
@@ -942,6 +957,7 @@ extern "C" int xpu_qwen3_generate(xpu_qwen3 *eng, const uint32_t *prompt, uint32
     const uint32_t first = eng->batched_prefill ? n_prompt - 1 : 0;
     const uint32_t st[4] = {first, prompt[first], 0, n_prompt};
     if ((rc = xpu_rt_copy_to_device(eng->rt, eng->state, st, sizeof(st)))) return rc;
+    if ((rc = set_rope_row(*eng, first))) return rc;
     void *ev[3] = {nullptr, nullptr, nullptr};
     for (auto &v : ev)
       if ((rc = xpu_rt_event_create(eng->rt, &v))) return rc;
