@@ -329,7 +329,12 @@ int setup_launches(xpu_qwen3 &e) {
   if ((rc = pick("xpu_q3_gemv_residual_r1", c.intermediate, residual_kernel(c.intermediate), e.down_l))) return rc;
   e.down_l.grid = std::min(cap, (c.hidden + 3) / 4);
   if ((rc = pick("xpu_q3_norm_gemv_logits_r2", c.hidden, "xpu_q3_norm_gemv_logits_r2", e.logits_l))) return rc;
-  e.logits_l.grid = std::min(e.nparts, (c.vocab + 7) / 8);
+  // two blocks per CU: 8 MiB of lm_head rows in flight on 256 CUs, the
+  // streaming optimum (8 blocks per CU, or a second row buffer per
+  // wavefront, read slower)
+  e.logits_l.grid = std::min(std::min(e.nparts, e.rt->compute_units * 2), (c.vocab + 7) / 8);
+  if (const char *g = std::getenv("XPU_Q3_LOGITS_BLOCKS"); g && *g)
+    e.logits_l.grid = std::max(1u, std::min({e.nparts, (c.vocab + 7) / 8, static_cast<uint32_t>(std::strtoul(g, nullptr, 10))}));
   if ((rc = find("xpu_q3_argmax_finish", e.finish_l))) return rc;
   e.finish_l.grid = 1;
   for (auto *l : {&e.qkv_l, &e.o_l, &e.gu_l, &e.down_l, &e.logits_l})
