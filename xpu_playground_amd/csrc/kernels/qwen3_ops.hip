@@ -662,9 +662,9 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
     // (the weights of the kernels that follow) so that they come from the
     // Infinity Cache, not HBM, when those kernels run; the attention itself
     // occupies only `heads` compute units for its latency-bound duration.
-    // start after prefetch_delay x 64 x 16 cycles, behind the attention's
+    // start after prefetch_delay x 64 x 8 cycles, behind the attention's
     // own loads
-    for (uint32_t d = 0; d < prefetch_delay; ++d) __builtin_amdgcn_s_sleep(16);
+    for (uint32_t d = 0; d < prefetch_delay; ++d) __builtin_amdgcn_s_sleep(8);
     const uint64_t n16 = prefetch_bytes / 16u;
     const u32x4 *p = reinterpret_cast<const u32x4 *>(prefetch);
     const uint64_t stride = static_cast<uint64_t>(gridDim.x - heads) * blockDim.x;

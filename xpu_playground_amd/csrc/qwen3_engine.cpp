@@ -142,7 +142,7 @@ struct xpu_qwen3 {
   // weight prefetch by the attention kernel's spare blocks: byte cap and
   // start delay (XPU_Q3_PREFETCH_MB, XPU_Q3_PREFETCH_DELAY)
   uint64_t pf_cap = ~uint64_t{0};
-  uint32_t pf_delay = 2;
+  uint32_t pf_delay = 1;
   bool pf_next = false;
   // fused-path geometry
   struct Launch {
@@ -312,7 +312,7 @@ int setup_launches(xpu_qwen3 &e) {
     const char *cap = std::getenv("XPU_Q3_PREFETCH_MB"), *delay = std::getenv("XPU_Q3_PREFETCH_DELAY");
     const char *next = std::getenv("XPU_Q3_PREFETCH_NEXT");
     e.pf_cap = cap && *cap ? std::strtoull(cap, nullptr, 10) << 20 : ~uint64_t{0};
-    e.pf_delay = delay && *delay ? static_cast<uint32_t>(std::strtoul(delay, nullptr, 10)) : 2u;
+    e.pf_delay = delay && *delay ? static_cast<uint32_t>(std::strtoul(delay, nullptr, 10)) : 1u;  // ~512 cycles
     e.pf_next = next && *next == '1';
   }
   // LDS-staged residual GEMVs: the whole row in one batch of loads when K is
