@@ -161,4 +161,42 @@ XPU_DEVICE u32x4 load_nt16(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 }
 
+// ------------------------------------------------ global -> LDS DMA (gfx950)
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor: 48-bit base, stride 0, num_records bytes, 32-bit
+// data format. Offsets at or past num_records read as zero.
+XPU_DEVICE i32x4 rsrc(const void *base, int64_t records) {
+  records = records < 0 ? 0 : (records > 0x7fffffff ? 0x7fffffff : records);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4{static_cast<int>(a & 0xffffffffu), static_cast<int>((a >> 32) & 0xffffu),
+               static_cast<int>(records), 0x00020000};
+}
+
+// 16 bytes per lane from the buffer at voff into LDS at m0 + 16 * lane (m0
+// wave-uniform). Written as asm so that the compiler's wait-count pass,
+// which does not track these writes, does not wait for every DMA before each
+// LDS read; callers issue the waits themselves (wait_vmcnt, then a barrier
+// before other wavefronts read the data).
+XPU_DEVICE void dma16(uint32_t m0, const i32x4 &r, uint32_t voff) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(r), "{m0}"(m0)
+               : "memory");
+}
+
+template <int N> XPU_DEVICE void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  // gfx9 s_waitcnt: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14; expcnt and
+  // lgkmcnt at their maxima (no wait)
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS byte address of a __shared__ object
+XPU_DEVICE uint32_t lds_addr(const void *p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)p));
+}
+
 }  // namespace xpu

@@ -46,7 +46,6 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr uint32_t kBM = 256;
@@ -62,33 +61,6 @@ XPU_DEVICE f32x16 mfma(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// Raw buffer descriptor: 48-bit base, stride 0, num_records bytes, 32-bit
-// data format. Offsets at or past num_records read as zero.
-XPU_DEVICE i32x4 rsrc(const void *base, int64_t records) {
-  records = records < 0 ? 0 : (records > 0x7fffffff ? 0x7fffffff : records);
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  return i32x4{static_cast<int>(a & 0xffffffffu), static_cast<int>((a >> 32) & 0xffffu),
-               static_cast<int>(records), 0x00020000};
-}
-
-// 16 bytes per lane from the buffer at voff into LDS at m0 + 16 * lane.
-// Written as asm so that the compiler's wait-count pass, which cannot tell
-// the stages apart, does not wait for every DMA before each LDS read; the
-// loop below issues the waits itself.
-XPU_DEVICE void dma16(uint32_t m0, const i32x4 &r, uint32_t voff) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voff), "s"(r), "{m0}"(m0)
-               : "memory");
-}
-
-template <int N> XPU_DEVICE void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  // gfx9 s_waitcnt: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14; expcnt and
-  // lgkmcnt at their maxima (no wait)
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 // XOR swizzles of 16-byte chunks. A: row r of the tile (2 BK bytes), B:
 // row k (512 bytes). With them the rows read by one ds_read_b128 (32 rows,
 // one chunk column) and the 4 x 4 (row, chunk) blocks read by one
@@ -99,11 +71,6 @@ template <int BK> XPU_DEVICE uint32_t a_swz(uint32_t r) {
   else return ((r >> 1) & 3u) ^ ((r >> 3) & 1u);
 }
 XPU_DEVICE uint32_t b_swz(uint32_t k) { return ((k & 1u) ? 10u : 0u) ^ ((k & 2u) ? 4u : 0u); }
-
-XPU_DEVICE uint32_t lds_addr(const void *p) {
-  return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)p));
-}
 
 struct TileCoord {
   uint32_t tm, tn;
