@@ -371,9 +371,23 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
         *reinterpret_cast<u32x4 *>(dst) = packed;  // n_out % 8 == 0: n + 7 < n_out
       } else {
         const uint32_t w[4] = {packed.x, packed.y, packed.z, packed.w};
+        if (n + 8u <= n_out && (reinterpret_cast<uintptr_t>(dst) & 3u) == 0) {
+          // 4-byte aligned: four dword stores
+          uint32_t *d32 = reinterpret_cast<uint32_t *>(dst);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (n + e < n_out) dst[e] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+          for (int i = 0; i < 4; ++i) d32[i] = w[i];
+        } else if (n + 8u <= n_out) {
+          // 2 bytes past a 4-byte boundary: element 0, three dwords, element 7
+          dst[0] = static_cast<uint16_t>(w[0]);
+          uint32_t *d32 = reinterpret_cast<uint32_t *>(dst + 1);
+#pragma unroll
+          for (int i = 0; i < 3; ++i) d32[i] = (w[i] >> 16) | (w[i + 1] << 16);
+          dst[7] = static_cast<uint16_t>(w[3] >> 16);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n + e < n_out) dst[e] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+        }
       }
     }
     __builtin_amdgcn_wave_barrier();
