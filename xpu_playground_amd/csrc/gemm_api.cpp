@@ -18,14 +18,31 @@ uint64_t round_up8(uint64_t v) { return (v + 7) & ~uint64_t{7}; }
 // Copies a rows x cols matrix (row stride src_ld) into dst with dst_cols
 // columns, zero-filling columns cols..dst_cols-1 (kernels/gemm.hip
 // xpu_pad_rows).
+uint32_t pad_grid(const xpu_runtime *rt, uint32_t rows, uint32_t dst_cols) {
+  const uint64_t threads = static_cast<uint64_t>(rows) * (dst_cols / 8);
+  return std::max(1u, static_cast<uint32_t>(std::min<uint64_t>((threads + 255) / 256, rt->compute_units * 16ull)));
+}
+
 int pad_rows(xpu_runtime *rt, const void *src, uint64_t src_ld, uint32_t rows, uint32_t cols, void *dst,
              uint32_t dst_cols) {
   const xpu::KernelInfo *k = rt->find_exact("xpu_pad_rows");
   if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: xpu_pad_rows");
-  const uint64_t threads = static_cast<uint64_t>(rows) * (dst_cols / 8);
-  const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>((threads + 255) / 256, rt->compute_units * 16ull));
   const xpu_kernel_arg args[] = {{8, &src}, {8, &src_ld}, {4, &rows}, {4, &cols}, {8, &dst}, {4, &dst_cols}};
-  return rt->launch(*k, std::max(grid, 1u), 1, 256, 0, args, 6);
+  return rt->launch(*k, pad_grid(rt, rows, dst_cols), 1, 256, 0, args, 6);
+}
+
+// Both operands in one launch (xpu_pad_rows2), the blocks split in
+// proportion to the two pad_rows grids.
+int pad_rows2(xpu_runtime *rt, const void *src_a, uint64_t ld_a, uint32_t rows_a, uint32_t cols_a, void *dst_a,
+              uint32_t dst_cols_a, const void *src_b, uint64_t ld_b, uint32_t rows_b, uint32_t cols_b, void *dst_b,
+              uint32_t dst_cols_b) {
+  const xpu::KernelInfo *k = rt->find_exact("xpu_pad_rows2");
+  if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: xpu_pad_rows2");
+  const uint32_t blocks_a = pad_grid(rt, rows_a, dst_cols_a), blocks_b = pad_grid(rt, rows_b, dst_cols_b);
+  const xpu_kernel_arg args[] = {{8, &src_a}, {8, &ld_a},   {4, &rows_a},     {4, &cols_a}, {8, &dst_a},
+                                 {4, &dst_cols_a}, {8, &src_b}, {8, &ld_b}, {4, &rows_b}, {4, &cols_b},
+                                 {8, &dst_b}, {4, &dst_cols_b}, {4, &blocks_a}};
+  return rt->launch(*k, blocks_a + blocks_b, 1, 256, 0, args, 13);
 }
 
 }  // namespace
@@ -51,15 +68,17 @@ extern "C" int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B
     void *ws = nullptr;
     int rc = rt->scratch(a_bytes + b_bytes, &ws);
     if (rc) return rc;
-    if (!a_direct) {
+    void *bp = static_cast<char *>(ws) + a_bytes;
+    if (!a_direct && !b_direct) {
+      if ((rc = pad_rows2(rt, A, K, M, K, ws, static_cast<uint32_t>(kp), B, N, K, N, bp, static_cast<uint32_t>(np))))
+        return rc;
+    } else if (!a_direct) {
       if ((rc = pad_rows(rt, A, K, M, K, ws, static_cast<uint32_t>(kp)))) return rc;
-      a_use = ws;
+    } else if ((rc = pad_rows(rt, B, N, K, N, bp, static_cast<uint32_t>(np)))) {
+      return rc;
     }
-    if (!b_direct) {
-      void *bp = static_cast<char *>(ws) + a_bytes;
-      if ((rc = pad_rows(rt, B, N, K, N, bp, static_cast<uint32_t>(np)))) return rc;
-      b_use = bp;
-    }
+    if (!a_direct) a_use = ws;
+    if (!b_direct) b_use = bp;
   }
   const uint32_t k_run = static_cast<uint32_t>(a_direct ? K : kp);  // reduction length seen by the kernel
   const uint32_t n_run = static_cast<uint32_t>(b_direct ? N : np);  // columns of the B operand

@@ -422,13 +422,14 @@ XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dmau, xpu::kFp16, 4, 64, 2, 4, 2, 1, false)
 // one element earlier plus the chunk's last element, shifted into place.
 // The chunk holding the row's end is read element by element, so no load
 // reaches past the last element of a row.
-extern "C" __global__ __launch_bounds__(256) void xpu_pad_rows(const uint16_t *__restrict__ src, uint64_t src_ld,
-                                                               uint32_t rows, uint32_t cols,
-                                                               uint16_t *__restrict__ dst, uint32_t dst_cols) {
+namespace xpu {
+// Blocks block0 .. block0 + nblocks - 1 of the grid copy one matrix.
+XPU_DEVICE void pad_rows(const uint16_t *__restrict__ src, uint64_t src_ld, uint32_t rows, uint32_t cols,
+                         uint16_t *__restrict__ dst, uint32_t dst_cols, uint32_t block0, uint32_t nblocks) {
   const uint64_t chunks_per_row = dst_cols / 8u;
   const uint64_t total = static_cast<uint64_t>(rows) * chunks_per_row;
-  for (uint64_t idx = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+  for (uint64_t idx = static_cast<uint64_t>(blockIdx.x - block0) * blockDim.x + threadIdx.x; idx < total;
+       idx += static_cast<uint64_t>(nblocks) * blockDim.x) {
     const uint64_t r = idx / chunks_per_row;
     const uint32_t c0 = static_cast<uint32_t>(idx % chunks_per_row) * 8u;
     const uint16_t *p = src + r * src_ld + c0;
@@ -454,4 +455,23 @@ extern "C" __global__ __launch_bounds__(256) void xpu_pad_rows(const uint16_t *_
     }
     *reinterpret_cast<xpu::u32x4 *>(dst + r * dst_cols + c0) = v;
   }
+}
+}  // namespace xpu
+
+extern "C" __global__ __launch_bounds__(256) void xpu_pad_rows(const uint16_t *__restrict__ src, uint64_t src_ld,
+                                                               uint32_t rows, uint32_t cols,
+                                                               uint16_t *__restrict__ dst, uint32_t dst_cols) {
+  xpu::pad_rows(src, src_ld, rows, cols, dst, dst_cols, 0, gridDim.x);
+}
+
+// Both GEMM operands in one launch: blocks 0 .. blocks_a - 1 copy the first
+// matrix, the others the second (same layout rules as xpu_pad_rows).
+extern "C" __global__ __launch_bounds__(256) void xpu_pad_rows2(
+    const uint16_t *__restrict__ src_a, uint64_t ld_a, uint32_t rows_a, uint32_t cols_a, uint16_t *__restrict__ dst_a,
+    uint32_t dst_cols_a, const uint16_t *__restrict__ src_b, uint64_t ld_b, uint32_t rows_b, uint32_t cols_b,
+    uint16_t *__restrict__ dst_b, uint32_t dst_cols_b, uint32_t blocks_a) {
+  if (blockIdx.x < blocks_a)
+    xpu::pad_rows(src_a, ld_a, rows_a, cols_a, dst_a, dst_cols_a, 0, blocks_a);
+  else
+    xpu::pad_rows(src_b, ld_b, rows_b, cols_b, dst_b, dst_cols_b, blocks_a, gridDim.x - blocks_a);
 }
