@@ -2,7 +2,7 @@
 // accumulation (reference: gemv_kernel.hpp:21-63, entries
 // level_zero/gem_spv_entry.cpp:11-27 with argument order (A, x, y, m, k)).
 //
-// Launch: 256 threads (4 wavefronts); dynamic LDS = round_up(K, 512) * 2
+// Launch: 256 threads (4 wavefronts, fixed at compile time); dynamic LDS = round_up(K, 512) * 2
 // bytes for the staged vector; the grid walks tiles of 4*R rows with a
 // grid-stride loop so each block stages the vector once. Any M, K >= 1 and
 // any leading dimension lda >= K are accepted; the _vec variants need A, x
@@ -20,14 +20,15 @@ XPU_DEVICE void gemv_entry(const uint16_t *__restrict__ A, const uint16_t *__res
                            uint16_t *__restrict__ y, uint32_t M, uint32_t K, uint64_t lda) {
   extern __shared__ __align__(16) uint16_t lds_x[];
   const uint16_t *xs = x;
+  constexpr uint32_t kBlock = 256;  // launched with 256 threads (gemv_api.cpp)
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t rows_per_block = (kBlock >> 6) * R;
   if constexpr (!XG) {
     const uint32_t kpad = (K + 511u) & ~511u;
-    stage_vector<VEC>(lds_x, x, K, kpad);
+    stage_vector<VEC, kBlock>(lds_x, x, K, kpad);
     __syncthreads();
     xs = lds_x;
   }
-  const uint32_t wave = threadIdx.x >> 6;
-  const uint32_t rows_per_block = (blockDim.x >> 6) * R;
   for (uint32_t base = blockIdx.x * rows_per_block; base < M; base += gridDim.x * rows_per_block) {
     const uint32_t row0 = base + wave * R;
     if (row0 >= M) continue;

@@ -15,10 +15,32 @@
 namespace xpu {
 
 // Copy x[0..K) into LDS zero-padded to kpad (a multiple of 512 codes).
-template <bool VEC>
-XPU_DEVICE void stage_vector(uint16_t *xs, const uint16_t *__restrict__ x, uint32_t K,
-                             uint32_t kpad) {
-  for (uint32_t i = threadIdx.x * 8u; i < kpad; i += blockDim.x * 8u) {
+// BLOCK: the launch's block size when fixed at compile time (0: read
+// blockDim.x, a load from the dispatch packet that the first loads would
+// wait for). VEC (K % 8 == 0, x 16-byte aligned): four 16-byte loads per
+// thread are issued before their LDS writes (a chunk past K, or past kpad,
+// reads the last chunk of x; past K it writes zeros, past kpad nothing).
+template <bool VEC, uint32_t BLOCK = 0>
+XPU_DEVICE void stage_vector(uint16_t *xs, const uint16_t *__restrict__ x, uint32_t K, uint32_t kpad) {
+  const uint32_t threads = BLOCK ? BLOCK : blockDim.x;
+  if constexpr (VEC) {
+    const uint32_t step = threads * 8u;
+    for (uint32_t i0 = threadIdx.x * 8u; i0 < kpad; i0 += 4u * step) {
+      u32x4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t i = i0 + u * step;
+        v[u] = *reinterpret_cast<const u32x4 *>(x + (i < K ? i : K - 8u));  // branch-free
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t i = i0 + u * step;
+        if (i < kpad) *reinterpret_cast<u32x4 *>(xs + i) = i < K ? v[u] : u32x4{0, 0, 0, 0};
+      }
+    }
+    return;
+  }
+  for (uint32_t i = threadIdx.x * 8u; i < kpad; i += threads * 8u) {
     u32x4 v;
     if (VEC && i + 8u <= K) {
       v = *reinterpret_cast<const u32x4 *>(x + i);
