@@ -795,8 +795,15 @@ extern "C" __global__ __launch_bounds__(1024) void xpu_q3_argmax_finish(
     const uint32_t *__restrict__ prompt, uint32_t *__restrict__ gen, uint32_t gen_capacity,
     const uint16_t *__restrict__ rope_cos, const uint16_t *__restrict__ rope_sin,
     uint16_t *__restrict__ rope_row, uint32_t max_seq) {
+  constexpr uint32_t kBlock = 1024;  // launched with 1024 threads
   __shared__ float redv[16];
   __shared__ uint32_t redi[16], redb[16];
+  float best = -__builtin_inff();
+  uint32_t best_index = 0xffffffffu, bad = 0;
+  for (uint32_t i = threadIdx.x; i < nparts; i += kBlock) {
+    bad |= part_bad[i];
+    xpu::argmax_merge(best, best_index, part_val[i], part_idx[i]);
+  }
   {
     // the RoPE rows of the next position into rope_row (cos, then sin), read
     // by the next step's attention kernels; state[0] is read here, before the
@@ -806,12 +813,6 @@ extern "C" __global__ __launch_bounds__(1024) void xpu_q3_argmax_finish(
     if (next_pos < max_seq && i < 2 * xpu::kHeadDim)
       rope_row[i] = i < xpu::kHeadDim ? rope_cos[static_cast<uint64_t>(next_pos) * xpu::kHeadDim + i]
                                       : rope_sin[static_cast<uint64_t>(next_pos) * xpu::kHeadDim + i - xpu::kHeadDim];
-  }
-  float best = -__builtin_inff();
-  uint32_t best_index = 0xffffffffu, bad = 0;
-  for (uint32_t i = threadIdx.x; i < nparts; i += blockDim.x) {
-    bad |= part_bad[i];
-    xpu::argmax_merge(best, best_index, part_val[i], part_idx[i]);
   }
   xpu::block_argmax(best, best_index, bad, redv, redi, redb);
   if (threadIdx.x == 0) {
