@@ -293,17 +293,24 @@ XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const 
     for (int j = 0; j < 16; ++j) *reinterpret_cast<u32x4 *>(vtile + slot * kVPitch + j * 8) = vv[j];
   };
   // pass 1: scores (kept in sbuf when one chunk holds them all) and the max;
-  // a single-tile context also stages its V rows here
+  // a single-tile context also stages its V rows here. Thread tid takes
+  // positions tid, tid + 256, ... (kAttnChunk is a multiple of 256); the K
+  // row of its next position is loaded before the current score is computed.
+  static_assert(kAttnChunk % kAttnTile == 0, "chunks hold whole tiles");
   float local_max = -__builtin_inff();
-  for (uint32_t c = 0; c < nchunks; ++c) {
-    const uint32_t base = c * kAttnChunk;
-    const uint32_t len = min(kAttnChunk, n - base);
-    for (uint32_t i = tid; i < len; i += blockDim.x) {
-      const float s = score_of(base + i);
-      if (single_tile) stage_v_row(base + i, i);
-      sbuf[i] = s;
-      local_max = fmaxf(local_max, s);
-    }
+  u32x4 knext[16];
+  if (tid < n) load_head_row(kbase + static_cast<uint64_t>(tid) * lay.kstride, knext, lay.kchunk);
+  for (uint32_t t = tid; t < n; t += kAttnTile) {
+    u32x4 kcur_row[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) kcur_row[j] = knext[j];
+    if (t + kAttnTile < n)
+      load_head_row(kbase + static_cast<uint64_t>(t + kAttnTile) * lay.kstride, knext, lay.kchunk);
+    const float s = (HAS_CURRENT && t + 1 == n) ? attention_score(qs, kcur, scale)
+                                                 : attention_score_regs(qs, kcur_row, scale);
+    if (single_tile) stage_v_row(t, t);
+    sbuf[t % kAttnChunk] = s;
+    local_max = fmaxf(local_max, s);
   }
   attention_tail<HAS_CURRENT>(qs, kbase, vbase, lay, n, kcur, vcur, scale, out, sbuf, vtile, red, local_max);
 }
@@ -326,13 +333,23 @@ XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const 
   auto vrow_of = [&](uint32_t t) -> const uint16_t * {
     return (HAS_CURRENT && t + 1 == n) ? vcur : vbase + static_cast<uint64_t>(t) * lay.vstride;
   };
-  auto stage_v_row = [&](uint32_t t, uint32_t slot) {
-    const uint16_t *src = vrow_of(t);
-    u32x4 vv[16];
+  // a tile of tlen V rows from position t0: thread tid holds chunk tid % 16
+  // of rows 16 j + tid / 16 (16 lanes per row, so one load instruction
+  // covers 4 whole rows)
+  const uint32_t v_chunk = tid & 15u, v_row0 = tid >> 4;
+  auto load_v_tile = [&](uint32_t t0, uint32_t tlen, u32x4 (&vv)[16]) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) vv[j] = *reinterpret_cast<const u32x4 *>(src + j * 8);
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t r = j * 16u + v_row0;
+      if (r < tlen) vv[j] = *reinterpret_cast<const u32x4 *>(vrow_of(t0 + r) + v_chunk * 8u);
+    }
+  };
+  auto store_v_tile = [&](uint32_t tlen, const u32x4 (&vv)[16]) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) *reinterpret_cast<u32x4 *>(vtile + slot * kVPitch + j * 8) = vv[j];
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t r = j * 16u + v_row0;
+      if (r < tlen) *reinterpret_cast<u32x4 *>(vtile + r * kVPitch + v_chunk * 8u) = vv[j];
+    }
   };
   const float mx = block_max(local_max, red);
   // pass 2: exponentials and the chunked canonical sum
@@ -376,11 +393,17 @@ XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const 
     }
     __syncthreads();
     float part[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+    // V tiles of 256 rows go through vtile; the next tile's row of this
+    // thread is loaded into registers while the current tile is used
+    u32x4 vnext[16];
+    if (!single_tile) load_v_tile(base, min(kAttnTile, len), vnext);
     for (uint32_t i0 = 0; i0 < len; i0 += kAttnTile) {
       const uint32_t tile_len = min(kAttnTile, len - i0);
       if (!single_tile) {
-        if (tid < tile_len) stage_v_row(base + i0 + tid, tid);
+        store_v_tile(tile_len, vnext);
         __syncthreads();
+        const uint32_t next_len = i0 + kAttnTile < len ? min(kAttnTile, len - i0 - kAttnTile) : 0u;
+        if (next_len) load_v_tile(base + i0 + kAttnTile, next_len, vnext);
       }
       for (uint32_t ii = 0; ii < tile_len; ii += 16u) {
         float pt[4];
