@@ -47,6 +47,32 @@ def test_gemm_small_shapes(rt, dtype, m, n, k):
     check(gpu_gemm(rt, a, b, m, n, k, dtype), a, b, m, n, k, dtype)
 
 
+@pytest.mark.parametrize("dtype", [xpu.BF16, xpu.FP16])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (255, 257, 65), (64, 40, 24)])
+def test_gemm_pointers_two_bytes_past_alignment(rt, dtype, m, n, k):
+    # A, B and C start 2 bytes past a 16-byte boundary: both operands go
+    # through the padding copy from 2-byte aligned rows, and every C row starts
+    # 2 bytes past a dword (or a 16-byte) boundary, the unaligned-C epilogue's
+    # cases. Guard codes around C catch any store outside it.
+    print(f"gemm unaligned pointers dtype={dtype} {m}x{n}x{k}", flush=True)
+    a = orc.uniform(m * k, 30 + m, dtype)
+    b = orc.uniform(k * n, 40 + n, dtype)
+    guard = 0x7E7E
+    pa, pb, pc = rt.alloc(m * k * 2 + 64), rt.alloc(k * n * 2 + 64), rt.alloc(m * n * 2 + 64)
+    try:
+        rt.copy_to(pc, np.full((m * n * 2 + 64) // 2, guard, np.uint16))
+        rt.copy_to(pa + 2, a)
+        rt.copy_to(pb + 2, b)
+        rt.gemm(dtype, pa + 2, pb + 2, pc + 2, m, n, k)
+        rt.synchronize()
+        out = rt.download(pc, (m * n * 2 + 64) // 2, np.uint16)
+    finally:
+        for p in (pa, pb, pc):
+            rt.free(p)
+    assert out[0] == guard and np.all(out[1 + m * n:] == guard)
+    check(out[1:1 + m * n].reshape(m, n), a, b, m, n, k, dtype)
+
+
 def test_gemm_constant_known_answer(rt):
     # gemm.cpp:81-85,109-117 (and level_zero/peak_l0.cpp:910-917,936-943)
     for dtype, (m, n, k) in [(0, (4096, 4096, 4096)), (1, (3000, 4097, 2050))]:
