@@ -107,6 +107,17 @@ int xpu_qwen3_set_mode(xpu_qwen3 *eng, int mode);
  * batched is requested for an unsupported shape. */
 int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int batched);
 
+/* Attention of the graph and eager modes for contexts of at least
+ * min_context positions (position + 1 >= min_context) runs split over
+ * compute units: a scores kernel over 256-position tiles and a P.V kernel
+ * per 16 output dims, with the same operations in the same order as the
+ * one-block-per-head kernel, so results are bit-identical; each variant has
+ * its own captured graph. 0 never splits. Default 257 (environment
+ * XPU_Q3_SPLIT_FROM at creation overrides it). No reference counterpart:
+ * the reference's Attention (qwen3/kernels.hpp:157-192) is one serial loop
+ * per head. XPU_ERR_INVALID when the module lacks the kernels. */
+int xpu_qwen3_set_attention_split(xpu_qwen3 *eng, uint32_t min_context);
+
 /* One forward step at `position` for input `token`; *next = greedy token
  * (Engine::decode, main.cpp:159-226). A non-finite logit fails with
  * XPU_ERR_VERIFY ("model produced a NaN or infinity", main.cpp:223-224). */

@@ -51,17 +51,52 @@ def test_generate_small_config_all_modes_agree(rt):
     eng.close()
 
 
-def test_attention_past_one_softmax_chunk(rt):
-    # positions beyond 4096 take the chunked (recomputing) attention path
+@pytest.mark.parametrize("split_from", [0, 257])
+def test_attention_past_one_softmax_chunk(rt, split_from):
+    # positions beyond 4096 take the chunked (recomputing) attention path, in
+    # one block per head (split_from 0) or split over compute units
     cfg = orc.config("tiny", layers=1, vocab=512)
     n_prompt = 4100
     prompt = orc.tokens(n_prompt, 6, cfg.vocab)
     m = orc.Model(cfg, seed=8, gain_std=0.1, max_seq=n_prompt + 4)
     ref, logits = m.generate(prompt, 4, logit_steps=4)
     eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=n_prompt + 4, seed=8, gain_std=0.1, runtime=rt)
+    eng.set_attention_split(split_from)
     out, _, _ = eng.generate(prompt, 4, stop_on_eos=False)
     assert out.tolist() == ref.tolist()
     assert np.array_equal(eng.logits(), logits[3])
+    eng.close()
+
+
+@pytest.mark.parametrize("mode", [qwen3.GRAPH, qwen3.EAGER])
+@pytest.mark.parametrize("split_from", [0, 1, 257])
+def test_split_attention_every_position_matches_oracle(rt, mode, split_from):
+    # 16 query / 8 kv heads (the 0.6B grouping): every position 0..299 through
+    # decode, with the attention split over compute units never, at every
+    # step, or from the 257th position on (both captured graphs in one run)
+    cfg = orc.config("small", layers=1, vocab=1024)
+    max_seq = 304
+    m = orc.Model(cfg, seed=6, gain_std=0.1, max_seq=max_seq)
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=max_seq, seed=6, gain_std=0.1, runtime=rt)
+    eng.set_mode(mode)
+    eng.set_attention_split(split_from)
+    prompt = orc.tokens(160, 12, cfg.vocab)
+    token = int(prompt[0])
+    print(f"mode={mode} split_from={split_from}", flush=True)
+    for pos in range(300):
+        ref_tok, ref_logits = m.decode(token, pos, want_logits=True)
+        tok = eng.decode(token, pos)
+        assert np.array_equal(eng.logits(), ref_logits), pos
+        assert tok == ref_tok, pos
+        token = int(prompt[pos + 1]) if pos + 1 < len(prompt) else tok
+    eng.close()
+
+
+def test_split_attention_setter(rt):
+    cfg = orc.config("tiny")
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=16, seed=1, gain_std=0.1, runtime=rt)
+    for v in (0, 1, 257, 1 << 20):
+        eng.set_attention_split(v)
     eng.close()
 
 

@@ -240,15 +240,15 @@ XPU_DEVICE float attention_score(const uint16_t *qs, const uint16_t *krow, float
   return attention_score_regs(qs, kv, scale);
 }
 
-// Cache addressing of one kv head: K row t chunk j at kbase + t * kstride +
-// j * kchunk, V row t at vbase + t * vstride (contiguous). The reference
-// layout [position][kv_head][128] has kstride = vstride = kv_heads * 128,
-// kchunk = 8; the engine's K cache is chunk-major [kv_head][16][max_seq][8]
-// (kstride = 8, kchunk = max_seq * 8: the chunk j of consecutive positions
-// is contiguous, so a lane-per-position read is coalesced) and its V cache
-// head-major [kv_head][max_seq][128] (vstride = 128).
+// Cache addressing of one kv head: K row t chunk j (8 codes) at kbase +
+// t * kstride + j * kchunk, V row t chunk j at vbase + t * vstride +
+// j * vchunk. The reference layout [position][kv_head][128] has kstride =
+// vstride = kv_heads * 128, kchunk = vchunk = 8; the engine's K and V caches
+// are chunk-major [kv_head][16][max_seq][8] (stride 8, chunk max_seq * 8:
+// chunk j of consecutive positions is contiguous, so a lane-per-position K
+// read is coalesced and a block that owns a few dims of V reads whole lines).
 struct KvLayout {
-  uint64_t kstride, kchunk, vstride;
+  uint64_t kstride, kchunk, vstride, vchunk;
 };
 
 constexpr uint32_t kAttnTile = 256;             // positions per V tile in LDS
@@ -281,14 +281,18 @@ XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const 
     if (HAS_CURRENT && t + 1 == n) return attention_score(qs, kcur, scale);
     return attention_score(qs, kbase + static_cast<uint64_t>(t) * lay.kstride, scale, lay.kchunk);
   };
+  // V row t: chunk j at vrow_of(t) + j * vchunk_of(t) (the new token's row,
+  // kept contiguous in vcur, when HAS_CURRENT and t is the last position)
   auto vrow_of = [&](uint32_t t) -> const uint16_t * {
     return (HAS_CURRENT && t + 1 == n) ? vcur : vbase + static_cast<uint64_t>(t) * lay.vstride;
   };
+  auto vchunk_of = [&](uint32_t t) -> uint64_t { return (HAS_CURRENT && t + 1 == n) ? 8u : lay.vchunk; };
   auto stage_v_row = [&](uint32_t t, uint32_t slot) {
     const uint16_t *src = vrow_of(t);
+    const uint64_t vc = vchunk_of(t);
     u32x4 vv[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) vv[j] = *reinterpret_cast<const u32x4 *>(src + j * 8);
+    for (int j = 0; j < 16; ++j) vv[j] = *reinterpret_cast<const u32x4 *>(src + j * vc);
 #pragma unroll
     for (int j = 0; j < 16; ++j) *reinterpret_cast<u32x4 *>(vtile + slot * kVPitch + j * 8) = vv[j];
   };
@@ -333,6 +337,7 @@ XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const 
   auto vrow_of = [&](uint32_t t) -> const uint16_t * {
     return (HAS_CURRENT && t + 1 == n) ? vcur : vbase + static_cast<uint64_t>(t) * lay.vstride;
   };
+  auto vchunk_of = [&](uint32_t t) -> uint64_t { return (HAS_CURRENT && t + 1 == n) ? 8u : lay.vchunk; };
   // a tile of tlen V rows from position t0: thread tid holds chunk tid % 16
   // of rows 16 j + tid / 16 (16 lanes per row, so one load instruction
   // covers 4 whole rows)
@@ -341,7 +346,7 @@ XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const 
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const uint32_t r = j * 16u + v_row0;
-      if (r < tlen) vv[j] = *reinterpret_cast<const u32x4 *>(vrow_of(t0 + r) + v_chunk * 8u);
+      if (r < tlen) vv[j] = *reinterpret_cast<const u32x4 *>(vrow_of(t0 + r) + v_chunk * vchunk_of(t0 + r));
     }
   };
   auto store_v_tile = [&](uint32_t tlen, const u32x4 (&vv)[16]) {

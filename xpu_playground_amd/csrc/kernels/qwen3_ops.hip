@@ -16,9 +16,9 @@
 //   xpu_q3_norm_gemv_logits final RMSNorm + tied lm_head + per-block argmax
 //   xpu_q3_argmax_finish    argmax, next token, position advance
 // The decode position and token live in device memory (state[0], state[1])
-// so one captured graph serves every step. Engine caches: K chunk-major
-// [kv_head][16][max_seq][8] (eight-element chunk j of every position
-// contiguous), V head-major [kv_head][max_seq][128].
+// so one captured graph serves every step. Engine caches: K and V
+// chunk-major [kv_head][16][max_seq][8] (eight-element chunk j of every
+// position contiguous).
 #include "qwen3_core.hpp"
 
 using xpu::u32x4;
@@ -112,7 +112,7 @@ extern "C" __global__ __launch_bounds__(256) void QwenAttention(
   __syncthreads();
   const uint64_t stride = static_cast<uint64_t>(kv_heads) * xpu::kHeadDim;
   xpu::attention_head<false>(qs, key_cache + kv * xpu::kHeadDim, value_cache + kv * xpu::kHeadDim,
-                             xpu::KvLayout{stride, 8, stride}, position + 1, nullptr, nullptr, 0.08838834764831845f,
+                             xpu::KvLayout{stride, 8, stride, 8}, position + 1, nullptr, nullptr, 0.08838834764831845f,
                              output + head * xpu::kHeadDim, sbuf, vtile, red);
 }
 
@@ -630,7 +630,7 @@ XPU_Q3_REG_SET(8)
 // keeps them in a fixed buffer, rewritten whenever the position changes), so
 // that no load before the QK-norm depends on the position.
 //
-// Contexts of up to kAttnTile positions (thread t <-> position t) take four
+// Contexts of up to kAttnTile positions (thread t <-> position t) take three
 // block barriers: the loads that do not depend on the position are issued at
 // entry without branches (q/k rows, norm gains and cos/sin first, so the
 // QK-norm / RoPE of waves 0 and 1 only waits for those; then the thread's K
@@ -641,8 +641,10 @@ XPU_Q3_REG_SET(8)
 // of canonical lane L are the exponentials of positions 8 L .. 8 L + 7,
 // held by 8 consecutive lanes, folded with quad permutations and a half-row
 // mirror) and its 64-lane butterfly is evaluated by every wave from LDS;
-// then P.V and the fixed class tree. Same operations in the same order as
-// attention_tail_short. Longer contexts use attention_head.
+// then P.V (lane <-> residue class, wave <-> four cache chunks) and the fixed
+// class tree across the 16 lanes of a chunk. Same operations in the same
+// order as attention_tail_short. Longer contexts use attention_head, or the
+// split kernels below.
 extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
     const uint16_t *__restrict__ qkv, const uint16_t *__restrict__ qnorm_w,
     const uint16_t *__restrict__ knorm_w, const uint16_t *__restrict__ cos_row,
@@ -714,30 +716,31 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   const uint32_t n = pos + 1;
   const bool short_ctx = n <= xpu::kAttnTile;
   if (head % group == 0 && tid < 16) {
-    // the new k (chunk-major) and v (head-major) at position pos
+    // the new k and v (chunk-major) at position pos
     *reinterpret_cast<u32x4 *>(kcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) =
         *reinterpret_cast<const u32x4 *>(ks + tid * 8u);
-    *reinterpret_cast<u32x4 *>(vcache + head_base + static_cast<uint64_t>(pos) * xpu::kHeadDim + tid * 8u) = hv;
+    *reinterpret_cast<u32x4 *>(vcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) = hv;
   }
   if (!short_ctx) {
     xpu::attention_head<true>(qs, kcache + head_base, vcache + head_base,
-                              xpu::KvLayout{8u, kchunk, xpu::kHeadDim}, n, ks, vsrc, scale,
+                              xpu::KvLayout{8u, kchunk, 8u, kchunk}, n, ks, vsrc, scale,
                               out + head * xpu::kHeadDim, sbuf, vtile, red);
     return;
   }
   // scores (the current position from ks) and the block maximum
   if (tid == pos) xpu::load_head_row(ks, krow);
   const float sc = tid < n ? xpu::attention_score_regs(qs, krow, scale) : -__builtin_inff();
-  // V pieces: lane l of wave w owns residue class cls = 4 w + l / 16 and
-  // dims 8 (l % 16) .. + 7; vpv[it] = V[16 it + cls] (the current position's
-  // v from qkv; entries past pos are not used)
+  // V pieces: lane l of wave w owns residue class cls = l % 16 and cache
+  // chunk vch = 4 w + l / 16 (dims 8 vch .. + 7); vpv[it] = V[16 it + cls]
+  // (the current position's v from qkv; entries past pos are not used), so
+  // a load instruction reads 256 contiguous bytes of each of 4 chunks
   u32x4 vpv[xpu::kAttnTile / 16];
-  const uint32_t cls = wave * 4u + (lane >> 4), dim0 = l16 * 8u;
+  const uint32_t cls = l16, vch = wave * 4u + (lane >> 4);
 #pragma unroll
   for (int it = 0; it < static_cast<int>(xpu::kAttnTile / 16); ++it) {
     const uint32_t t = it * 16u + cls;
-    const uint16_t *src = t < pos ? vcache + head_base + static_cast<uint64_t>(t) * xpu::kHeadDim : vsrc;
-    vpv[it] = *reinterpret_cast<const u32x4 *>(src + dim0);
+    const uint16_t *src = t < pos ? vcache + head_base + vch * kchunk + static_cast<uint64_t>(t) * 8u : vsrc + vch * 8u;
+    vpv[it] = *reinterpret_cast<const u32x4 *>(src);
   }
   const float wmax = xpu::wave_reduce(sc, [](float x, float y) { return fmaxf(x, y); });
   if (lane == 0) red[wave] = wmax;
@@ -766,21 +769,271 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
       for (int e = 0; e < 8; ++e) part[e] = __builtin_fmaf(pt, v[e], part[e]);
     }
   }
-  float sum[8];
+  // the class tree over the 16 lanes of a chunk: (c0 + c1), then
+  // ((c0 + c1) + (c2 + c3)), then the two quads of eight (half-row mirror:
+  // the values are uniform within a quad), then the two eights
+  uint32_t code[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float pair = part[e] + xpu::xor16_f(part[e]);  // (c0 + c1), (c2 + c3)
-    sum[e] = pair + xpu::xor32_f(pair);                   // (c0 + c1) + (c2 + c3)
+    float v = part[e];
+    v = v + xpu::dpp_f<0xB1>(v);   // xor 1
+    v = v + xpu::dpp_f<0x4E>(v);   // xor 2
+    v = v + xpu::dpp_f<0x141>(v);  // row_half_mirror
+    v = v + xpu::xor8_f(v);
+    code[e] = xpu::f32_to_bf16(v);
   }
-  float *wsum = sbuf + xpu::kAttnTile;  // 4 x 128 wave partials, past the exponentials
-  if (lane < 16) {
+  if (cls == 0)
+    *reinterpret_cast<u32x4 *>(out + head * xpu::kHeadDim + vch * 8u) =
+        u32x4{code[0] | (code[1] << 16), code[2] | (code[3] << 16), code[4] | (code[5] << 16), code[6] | (code[7] << 16)};
+}
+
+// Attention split over compute units (two kernels, for long contexts): the
+// operations and their order are those of xpu_q3_attention /
+// attention_head (qwen3/kernels.hpp:157-192 with transformers rounding), so
+// results are bit-identical; the work of one head is spread over many
+// blocks because one compute unit's load path bounds a block that reads a
+// long K/V history.
+//
+// Block b of both kernels serves kv head b % kv_heads, query head
+// kv_head * group + (b / kv_heads) % group and part (b / kv_heads) / group,
+// so with 8 kv heads and round-robin dispatch over 8 XCDs all blocks of a
+// kv head share one L2.
+XPU_DEVICE void split_block(uint32_t b, uint32_t heads, uint32_t kv_heads, uint32_t &kv, uint32_t &head,
+                            uint32_t &part) {
+  const uint32_t group = heads / kv_heads, rest = b / kv_heads;
+  kv = b % kv_heads;
+  head = kv * group + rest % group;
+  part = rest / group;
+}
+
+// Part 1: QK-norm + RoPE of q and of its kv head's k (every block; the
+// first query head of each group with part 0 writes k and v into the caches
+// at position state[0]), then the scores of the 256-position tiles
+// part, part + parts, ... (thread t <-> position tile * 256 + t, the current
+// position from the freshly roped k) into scores[head * spitch + t], and the
+// block's maximum into maxima[head * parts + part] (-inf without a tile).
+// grid = heads * parts; cos_row / sin_row as for xpu_q3_attention.
+extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_scores(
+    const uint16_t *__restrict__ qkv, const uint16_t *__restrict__ qnorm_w,
+    const uint16_t *__restrict__ knorm_w, const uint16_t *__restrict__ cos_row,
+    const uint16_t *__restrict__ sin_row, uint16_t *__restrict__ kcache,
+    uint16_t *__restrict__ vcache, float *__restrict__ scores, float *__restrict__ maxima,
+    const uint32_t *__restrict__ state, uint32_t heads, uint32_t kv_heads, uint32_t max_seq,
+    uint32_t spitch, uint32_t parts, float eps, float scale) {
+  __shared__ float red[4];
+  __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
+  __shared__ __align__(16) uint16_t ks[xpu::kHeadDim];
+  __shared__ __align__(16) uint16_t junk[2 * xpu::kHeadDim];
+  uint32_t kv, head, part;
+  split_block(blockIdx.x, heads, kv_heads, kv, head, part);
+  const uint32_t group = heads / kv_heads;
+  const uint16_t *qsrc = qkv + head * xpu::kHeadDim;
+  const uint16_t *ksrc = qkv + (heads + kv) * xpu::kHeadDim;
+  const uint16_t *vsrc = qkv + (heads + kv_heads + kv) * xpu::kHeadDim;
+  const uint32_t tid = threadIdx.x, lane = xpu::lane_id();
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
+  const uint64_t kchunk = static_cast<uint64_t>(max_seq) * 8u;  // chunk-major K cache
+  const uint32_t l16 = lane & 15u;
+  const u32x4 hx = *reinterpret_cast<const u32x4 *>((wave == 0 ? qsrc : ksrc) + l16 * 8u);
+  const u32x4 hw = *reinterpret_cast<const u32x4 *>((wave == 0 ? qnorm_w : knorm_w) + l16 * 8u);
+  const u32x4 hc = *reinterpret_cast<const u32x4 *>(cos_row + l16 * 8u);
+  const u32x4 hs = *reinterpret_cast<const u32x4 *>(sin_row + l16 * 8u);
+  const u32x4 hv = *reinterpret_cast<const u32x4 *>(vsrc + l16 * 8u);
+  __builtin_amdgcn_sched_barrier(0);  // these five loads go out first
+  // K row of this thread's position in the block's first tile (clamped into
+  // the cache; positions past the context are not used)
+  u32x4 knext[16];
+  xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(min(part * 256u + tid, max_seq - 1)) * 8u, knext,
+                     kchunk);
+  {
+    const bool active = lane < 16;
+    const u32x4 zero{0, 0, 0, 0};
+    xpu::head_norm_rope_vec(active ? hx : zero, active ? hw : zero, hc, hs, eps,
+                            wave == 0 ? qs : wave == 1 ? ks : junk + (wave - 2) * xpu::kHeadDim);
+  }
+  __syncthreads();  // qs, ks
+  const uint32_t pos = state[0];
+  if (pos >= max_seq) return;  // the reference skips the step (kernels.hpp:74-75)
+  const uint32_t n = pos + 1, ntiles = (n + 255u) / 256u;
+  if (head % group == 0 && part == 0 && tid < 16) {
+    *reinterpret_cast<u32x4 *>(kcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) =
+        *reinterpret_cast<const u32x4 *>(ks + tid * 8u);
+    *reinterpret_cast<u32x4 *>(vcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) = hv;
+  }
+  float *srow = scores + static_cast<uint64_t>(head) * spitch;
+  float local_max = -__builtin_inff();
+  for (uint32_t tile = part; tile < ntiles; tile += parts) {
+    u32x4 kcur[16];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) wsum[wave * xpu::kHeadDim + lane * 8u + e] = sum[e];
+    for (int j = 0; j < 16; ++j) kcur[j] = knext[j];
+    if (tile + parts < ntiles)  // the next tile's row, loaded while this one is scored
+      xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(min((tile + parts) * 256u + tid, max_seq - 1)) * 8u,
+                         knext, kchunk);
+    const uint32_t t = tile * 256u + tid;
+    if (t < n) {
+      const float s = t == pos ? xpu::attention_score(qs, ks, scale) : xpu::attention_score_regs(qs, kcur, scale);
+      srow[t] = s;
+      local_max = fmaxf(local_max, s);
+    }
   }
-  __syncthreads();  // 4: wave partials
-  if (tid < xpu::kHeadDim) {
-    const float r = (wsum[tid] + wsum[xpu::kHeadDim + tid]) + (wsum[2 * xpu::kHeadDim + tid] + wsum[3 * xpu::kHeadDim + tid]);
-    out[head * xpu::kHeadDim + tid] = static_cast<uint16_t>(xpu::f32_to_bf16(r));
+  const float wmax = xpu::wave_reduce(local_max, [](float x, float y) { return fmaxf(x, y); });
+  if (lane == 0) red[wave] = wmax;
+  __syncthreads();
+  if (tid == 0) maxima[head * parts + part] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Part 2: block (kv head, query head, dim group g) of grid heads * 8 owns
+// dims 16 g .. 16 g + 15 of its head's output. Every block rebuilds the
+// softmax maximum (from the parts' maxima) and the canonical denominator
+// (chunks of kAttnChunk positions: lane L adds the exponentials of
+// positions 512 j + 8 L + e of the chunk into slot e, the chunk sum is the
+// 8 -> 1 fold and 64-lane butterfly, chunk sums are added in order), then
+// p_t = bf16(exp(s_t - max) * (1 / sum)) and, for each of its 16 dims, the
+// 16 residue-class FMA chains over ascending t (one chain per chunk, chunks
+// added in order), combined by the fixed class tree ((c0 + c1) + (c2 + c3))
+// ... as attention_tail does. The exponentials of a chunk are computed once
+// by all threads into LDS; the block's 32-byte slice of the V rows goes
+// through registers into LDS in 1024-row tiles, each tile loaded while the
+// previous one's chains run; the chains take their operands 16 steps at a
+// time from LDS. spitch: a multiple of 512.
+extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_pv(
+    const float *__restrict__ scores, const float *__restrict__ maxima, const uint16_t *__restrict__ vcache,
+    uint16_t *__restrict__ out, const uint32_t *__restrict__ state, uint32_t heads, uint32_t kv_heads,
+    uint32_t max_seq, uint32_t spitch, uint32_t parts) {
+  constexpr uint32_t kDims = 16, kChunk = xpu::kAttnChunk, kTile = 1024, kRows = kTile / 128, kMaxChunks = 64;
+  constexpr uint32_t kPer = kChunk / 256, kBatch = 16;
+  extern __shared__ __align__(16) uint8_t pv_lds[];
+  float *pbuf = reinterpret_cast<float *>(pv_lds);                           // kChunk floats
+  uint16_t *vt = reinterpret_cast<uint16_t *>(pv_lds + kChunk * 4);         // kChunk x 16 codes
+  float *csum = reinterpret_cast<float *>(pv_lds + kChunk * 4 + kChunk * kDims * 2);
+  float *wsum = csum + kMaxChunks;                                           // 4 x 16
+  uint32_t kv, head, g;
+  split_block(blockIdx.x, heads, kv_heads, kv, head, g);
+  const uint32_t tid = threadIdx.x, lane = xpu::lane_id();
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const float pm = maxima[head * parts + min(lane, parts - 1)];
+  const uint32_t pos = state[0];
+  if (pos >= max_seq) return;
+  const uint32_t n = pos + 1, nchunks = (n + kChunk - 1) / kChunk;
+  const float *srow = scores + static_cast<uint64_t>(head) * spitch;
+  // the chunk's scores (16 per thread, positions tid + 256 k, index clamped)
+  auto load_s = [&](uint32_t base, uint32_t len, float (&sv)[kPer]) {
+#pragma unroll
+    for (int k = 0; k < static_cast<int>(kPer); ++k) sv[k] = srow[base + min(tid + 256u * k, len - 1)];
+  };
+  // V rows from the chunk-major cache (dims 16 g .. 16 g + 15 are cache
+  // chunks 2 g and 2 g + 1): waves 0, 1 read chunk 2 g and waves 2, 3 chunk
+  // 2 g + 1, lane l of wave w rows 128 k + 64 (w % 2) + l of a tile, so a
+  // load instruction reads 1 KiB contiguous. The loads go through a buffer
+  // descriptor that ends at the context: rows past it read zeros without a
+  // memory access, and no load is behind a branch (which would make the
+  // compiler wait for all earlier loads before each one).
+  const uint32_t vr = (wave & 1u) * 64u + lane, vh = (wave >> 1) * 8u;
+  const uint16_t *vb = vcache + static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim +
+                       static_cast<uint64_t>(2u * g + (wave >> 1)) * max_seq * 8u;
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(vb), static_cast<short>(0), static_cast<int>(n * 16u),
+                                        0x00020000);
+  auto load_tile = [&](uint32_t t0, u32x4 (&vv)[kRows]) {  // rows t0 .. t0 + 1023 of the context
+#pragma unroll
+    for (int k = 0; k < static_cast<int>(kRows); ++k)
+      vv[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, (t0 + k * 128u + vr) * 16u, 0, 0));
+  };
+  auto store_tile = [&](uint32_t r0, const u32x4 (&vv)[kRows]) {  // into chunk rows r0 .. r0 + 1023
+#pragma unroll
+    for (int k = 0; k < static_cast<int>(kRows); ++k)
+      *reinterpret_cast<u32x4 *>(vt + (r0 + k * 128u + vr) * kDims + vh) = vv[k];
+  };
+  float sv[kPer];
+  u32x4 vv[kRows];
+  load_s(0, min(kChunk, n), sv);
+  load_tile(0, vv);
+  const float mx = xpu::wave_reduce(pm, [](float x, float y) { return fmaxf(x, y); });
+  auto exps = [&](uint32_t len, const float (&s)[kPer], bool scaled, float sinv) {
+#pragma unroll
+    for (int k = 0; k < static_cast<int>(kPer); ++k) {
+      const uint32_t i = tid + 256u * k;
+      if (i < len) {
+        const float e = xpu::canonical_exp(s[k] - mx);
+        pbuf[i] = scaled ? xpu::round_bf16(e * sinv) : e;
+      }
+    }
+  };
+  for (uint32_t c = 0; c < nchunks; ++c) {
+    const uint32_t base = c * kChunk, len = min(kChunk, n - base);
+    if (c) {
+      float sc[kPer];
+      load_s(base, len, sc);
+      exps(len, sc, false, 0.0f);
+    } else {
+      exps(len, sv, false, 0.0f);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (uint32_t j = 0; j < len; j += 512u) {
+        const float4 a = *reinterpret_cast<const float4 *>(pbuf + j + lane * 8u);
+        const float4 b = *reinterpret_cast<const float4 *>(pbuf + j + lane * 8u + 4u);
+        const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (j + lane * 8u + e < len) acc[e] = acc[e] + x[e];
+      }
+      const float cs = xpu::wave_butterfly(xpu::fold8(acc));
+      if (lane == 0) csum[c] = cs;
+    }
+    __syncthreads();
+  }
+  float total = 0.0f;
+  for (uint32_t c = 0; c < nchunks; ++c) total = total + csum[c];
+  const float inv = 1.0f / total;
+  // P.V: lane l of wave w owns residue class 4 w + l / 16 and dim l % 16
+  const uint32_t cls = wave * 4u + (lane >> 4), d = lane & 15u;
+  float tot = 0.0f;
+  for (uint32_t c = 0; c < nchunks; ++c) {
+    const uint32_t base = c * kChunk, len = min(kChunk, n - base);
+    if (c) {
+      __syncthreads();  // the previous chunk's probabilities and rows are no longer read
+      float sc[kPer];
+      load_s(base, len, sc);
+      exps(len, sc, true, inv);
+    } else if (nchunks == 1) {
+      for (uint32_t i = tid; i < len; i += 256u) pbuf[i] = xpu::round_bf16(pbuf[i] * inv);
+    } else {
+      exps(len, sv, true, inv);
+    }
+    float part = 0.0f;
+    for (uint32_t i0 = 0; i0 < len; i0 += kTile) {
+      store_tile(i0, vv);  // a region of the chunk's rows that no chain reads yet
+      load_tile(base + i0 + kTile, vv);  // the next tile (zeros past the context)
+      __syncthreads();  // the tile (and the chunk's probabilities) in LDS
+      // rows i0 + cls, i0 + cls + 16, ... of the tile, 16 at a time: the
+      // operands of a batch are read before its FMAs
+      const uint32_t tend = min(i0 + kTile, len);
+      uint32_t t0 = i0 + cls;
+      for (; t0 + 16u * (kBatch - 1) < tend; t0 += 16u * kBatch) {
+        float pp[kBatch];
+        uint32_t v[kBatch];
+#pragma unroll
+        for (int u = 0; u < static_cast<int>(kBatch); ++u) {
+          pp[u] = pbuf[t0 + 16u * u];
+          v[u] = vt[(t0 + 16u * u) * kDims + d];
+        }
+#pragma unroll
+        for (int u = 0; u < static_cast<int>(kBatch); ++u) part = __builtin_fmaf(pp[u], xpu::bf16_to_f32(v[u]), part);
+      }
+      for (; t0 < tend; t0 += 16u) part = __builtin_fmaf(pbuf[t0], xpu::bf16_to_f32(vt[t0 * kDims + d]), part);
+    }
+    tot = tot + part;
+  }
+  const float pair = tot + xpu::xor16_f(tot);  // (c0 + c1), (c2 + c3)
+  const float sum = pair + xpu::xor32_f(pair); // (c0 + c1) + (c2 + c3)
+  if (lane < 16) wsum[wave * kDims + lane] = sum;
+  __syncthreads();
+  if (tid < kDims) {
+    const float r = (wsum[tid] + wsum[kDims + tid]) + (wsum[2 * kDims + tid] + wsum[3 * kDims + tid]);
+    out[head * xpu::kHeadDim + g * kDims + tid] = static_cast<uint16_t>(xpu::f32_to_bf16(r));
   }
 }
 
@@ -1011,14 +1264,14 @@ extern "C" __global__ __launch_bounds__(64) void xpu_q3_pf_rope_cache(
     hc = *reinterpret_cast<const u32x4 *>(rope_cos + static_cast<uint64_t>(pos) * xpu::kHeadDim + lane * 8u);
     hs = *reinterpret_cast<const u32x4 *>(rope_sin + static_cast<uint64_t>(pos) * xpu::kHeadDim + lane * 8u);
   }
-  const uint64_t slot = (static_cast<uint64_t>(kvh) * max_seq + pos) * xpu::kHeadDim;
-  // K: chunk-major [kv_head][16][max_seq][8]
+  // K and V: chunk-major [kv_head][16][max_seq][8]
   const uint64_t kslot = static_cast<uint64_t>(kvh) * max_seq * xpu::kHeadDim + static_cast<uint64_t>(pos) * 8u;
   uint16_t *dst = is_q ? Q + static_cast<uint64_t>(t) * heads * xpu::kHeadDim + h * xpu::kHeadDim : kcache + kslot;
   xpu::head_norm_rope_vec(hx, hw, hc, hs, eps, dst, is_q ? 8u : static_cast<uint64_t>(max_seq) * 8u);
   if (!is_q && lane < 16) {
     const uint16_t *vsrc = row + (heads + kv_heads + kvh) * xpu::kHeadDim;
-    *reinterpret_cast<u32x4 *>(vcache + slot + lane * 8u) = *reinterpret_cast<const u32x4 *>(vsrc + lane * 8u);
+    *reinterpret_cast<u32x4 *>(vcache + kslot + lane * static_cast<uint64_t>(max_seq) * 8u) =
+        *reinterpret_cast<const u32x4 *>(vsrc + lane * 8u);
   }
 }
 
@@ -1039,6 +1292,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_attention(
   __syncthreads();
   const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
   xpu::attention_head<false>(qs, kcache + head_base, vcache + head_base,
-                             xpu::KvLayout{8u, static_cast<uint64_t>(max_seq) * 8u, xpu::kHeadDim}, p0 + t + 1, nullptr,
+                             xpu::KvLayout{8u, static_cast<uint64_t>(max_seq) * 8u, 8u, static_cast<uint64_t>(max_seq) * 8u},
+                             p0 + t + 1, nullptr,
                              nullptr, scale, A + qoff, sbuf, vtile, red);
 }

@@ -11,9 +11,9 @@
 // Memory layout (one arena, 4 KiB aligned tensors as in model.cpp:481-491):
 // per layer [q; k; v] projection (rows q then k then v), o_proj, [gate; up]
 // (2I x H), down_proj, the four norm gains; then embed_tokens, the final norm
-// and, when untied, lm_head. KV caches bf16: K [layer][kv_head][16][max_seq][8]
-// (chunk-major), V [layer][kv_head][max_seq][128] (the reference-mode
-// kernels use [layer][max_seq][kv_head][128] for both).
+// and, when untied, lm_head. KV caches bf16: K and V chunk-major
+// [layer][kv_head][16][max_seq][8] (the reference-mode kernels use
+// [layer][max_seq][kv_head][128] for both).
 #include "../../include/xpu_qwen3.h"
 #include "../../include/xpu_kernels.h"
 #include "host_common.hpp"
@@ -139,6 +139,13 @@ struct xpu_qwen3 {
   uint32_t *ref_token = nullptr;
   uint32_t nparts = 0;
   void *graph = nullptr;
+  // attention split over compute units (xpu_q3_attn_scores + xpu_q3_attn_pv)
+  // for contexts of at least split_from positions (0: never), with its own
+  // graph; scores [heads][att_spitch] and maxima [heads][att_parts]
+  bool split_ok = false;
+  uint32_t split_from = 257, att_spitch = 0, att_parts = 0;
+  float *att_scores = nullptr, *att_max = nullptr;
+  void *graph_split = nullptr;
   // weight prefetch by the attention kernel's spare blocks: byte cap and
   // start delay (XPU_Q3_PREFETCH_MB, XPU_Q3_PREFETCH_DELAY)
   uint64_t pf_cap = ~uint64_t{0};
@@ -148,7 +155,7 @@ struct xpu_qwen3 {
   struct Launch {
     const xpu::KernelInfo *k = nullptr;
     uint32_t grid = 0, shared = 0;
-  } qkv_l, attn_l, o_l, gu_l, down_l, logits_l, finish_l;
+  } qkv_l, attn_l, scores_l, pv_l, o_l, gu_l, down_l, logits_l, finish_l;
   // batched prefill (kernels/qwen3_ops.hip part 3): chunk buffers of
   // pf_chunk tokens; pf_ok when the shape has kernels for every projection
   bool pf_ok = false, batched_prefill = false;
@@ -161,6 +168,7 @@ struct xpu_qwen3 {
 
   ~xpu_qwen3() {
     if (graph) xpu_rt_graph_destroy(graph);
+    if (graph_split) xpu_rt_graph_destroy(graph_split);
     if (rt) {
       for (void *p : {static_cast<void *>(arena), static_cast<void *>(kcache), static_cast<void *>(vcache),
                       static_cast<void *>(cos_t), static_cast<void *>(sin_t), static_cast<void *>(x), pf_block})
@@ -179,6 +187,8 @@ int allocate_buffers(xpu_qwen3 &e) {
   const uint64_t cache = uint64_t{c.layers} * c.kv_heads * e.max_seq * c.head_dim * 2;
   const uint64_t rope = uint64_t{e.max_seq} * c.head_dim * 2;
   e.nparts = e.rt->compute_units * 8;
+  e.att_parts = std::min(64u, std::max(1u, e.rt->compute_units / c.heads));
+  e.att_spitch = (e.max_seq + 511u) & ~511u;
   std::vector<std::pair<void **, uint64_t>> parts = {
       {reinterpret_cast<void **>(&e.x), c.hidden * 2ull},
       {reinterpret_cast<void **>(&e.qkv), (qd + 2 * kvd) * 2},
@@ -196,6 +206,8 @@ int allocate_buffers(xpu_qwen3 &e) {
       {reinterpret_cast<void **>(&e.prompt), e.max_seq * 4ull},
       {reinterpret_cast<void **>(&e.gen), e.max_seq * 4ull},
       {reinterpret_cast<void **>(&e.ref_token), 4},
+      {reinterpret_cast<void **>(&e.att_scores), uint64_t{c.heads} * e.att_spitch * 4},
+      {reinterpret_cast<void **>(&e.att_max), uint64_t{c.heads} * e.att_parts * 4},
   };
   uint64_t total = 0;
   for (auto &p : parts) total += (p.second + 255) & ~uint64_t{255};
@@ -308,6 +320,16 @@ int setup_launches(xpu_qwen3 &e) {
   if ((rc = find("xpu_q3_attention", e.attn_l))) return rc;
   // one block per query head, the other compute units prefetch weights
   e.attn_l.grid = std::max(c.heads, e.rt->compute_units);
+  e.scores_l.k = e.rt->find_exact("xpu_q3_attn_scores");
+  e.pv_l.k = e.rt->find_exact("xpu_q3_attn_pv");
+  e.scores_l.grid = c.heads * e.att_parts;
+  e.pv_l.grid = c.heads * 8;  // 16 output dims per block
+  // probabilities (4096 floats) + V rows (4096 x 16 codes) of a softmax
+  // chunk + 64 chunk sums + 4 x 16 wave partials
+  e.pv_l.shared = 4096 * 4 + 4096 * 16 * 2 + 64 * 4 + 64 * 4;
+  e.split_ok = e.scores_l.k && e.pv_l.k && e.max_seq <= 64u * 4096u && e.pv_l.shared <= e.rt->max_shared;
+  if (const char *from = std::getenv("XPU_Q3_SPLIT_FROM"); from && *from)
+    e.split_from = static_cast<uint32_t>(std::strtoul(from, nullptr, 10));
   {
     const char *cap = std::getenv("XPU_Q3_PREFETCH_MB"), *delay = std::getenv("XPU_Q3_PREFETCH_DELAY");
     const char *next = std::getenv("XPU_Q3_PREFETCH_NEXT");
@@ -385,7 +407,7 @@ int launch(xpu_qwen3 &e, const xpu_qwen3::Launch &l, uint32_t block, std::initia
 }
 
 // One token through the fused kernels (reads position/token from state).
-int enqueue_fused_step(xpu_qwen3 &e) {
+int enqueue_fused_step(xpu_qwen3 &e, bool split) {
   const xpu_qwen3_config &c = e.c;
   const uint32_t H = c.hidden, I = c.intermediate, V = c.vocab, heads = c.heads, kv = c.kv_heads;
   const uint32_t qkv_rows = (heads + 2 * kv) * c.head_dim, qd = heads * c.head_dim, max_seq = e.max_seq;
@@ -412,7 +434,18 @@ int enqueue_fused_step(xpu_qwen3 &e) {
     const uint64_t pf_bytes =
         std::min<uint64_t>(e.pf_cap, static_cast<uint64_t>(pf_end - reinterpret_cast<const uint8_t *>(L.o)));
     const uint32_t pf_delay = e.pf_delay;
-    if ((rc = launch(e, e.attn_l, 256,
+    if (split) {
+      const uint32_t spitch = e.att_spitch, parts = e.att_parts;
+      if ((rc = launch(e, e.scores_l, 256,
+                       {{8, &e.qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.rope_row}, {8, &sin_row}, {8, &kc},
+                        {8, &vc}, {8, &e.att_scores}, {8, &e.att_max}, {8, &e.state}, {4, &heads}, {4, &kv},
+                        {4, &max_seq}, {4, &spitch}, {4, &parts}, {4, &eps}, {4, &scale}})))
+        return rc;
+      if ((rc = launch(e, e.pv_l, 256,
+                       {{8, &e.att_scores}, {8, &e.att_max}, {8, &vc}, {8, &e.attn}, {8, &e.state}, {4, &heads},
+                        {4, &kv}, {4, &max_seq}, {4, &spitch}, {4, &parts}})))
+        return rc;
+    } else if ((rc = launch(e, e.attn_l, 256,
                      {{8, &e.qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.rope_row}, {8, &sin_row}, {8, &kc},
                       {8, &vc}, {8, &e.attn}, {8, &e.state}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps},
                       {4, &scale}, {8, &pf}, {8, &pf_bytes}, {4, &pf_delay}})))
@@ -498,19 +531,24 @@ int set_rope_row(xpu_qwen3 &e, uint32_t position) {
   return rc;
 }
 
-int run_fused_step(xpu_qwen3 &e) {
-  if (e.mode == XPU_QWEN3_EAGER) return enqueue_fused_step(e);
-  if (!e.graph) {
+// One decode step at `position` (the value state[0] holds when it runs): the
+// attention is split over compute units from split_from positions on; each
+// variant has its own graph.
+int run_fused_step(xpu_qwen3 &e, uint32_t position) {
+  const bool split = e.split_ok && e.split_from && position + 1 >= e.split_from;
+  if (e.mode == XPU_QWEN3_EAGER) return enqueue_fused_step(e, split);
+  void *&graph = split ? e.graph_split : e.graph;
+  if (!graph) {
     int rc = xpu_rt_capture_begin(e.rt);
     if (rc) return rc;
-    rc = enqueue_fused_step(e);
+    rc = enqueue_fused_step(e, split);
     void *exec = nullptr;
     const int rc2 = xpu_rt_capture_end(e.rt, &exec);
     if (rc) return rc;
     if (rc2) return rc2;
-    e.graph = exec;
+    graph = exec;
   }
-  return xpu_rt_graph_launch(e.rt, e.graph);
+  return xpu_rt_graph_launch(e.rt, graph);
 }
 
 // Reference-mode step: the reference's kernel sequence, each launch blocking
@@ -890,6 +928,14 @@ extern "C" int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int batched) {
   return XPU_OK;
 }
 
+extern "C" int xpu_qwen3_set_attention_split(xpu_qwen3 *eng, uint32_t min_context) {
+  if (!eng) return set_error(XPU_ERR_INVALID, "null engine");
+  if (min_context && !eng->split_ok)
+    return set_error(XPU_ERR_INVALID, "split attention has no kernels for this engine");
+  eng->split_from = min_context;
+  return XPU_OK;
+}
+
 extern "C" int xpu_qwen3_decode(xpu_qwen3 *eng, uint32_t token, uint32_t position, uint32_t *next) {
   if (!eng || !next) return set_error(XPU_ERR_INVALID, "null argument");
   if (token >= eng->c.vocab) return set_error(XPU_ERR_INVALID, "input token ID is outside the vocabulary");
@@ -902,7 +948,7 @@ extern "C" int xpu_qwen3_decode(xpu_qwen3 *eng, uint32_t token, uint32_t positio
     const uint32_t st[4] = {position, token, 0, 0};
     if ((rc = xpu_rt_copy_to_device(eng->rt, eng->state, st, sizeof(st)))) return rc;
     if ((rc = set_rope_row(*eng, position))) return rc;
-    if ((rc = run_fused_step(*eng))) return rc;
+    if ((rc = run_fused_step(*eng, position))) return rc;
     uint32_t back[4];
     if ((rc = xpu_rt_copy_from_device(eng->rt, back, eng->state, sizeof(back)))) return rc;
     result = back[2];
@@ -969,7 +1015,7 @@ extern "C" int xpu_qwen3_generate(xpu_qwen3 *eng, const uint32_t *prompt, uint32
     rc = xpu_rt_event_record(eng->rt, ev[0]);
     if (!rc && first) rc = run_prefill(*eng, first);
     for (uint32_t s = first; !rc && s < steps; ++s) {
-      rc = run_fused_step(*eng);
+      rc = run_fused_step(*eng, s);
       if (!rc && s + 1 == n_prompt) rc = xpu_rt_event_record(eng->rt, ev[1]);
     }
     if (!rc) rc = xpu_rt_event_record(eng->rt, ev[2]);

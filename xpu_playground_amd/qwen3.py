@@ -107,6 +107,11 @@ class Engine:
         """Batched (default) or stepwise prompt processing in generate."""
         check(self.lib.xpu_qwen3_set_prefill(self.handle, 1 if batched else 0))
 
+    def set_attention_split(self, min_context: int) -> None:
+        """Split the attention over compute units for contexts of at least
+        min_context positions (0: never); results are bit-identical."""
+        check(self.lib.xpu_qwen3_set_attention_split(self.handle, c_uint32(min_context)))
+
     def decode(self, token: int, position: int) -> int:
         nxt = c_uint32()
         check(self.lib.xpu_qwen3_decode(self.handle, token, position, ctypes.byref(nxt)))
