@@ -338,10 +338,11 @@ XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const 
     return (HAS_CURRENT && t + 1 == n) ? vcur : vbase + static_cast<uint64_t>(t) * lay.vstride;
   };
   auto vchunk_of = [&](uint32_t t) -> uint64_t { return (HAS_CURRENT && t + 1 == n) ? 8u : lay.vchunk; };
-  // a tile of tlen V rows from position t0: thread tid holds chunk tid % 16
-  // of rows 16 j + tid / 16 (16 lanes per row, so one load instruction
-  // covers 4 whole rows)
-  const uint32_t v_chunk = tid & 15u, v_row0 = tid >> 4;
+  // a tile of tlen V rows from position t0: thread tid holds chunk tid / 16
+  // of rows 16 j + tid % 16 (in the chunk-major cache a load instruction
+  // reads 16 consecutive rows of each of 4 chunks, 256 contiguous bytes
+  // each)
+  const uint32_t v_chunk = tid >> 4, v_row0 = tid & 15u;
   auto load_v_tile = [&](uint32_t t0, uint32_t tlen, u32x4 (&vv)[16]) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
