@@ -68,13 +68,15 @@ def test_attention_past_one_softmax_chunk(rt, split_from):
     eng.close()
 
 
+@pytest.mark.parametrize("heads", [16, 32])
 @pytest.mark.parametrize("mode", [qwen3.GRAPH, qwen3.EAGER])
 @pytest.mark.parametrize("split_from", [0, 1, 257])
-def test_split_attention_every_position_matches_oracle(rt, mode, split_from):
-    # 16 query / 8 kv heads (the 0.6B grouping): every position 0..299 through
-    # decode, with the attention split over compute units never, at every
-    # step, or from the 257th position on (both captured graphs in one run)
-    cfg = orc.config("small", layers=1, vocab=1024)
+def test_split_attention_every_position_matches_oracle(rt, mode, split_from, heads):
+    # 16 or 32 query heads over 8 kv heads (the 0.6B and 8B groupings): every
+    # position 0..299 through decode, with the attention split over compute
+    # units never, at every step, or from the 257th position on (both
+    # captured graphs in one run)
+    cfg = orc.config("small", layers=1, vocab=1024, heads=heads)
     max_seq = 304
     m = orc.Model(cfg, seed=6, gain_std=0.1, max_seq=max_seq)
     eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=max_seq, seed=6, gain_std=0.1, runtime=rt)
@@ -82,7 +84,7 @@ def test_split_attention_every_position_matches_oracle(rt, mode, split_from):
     eng.set_attention_split(split_from)
     prompt = orc.tokens(160, 12, cfg.vocab)
     token = int(prompt[0])
-    print(f"mode={mode} split_from={split_from}", flush=True)
+    print(f"mode={mode} split_from={split_from} heads={heads}", flush=True)
     for pos in range(300):
         ref_tok, ref_logits = m.decode(token, pos, want_logits=True)
         tok = eng.decode(token, pos)

@@ -411,23 +411,29 @@ XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const 
         const uint32_t next_len = i0 + kAttnTile < len ? min(kAttnTile, len - i0 - kAttnTile) : 0u;
         if (next_len) load_v_tile(base + i0 + kAttnTile, next_len, vnext);
       }
-      for (uint32_t ii = 0; ii < tile_len; ii += 16u) {
-        float pt[4];
-        uint32_t vv[4];
+      // 64 rows per step: the operands of 4 groups of 16 rows are read
+      // (index clamped into the tile) before their FMAs, each chain in
+      // ascending row order
+      for (uint32_t ii0 = 0; ii0 < tile_len; ii0 += 64u) {
+        float pt[4][4];
+        uint32_t vv[4][4];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const uint32_t i = ii + wave * 4u + rr;
-          const bool ok = i < tile_len;
-          pt[rr] = ok ? sbuf[i0 + i] : 0.0f;
-          vv[rr] = ok ? *reinterpret_cast<const uint32_t *>(vtile + i * kVPitch + lane * 2u) : 0u;
-        }
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          if (ii + wave * 4u + rr < tile_len) {
-            part[rr][0] = __builtin_fmaf(pt[rr], lo16<kBf16>(vv[rr]), part[rr][0]);
-            part[rr][1] = __builtin_fmaf(pt[rr], hi16<kBf16>(vv[rr]), part[rr][1]);
+          for (int rr = 0; rr < 4; ++rr) {
+            const uint32_t i = min(ii0 + 16u * q + wave * 4u + rr, tile_len - 1);
+            pt[q][rr] = sbuf[i0 + i];
+            vv[q][rr] = *reinterpret_cast<const uint32_t *>(vtile + i * kVPitch + lane * 2u);
           }
-        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            if (ii0 + 16u * q + wave * 4u + rr < tile_len) {
+              part[rr][0] = __builtin_fmaf(pt[q][rr], lo16<kBf16>(vv[q][rr]), part[rr][0]);
+              part[rr][1] = __builtin_fmaf(pt[q][rr], hi16<kBf16>(vv[q][rr]), part[rr][1]);
+            }
+          }
       }
       if (!single_tile) __syncthreads();
     }
