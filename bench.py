@@ -251,7 +251,7 @@ def main() -> int:
         return traffic_workload()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the hot path is "
-              "single-device and sharding is described in DESIGN.md", file=sys.stderr)
+              "built for a single device (no collectives, no sharded launch)", file=sys.stderr)
         return 2
 
     import xpu_playground_amd as xpu
