@@ -1126,6 +1126,41 @@ namespace {
 // c*512 + 8 l + s over chunks c in order (FMA), then fold8 and the xor
 // butterfly. EPI 0: Out = bf16(y); 1: Out = bf16(Out + bf16(y)) (residual);
 // 2 (PAIRED): Out[t][i] = bf16(bf16(silu(bf16(g))) * bf16(u)).
+//
+// The 64-lane butterflies of the TT = 8 tokens of a tile are evaluated by
+// recursive halving: at the l ^ 32, l ^ 16 and l ^ 8 steps each lane keeps
+// half of its tokens (chosen by that lane bit) and adds the partner's value
+// of the same token, own + partner, as the butterfly does; the l ^ 4, l ^ 2
+// and l ^ 1 steps run on the one token left (4 b5 + 2 b4 + b3 of the lane
+// index). Every sum is the butterfly's, with 10 exchanges instead of 48.
+XPU_DEVICE float xor4_f(float v) {  // ds_swizzle, bit mode: and 0x1f, xor 4
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x101F));
+}
+
+template <int N>
+XPU_DEVICE void halve_tokens(float (&v)[2 * N], float (&w)[N], bool upper, float (*xchg)(float)) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const float keep = upper ? v[N + j] : v[j];
+    const float send = upper ? v[j] : v[N + j];
+    w[j] = keep + xchg(send);
+  }
+}
+
+// the 64-lane sums of v[t] for t < 8, token 4 b5 + 2 b4 + b3 of this lane
+XPU_DEVICE float token_butterfly8(float (&v)[8]) {
+  const uint32_t lane = xpu::lane_id();
+  float w4[4], w2[2], w1[1];
+  halve_tokens<4>(v, w4, (lane & 32u) != 0, xpu::xor32_f);
+  halve_tokens<2>(w4, w2, (lane & 16u) != 0, xpu::xor16_f);
+  halve_tokens<1>(w2, w1, (lane & 8u) != 0, xpu::xor8_f);
+  float s = w1[0];
+  s = s + xor4_f(s);
+  s = s + xpu::dpp_f<0x4E>(s);  // quad_perm [2,3,0,1]
+  s = s + xpu::dpp_f<0xB1>(s);  // quad_perm [1,0,3,2]
+  return s;
+}
+
 template <int R, int NC, int TT, int EPI>
 XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restrict__ In, uint16_t *Out, uint32_t M,
                         uint32_t T) {
@@ -1148,6 +1183,15 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
     const uint16_t *p = W + static_cast<uint64_t>(row) * K + lane * 8u;
 #pragma unroll
     for (int c = 0; c < NC; ++c) a[r][c] = xpu::load_nt16(p + c * 512u);
+  }
+  // the rows unpacked to FP32 once, when that fits the registers
+  constexpr bool kHoist = R * NC <= 8;
+  float af[kHoist ? R : 1][kHoist ? NC : 1][8];
+  if constexpr (kHoist) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) xpu::unpack8<xpu::kBf16>(a[r][c], af[r][c]);
   }
   // token tiles are double buffered: the loads of tile i + 1 are issued
   // before the FMAs of tile i and stored to the other buffer after them
@@ -1187,24 +1231,36 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
         xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const u32x4 *>(tile + tt * K + c * 512u + lane * 8u), xf);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          float af[8];
-          xpu::unpack8<xpu::kBf16>(a[r][c], af);
+          float aw[8];
+          if constexpr (kHoist) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[r][tt][e] = __builtin_fmaf(af[e], xf[e], acc[r][tt][e]);
+            for (int e = 0; e < 8; ++e) aw[e] = af[r][c][e];
+          } else {
+            xpu::unpack8<xpu::kBf16>(a[r][c], aw);
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[r][tt][e] = __builtin_fmaf(aw[e], xf[e], acc[r][tt][e]);
         }
       }
     }
-#pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
+    static_assert(TT == 8, "token_butterfly8 reduces 8 tokens");
+    {
+      // row r's sum for token tt_l = 4 b5 + 2 b4 + b3 of the lane; lane
+      // 8 tt_l + o writes output o of that token
       float y[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) y[r] = xpu::wave_butterfly(xpu::fold8(acc[r][tt]));
-      const uint32_t t = t0 + tt;
-      if (t >= T) continue;
+      for (int r = 0; r < R; ++r) {
+        float v[8];
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt) v[tt] = xpu::fold8(acc[r][tt]);
+        y[r] = token_butterfly8(v);
+      }
+      const uint32_t tt_l = ((lane >> 5) & 1u) * 4u + ((lane >> 4) & 1u) * 2u + ((lane >> 3) & 1u);
+      const uint32_t t = t0 + tt_l;
       uint16_t *orow = Out + static_cast<uint64_t>(t) * M;
 #pragma unroll
       for (int o = 0; o < kOuts; ++o) {
-        if (lane != static_cast<uint32_t>(o) || o0 + o >= M) continue;
+        if ((lane & 7u) != static_cast<uint32_t>(o) || t >= T || o0 + o >= M) continue;
         if constexpr (EPI == 0) {
           orow[o0 + o] = static_cast<uint16_t>(xpu::f32_to_bf16(y[o]));
         } else if constexpr (EPI == 1) {
