@@ -57,6 +57,31 @@ def test_gemv_matches_oracle(rt, dtype, m, k, lda):
     check_against_fp64(y, a, x, m, k, lda, dtype)
 
 
+@pytest.mark.parametrize("dtype", [xpu.BF16, xpu.FP16])
+@pytest.mark.parametrize("m,k,lda", [(64, 512, 512), (37, 1000, 1000), (1000, 1032, 1040), (5, 3, 7)])
+def test_gemv_pointers_two_bytes_past_alignment(rt, dtype, m, k, lda):
+    # A, x and y start 2 bytes past a 16-byte boundary, which the 16-byte
+    # loads of the vector variants cannot take: the 16-bit-load variant runs.
+    # Guard codes around y catch any store outside it.
+    print(f"gemv unaligned pointers dtype={dtype} m={m} k={k} lda={lda}", flush=True)
+    a = orc.uniform(m * lda, 300 + m, dtype)
+    x = orc.uniform(k, 400 + k, dtype)
+    guard = 0x7E7E
+    pa, px, py = rt.alloc(m * lda * 2 + 64), rt.alloc(k * 2 + 64), rt.alloc(m * 2 + 64)
+    try:
+        rt.copy_to(py, np.full((m * 2 + 64) // 2, guard, np.uint16))
+        rt.copy_to(pa + 2, a)
+        rt.copy_to(px + 2, x)
+        rt.gemv(dtype, pa + 2, px + 2, py + 2, m, k, lda)
+        rt.synchronize()
+        out = rt.download(py, (m * 2 + 64) // 2, np.uint16)
+    finally:
+        for p in (pa, px, py):
+            rt.free(p)
+    assert out[0] == guard and np.all(out[1 + m:] == guard)
+    assert np.array_equal(out[1:1 + m], orc.gemv_canonical(a, x, m, k, lda, dtype))
+
+
 def test_gemv_large_k_reads_vector_from_global(rt):
     m, k = 8, 100000
     a = orc.uniform(m * k, 7, 0)
