@@ -1352,3 +1352,77 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_attention(
                              p0 + t + 1, nullptr,
                              nullptr, scale, A + qoff, sbuf, vtile, red);
 }
+
+// xpu_q3_pf_attention for chunks whose contexts stay within kAttnTile
+// positions (p0 + gridDim.y <= 256): the decode kernel's short path with
+// every position read from the caches (thread t <-> position t, the V
+// pieces in registers in the P.V layout, three block barriers), the same
+// operations in the same order.
+extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_attention_short(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache,
+    uint16_t *__restrict__ A, uint32_t p0, uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float scale) {
+  __shared__ float sbuf[xpu::kAttnTile];
+  __shared__ float red[4 + 32];
+  __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
+  const uint32_t head = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = xpu::lane_id();
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t kv = head / (heads / kv_heads);
+  const uint64_t qoff = (static_cast<uint64_t>(t) * heads + head) * xpu::kHeadDim;
+  const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
+  const uint64_t kchunk = static_cast<uint64_t>(max_seq) * 8u;
+  const uint32_t n = p0 + t + 1;
+  if (tid < 16) *reinterpret_cast<u32x4 *>(qs + tid * 8u) = *reinterpret_cast<const u32x4 *>(Q + qoff + tid * 8u);
+  u32x4 krow[16];
+  xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(min(tid, n - 1)) * 8u, krow, kchunk);
+  __syncthreads();  // 1: qs
+  const float sc = tid < n ? xpu::attention_score_regs(qs, krow, scale) : -__builtin_inff();
+  // V pieces: lane l of wave w owns residue class l % 16 and cache chunk
+  // 4 w + l / 16; vpv[it] = V[16 it + cls] (rows past the context re-read
+  // the last row and are not used)
+  u32x4 vpv[xpu::kAttnTile / 16];
+  const uint32_t cls = lane & 15u, vch = wave * 4u + (lane >> 4);
+#pragma unroll
+  for (int it = 0; it < static_cast<int>(xpu::kAttnTile / 16); ++it) {
+    const uint32_t tv = min(it * 16u + cls, n - 1);
+    vpv[it] = *reinterpret_cast<const u32x4 *>(vcache + head_base + vch * kchunk + static_cast<uint64_t>(tv) * 8u);
+  }
+  const float wmax = xpu::wave_reduce(sc, [](float x, float y) { return fmaxf(x, y); });
+  if (lane == 0) red[wave] = wmax;
+  __syncthreads();  // 2: wave maxima
+  const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float ex = tid < n ? xpu::canonical_exp(sc - mx) : 0.0f;
+  sbuf[tid] = ex;
+  float f = ex + xpu::dpp_f<0xB1>(ex);  // (a0 + a1), (a2 + a3), ...
+  f = f + xpu::dpp_f<0x4E>(f);          // (a0 + a1) + (a2 + a3)
+  f = f + xpu::dpp_f<0x141>(f);         // row_half_mirror: the other quad of the eight
+  float *lane_sum = red + 4;            // 32 canonical lane sums
+  if ((tid & 7u) == 0) lane_sum[tid >> 3] = f;
+  __syncthreads();  // 3: exponentials and lane sums
+  const float total = xpu::wave_butterfly(lane < 32 ? lane_sum[lane] : 0.0f);
+  const float inv = 1.0f / total;
+  float part[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int it = 0; it < static_cast<int>(xpu::kAttnTile / 16); ++it) {
+    const uint32_t tp = it * 16u + cls;
+    if (tp < n) {
+      const float pt = xpu::round_bf16(sbuf[tp] * inv);
+      float v[8];
+      xpu::unpack8<xpu::kBf16>(vpv[it], v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[e] = __builtin_fmaf(pt, v[e], part[e]);
+    }
+  }
+  uint32_t code[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float v = part[e];
+    v = v + xpu::dpp_f<0xB1>(v);   // xor 1
+    v = v + xpu::dpp_f<0x4E>(v);   // xor 2
+    v = v + xpu::dpp_f<0x141>(v);  // row_half_mirror
+    v = v + xpu::xor8_f(v);
+    code[e] = xpu::f32_to_bf16(v);
+  }
+  if (cls == 0)
+    *reinterpret_cast<u32x4 *>(A + qoff + vch * 8u) =
+        u32x4{code[0] | (code[1] << 16), code[2] | (code[3] << 16), code[4] | (code[5] << 16), code[6] | (code[7] << 16)};
+}

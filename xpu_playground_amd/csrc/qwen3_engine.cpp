@@ -163,6 +163,7 @@ struct xpu_qwen3 {
   void *pf_block = nullptr;
   uint16_t *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_a = nullptr,
            *pf_h = nullptr;
+  const xpu::KernelInfo *pf_attn_short_k = nullptr;  // chunks whose contexts stay within 256 positions
   const xpu::KernelInfo *pf_embed_k = nullptr, *pf_norm_k = nullptr, *pf_rope_k = nullptr, *pf_attn_k = nullptr,
                         *pf_qkv_k = nullptr, *pf_o_k = nullptr, *pf_gu_k = nullptr, *pf_down_k = nullptr;
 
@@ -381,6 +382,7 @@ int setup_prefill(xpu_qwen3 &e) {
   e.pf_norm_k = e.rt->find_exact("xpu_q3_pf_rmsnorm");
   e.pf_rope_k = e.rt->find_exact("xpu_q3_pf_rope_cache");
   e.pf_attn_k = e.rt->find_exact("xpu_q3_pf_attention");
+  e.pf_attn_short_k = e.rt->find_exact("xpu_q3_pf_attention_short");
   e.pf_ok = e.pf_qkv_k && e.pf_o_k && e.pf_gu_k && e.pf_down_k && e.pf_embed_k && e.pf_norm_k && e.pf_rope_k &&
             e.pf_attn_k && c.hidden % 8 == 0 && kpad_bytes(c.hidden) <= e.rt->max_shared &&
             32u * std::max({c.hidden, qd, c.intermediate}) <= e.rt->max_shared;
@@ -502,7 +504,8 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
                    {{8, &e.pf_qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &kc},
                     {8, &vc}, {8, &e.pf_q}, {4, &p0}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps}})))
         return rc;
-      if ((rc = go(e.pf_attn_k, heads, T, 256, 0,
+      const bool short_ctx = e.pf_attn_short_k && p0 + T <= 256;  // every token's context within 256 positions
+      if ((rc = go(short_ctx ? e.pf_attn_short_k : e.pf_attn_k, heads, T, 256, 0,
                    {{8, &e.pf_q}, {8, &kc}, {8, &vc}, {8, &e.pf_a}, {4, &p0}, {4, &heads}, {4, &kv},
                     {4, &max_seq}, {4, &scale}})))
         return rc;
