@@ -1216,17 +1216,19 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
     const bool more = t0 + TT < T;
     if (more) load_tile(t0 + TT);
     const uint16_t *tile = xt + cur * kTile;
-    float acc[R][TT][8];
+    static_assert(TT == 8, "token_butterfly8 reduces 8 tokens");
+    // token by token: each slot's FMA chain over the chunks, then its fold,
+    // so only one token's accumulators are live
+    float v[R][TT];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int tt = 0; tt < TT; ++tt) {
+      float acc[R][8];
 #pragma unroll
-      for (int tt = 0; tt < TT; ++tt)
+      for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[r][tt][e] = 0.0f;
+        for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-#pragma unroll
-      for (int tt = 0; tt < TT; ++tt) {
+      for (int c = 0; c < NC; ++c) {
         float xf[8];
         xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const u32x4 *>(tile + tt * K + c * 512u + lane * 8u), xf);
 #pragma unroll
@@ -1239,22 +1241,18 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
             xpu::unpack8<xpu::kBf16>(a[r][c], aw);
           }
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[r][tt][e] = __builtin_fmaf(aw[e], xf[e], acc[r][tt][e]);
+          for (int e = 0; e < 8; ++e) acc[r][e] = __builtin_fmaf(aw[e], xf[e], acc[r][e]);
         }
       }
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[r][tt] = xpu::fold8(acc[r]);
     }
-    static_assert(TT == 8, "token_butterfly8 reduces 8 tokens");
     {
       // row r's sum for token tt_l = 4 b5 + 2 b4 + b3 of the lane; lane
       // 8 tt_l + o writes output o of that token
       float y[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float v[8];
-#pragma unroll
-        for (int tt = 0; tt < 8; ++tt) v[tt] = xpu::fold8(acc[r][tt]);
-        y[r] = token_butterfly8(v);
-      }
+      for (int r = 0; r < R; ++r) y[r] = token_butterfly8(v[r]);
       const uint32_t tt_l = ((lane >> 5) & 1u) * 4u + ((lane >> 4) & 1u) * 2u + ((lane >> 3) & 1u);
       const uint32_t t = t0 + tt_l;
       uint16_t *orow = Out + static_cast<uint64_t>(t) * M;
