@@ -9,7 +9,8 @@ synchronisation and timed with HIP events recorded on the runtime's stream
 launch / average launch time, in GB/s; roofline.peak = 8000 GB/s (HBM3E).
 
 Secondary lines (same JSON object): GEMM bf16 4096^3 TFLOP/s
-and Qwen3-0.6B-shape batch-1 greedy decode tok/s.
+and Qwen3-0.6B-shape batch-1 greedy decode tok/s, plus the
+same decode after a 2048-id prompt (the attention split over compute units).
 
 cpu_baseline: the CPU oracle's reference-order GEMV (gemv.cpp:126-134,
 sequential FP32 sum per row) over the same 16384 x 16384 fp16 matrix on all
@@ -133,9 +134,9 @@ def xpu_check(code):
     xpu.check(code)
 
 
-def qwen3_decode(xpu):
-    """Qwen3-0.6B shape, random N(0, 0.02^2) bf16 weights, 128-token seeded
-    prompt, 128 greedy steps; returns (decode tok/s, prompt tok/s)."""
+def qwen3_decode(xpu, n_prompt=128, max_seq=256):
+    """Qwen3-0.6B shape, random N(0, 0.02^2) bf16 weights, n_prompt seeded
+    prompt ids, 128 greedy steps; returns decode and prompt tok/s."""
     import numpy as np
 
     lib = xpu.library()
@@ -147,24 +148,24 @@ def qwen3_decode(xpu):
     cfg = xpu.Qwen3Config()
     xpu.check(lib.xpu_qwen3_preset(b"qwen3-0.6b", ctypes.byref(cfg)))
     eng = ctypes.c_void_p()
-    xpu.check(lib.xpu_qwen3_create(rt.handle, ctypes.byref(cfg), 256, 0, 0.0, ctypes.byref(eng)))
+    xpu.check(lib.xpu_qwen3_create(rt.handle, ctypes.byref(cfg), max_seq, 0, 0.0, ctypes.byref(eng)))
     try:
-        prompt = np.empty(128, np.uint32)
+        prompt = np.empty(n_prompt, np.uint32)
         # the same seeded ids as the oracle's orc_fill_tokens(seed 1)
         from xpu_playground_amd import qwen3 as q3
 
-        prompt[:] = q3.prompt_tokens(128, 1, cfg.vocab)
+        prompt[:] = q3.prompt_tokens(n_prompt, 1, cfg.vocab)
         out = (ctypes.c_uint32 * 128)()
         n_out = ctypes.c_uint32()
         prompt_ms, decode_ms = ctypes.c_double(), ctypes.c_double()
-        arr = (ctypes.c_uint32 * 128)(*prompt.tolist())
-        for _ in range(2):  # first run builds the graph
-            xpu.check(lib.xpu_qwen3_generate(eng, arr, 128, 128, 0, out, ctypes.byref(n_out),
+        arr = (ctypes.c_uint32 * n_prompt)(*prompt.tolist())
+        for _ in range(2):  # first run builds the graphs
+            xpu.check(lib.xpu_qwen3_generate(eng, arr, n_prompt, 128, 0, out, ctypes.byref(n_out),
                                              ctypes.byref(prompt_ms), ctypes.byref(decode_ms)))
         decode_steps = n_out.value - 1
         return {
             "decode_tok_s": decode_steps / (decode_ms.value * 1e-3),
-            "prompt_tok_s": 128 / (prompt_ms.value * 1e-3),
+            "prompt_tok_s": n_prompt / (prompt_ms.value * 1e-3),
             "ms_per_token": decode_ms.value / decode_steps,
             "generated": n_out.value,
         }
@@ -298,6 +299,14 @@ def main() -> int:
                 "value": round(q["decode_tok_s"], 1), "unit": "tok/s", "ms_per_token": round(q["ms_per_token"], 4),
                 "prompt_tok_s": round(q["prompt_tok_s"], 1)}
             log(f"Qwen3 decode {q['decode_tok_s']:.1f} tok/s")
+        log("Qwen3-0.6B decode: 2048 prompt + 128 greedy steps")
+        q = qwen3_decode(xpu, 2048, 2304)
+        if q:
+            secondary["qwen3_0.6b_decode_after_2048_prompt"] = {
+                "value": round(q["decode_tok_s"], 1), "unit": "tok/s", "ms_per_token": round(q["ms_per_token"], 4),
+                "prompt_tok_s": round(q["prompt_tok_s"], 1),
+                "attention": "split over compute units from 257 positions"}
+            log(f"Qwen3 decode after 2048 prompt ids {q['decode_tok_s']:.1f} tok/s")
 
     cpu = None
     if not args.no_cpu:
