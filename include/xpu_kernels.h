@@ -55,8 +55,10 @@ int xpu_fill_reference_gemv(xpu_runtime *rt, int dtype, void *matrix, void *vect
  *           --iterations N (50), --warmups N (5); default 16384 x 16384 bf16)
  * run_gemm: gemm.cpp:135-155 (--size N | --m M --n N --k K, --type,
  *           --iterations N (20), --warmups N (5); default 4096^3 bf16)
- * Both return 0 on success, 1 on error (message "Error: ..." on stderr) and
- * 2 when verification fails (level_zero/peak_l0.cpp:892,948). */
+ * Both return 0 after "Verification: PASS", 1 on any error, a failed
+ * verification included ("Error: GEMV verification failed" /
+ * "Error: GEMM verification failed: ..." on stderr, as gemv.cpp:135-136,
+ * gemm.cpp:117-123 throw into the catch of run_gemv / run_gemm). */
 int run_gemv(int argc, char **argv);
 int run_gemm(int argc, char **argv);
 

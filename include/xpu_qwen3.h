@@ -89,6 +89,16 @@ int xpu_qwen3_create(xpu_runtime *rt, const xpu_qwen3_config *cfg, uint32_t max_
  * dtype bfloat16, no rope_scaling, head_dim 128). */
 int xpu_qwen3_read_config(const char *model_dir, xpu_qwen3_config *out);
 
+/* Host-only check of a checkpoint directory, the counterpart of
+ * load_and_validate_checkpoint (qwen3/model.cpp:448-495): the config as
+ * xpu_qwen3_read_config; with model.safetensors.index.json, every
+ * weight_map shard's header lists exactly the tensors mapped to it and
+ * metadata.total_size equals the payload bytes; every tensor is BF16 and
+ * lies inside its shard's payload, no two payloads of a shard overlap; the
+ * tensor set and shapes are those of the config. XPU_ERR_INVALID with the
+ * reason otherwise. out (may be NULL) receives the config. */
+int xpu_qwen3_validate_checkpoint(const char *model_dir, xpu_qwen3_config *out);
+
 /* Same, loading a Hugging Face checkpoint directory (config.json,
  * model.safetensors[.index.json]) with bf16 tensors (model.cpp:448-495). */
 int xpu_qwen3_create_from_checkpoint(xpu_runtime *rt, const char *model_dir, uint32_t max_seq,
@@ -96,6 +106,13 @@ int xpu_qwen3_create_from_checkpoint(xpu_runtime *rt, const char *model_dir, uin
 void xpu_qwen3_destroy(xpu_qwen3 *eng);
 int xpu_qwen3_get_config(const xpu_qwen3 *eng, xpu_qwen3_config *out);
 
+/* Select the mode for the following calls. Reference mode keeps the KV
+ * caches position-major ([layer][position][kv_head][128], as
+ * qwen3/main.cpp:131-137), graph and eager modes chunk-major, in the same
+ * buffers; graph and eager modes may alternate within a sequence. A decode
+ * at position > 0 whose mode's layout differs from the one the sequence was
+ * started in fails with XPU_ERR_INVALID: after switching between reference
+ * and graph/eager mode, start again at position 0 (generate always does). */
 int xpu_qwen3_set_mode(xpu_qwen3 *eng, int mode);
 
 /* Prompt processing in xpu_qwen3_generate (graph and eager modes): batched
@@ -112,8 +129,7 @@ int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int batched);
  * compute units: a scores kernel over 256-position tiles and a P.V kernel
  * per 16 output dims, with the same operations in the same order as the
  * one-block-per-head kernel, so results are bit-identical; each variant has
- * its own captured graph. 0 never splits. Default 257 (environment
- * XPU_Q3_SPLIT_FROM at creation overrides it). No reference counterpart:
+ * its own captured graph. 0 never splits. Default 257. No reference counterpart:
  * the reference's Attention (qwen3/kernels.hpp:157-192) is one serial loop
  * per head. XPU_ERR_INVALID when the module lacks the kernels. */
 int xpu_qwen3_set_attention_split(xpu_qwen3 *eng, uint32_t min_context);

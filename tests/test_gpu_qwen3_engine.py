@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as orc
+from checkpoint_util import write_checkpoint
 import xpu_playground_amd as xpu
 from xpu_playground_amd import qwen3
 
@@ -142,57 +143,6 @@ def test_baseline_workload_qwen3_0_6b(rt):
     eng.close()
 
 
-def write_checkpoint(directory, cfg, seed, gain_std, sharded=False, nan_embed=False):
-    import torch
-    from safetensors.torch import save_file
-
-    names = ["self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
-             "self_attn.o_proj.weight", "self_attn.q_norm.weight", "self_attn.k_norm.weight",
-             "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight", "input_layernorm.weight",
-             "post_attention_layernorm.weight"]
-    h, hd = cfg.hidden, cfg.head_dim
-    shapes = [(cfg.heads * hd, h), (cfg.kv_heads * hd, h), (cfg.kv_heads * hd, h), (h, cfg.heads * hd), (hd,),
-              (hd,), (cfg.intermediate, h), (cfg.intermediate, h), (h, cfg.intermediate), (h,), (h,)]
-
-    def tensor(kind, layer, shape):
-        a = orc.fill_tensor(cfg, seed, gain_std, kind, layer)
-        return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).reshape(shape)
-
-    tensors = {}
-    for layer in range(cfg.layers):
-        for kind, (n, shape) in enumerate(zip(names, shapes)):
-            tensors[f"model.layers.{layer}.{n}"] = tensor(kind, layer, shape)
-    emb = tensor(orc.W_EMBED, 0, (cfg.vocab, h))
-    if nan_embed:
-        emb = emb.clone()
-        emb[:, 7] = float("nan")
-    tensors["model.embed_tokens.weight"] = emb
-    tensors["model.norm.weight"] = tensor(orc.W_FINALNORM, 0, (h,))
-    if not cfg.tied:
-        tensors["lm_head.weight"] = tensor(orc.W_LMHEAD, 0, (cfg.vocab, h))
-    config = {"hidden_size": h, "intermediate_size": cfg.intermediate, "head_dim": hd,
-              "num_attention_heads": cfg.heads, "num_key_value_heads": cfg.kv_heads,
-              "num_hidden_layers": cfg.layers, "vocab_size": cfg.vocab, "max_position_embeddings": 40960,
-              "eos_token_id": 151645, "rms_norm_eps": 1e-6, "rope_theta": 1000000.0,
-              "tie_word_embeddings": bool(cfg.tied), "hidden_act": "silu", "model_type": "qwen3",
-              "torch_dtype": "bfloat16", "rope_scaling": None}
-    with open(os.path.join(directory, "config.json"), "w") as fh:
-        json.dump(config, fh)
-    if not sharded:
-        save_file(tensors, os.path.join(directory, "model.safetensors"))
-        return
-    keys = sorted(tensors)
-    half = len(keys) // 2
-    shards = {"model-00001-of-00002.safetensors": keys[:half], "model-00002-of-00002.safetensors": keys[half:]}
-    weight_map = {}
-    for shard, ks in shards.items():
-        save_file({k: tensors[k] for k in ks}, os.path.join(directory, shard))
-        weight_map.update({k: shard for k in ks})
-    total = sum(t.numel() * 2 for t in tensors.values())
-    with open(os.path.join(directory, "model.safetensors.index.json"), "w") as fh:
-        json.dump({"metadata": {"total_size": total}, "weight_map": weight_map}, fh)
-
-
 @pytest.mark.parametrize("tied,sharded", [(1, False), (0, True)])
 def test_checkpoint_loading(rt, tmp_path, tied, sharded):
     cfg = orc.config("tiny", tied=tied)
@@ -283,3 +233,76 @@ def test_prefill_cli_flag():
     bad = subprocess.run([exe, "--synthetic", "tiny", "--input-ids", "-", "--max-new-tokens", "1", "--prefill", "x"],
                          input="1 2 3\n", capture_output=True, text=True, timeout=120)
     assert bad.returncode == 1 and "--prefill must be" in bad.stderr
+
+
+def run_steps_all_modes(rt, cfg, seed, steps, max_seq, label):
+    """decode `steps` positions (the first half from a seeded prompt) in
+    every mode; logits, hidden state and tokens bit for bit against the oracle"""
+    m = orc.Model(cfg, seed=seed, gain_std=0.1, max_seq=max_seq)
+    prompt = orc.tokens(steps // 2, seed + 1, cfg.vocab)
+    ref = []
+    token = int(prompt[0])
+    for pos in range(steps):
+        tok, logits = m.decode(token, pos, want_logits=True)
+        ref.append((tok, logits, m.hidden().copy()))
+        token = int(prompt[pos + 1]) if pos + 1 < len(prompt) else tok
+    m.close()
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=max_seq, seed=seed, gain_std=0.1, runtime=rt)
+    for mode in MODES:
+        eng.set_mode(mode)
+        token = int(prompt[0])
+        for pos in range(steps):
+            print(f"{label} mode={mode} pos={pos}", flush=True)
+            tok = eng.decode(token, pos)
+            assert np.array_equal(eng.logits(), ref[pos][1]), (mode, pos)
+            assert np.array_equal(eng.hidden(), ref[pos][2]), (mode, pos)
+            assert tok == ref[pos][0], (mode, pos)
+            token = int(prompt[pos + 1]) if pos + 1 < len(prompt) else tok
+    eng.close()
+
+
+def test_reference_engine_shape_qwen3_8b(rt):
+    # the reference's own shape (qwen3/model.hpp:11-22): hidden 4096,
+    # intermediate 12288, 32 query / 8 kv heads, untied lm_head; two layers
+    # and a 4096-id vocabulary keep the oracle fast. down_proj (K = 12288)
+    # runs the LDS-staged residual GEMV, the other projections the
+    # register-vector kernels with 8 chunks per lane.
+    cfg = orc.config("qwen3-8b", layers=2, vocab=4096)
+    assert cfg.tied == 0
+    run_steps_all_modes(rt, cfg, seed=21, steps=8, max_seq=16, label="8b")
+
+
+def test_wide_shape_takes_the_lds_staged_kernels(rt):
+    # hidden 5120 (> 4096 = 8 chunks of 512 per lane) with 40 query heads
+    # over 8 kv heads (a group of 5): RMSNorm + QKV, gate/up + SiLU, the
+    # o_proj / down residual GEMVs and the final norm + lm_head all take
+    # their LDS-staged kernels
+    cfg = orc.config("small", hidden=5120, intermediate=6656, heads=40, kv_heads=8, layers=1, vocab=2048, tied=0)
+    run_steps_all_modes(rt, cfg, seed=23, steps=6, max_seq=8, label="wide")
+
+
+def test_mode_switch_mid_sequence_is_rejected(rt):
+    # reference mode keeps the KV caches position-major, graph and eager
+    # chunk-major: continuing a sequence across that switch is an error;
+    # graph <-> eager may alternate; position 0 starts afresh
+    cfg = orc.config("tiny")
+    m = orc.Model(cfg, seed=5, gain_std=0.1, max_seq=16)
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=16, seed=5, gain_std=0.1, runtime=rt)
+    seq = [3, 17, 400, 9]
+    ref = [m.decode(t, p) for p, t in enumerate(seq)]
+    for first, second in [(qwen3.GRAPH, qwen3.REFERENCE), (qwen3.REFERENCE, qwen3.EAGER)]:
+        eng.set_mode(first)
+        eng.decode(seq[0], 0)
+        eng.decode(seq[1], 1)
+        eng.set_mode(second)
+        with pytest.raises(xpu.XpuError, match="other mode's layout"):
+            eng.decode(seq[2], 2)
+        assert [eng.decode(t, p) for p, t in enumerate(seq)] == ref
+    eng.set_mode(qwen3.GRAPH)
+    out = [eng.decode(seq[0], 0)]
+    eng.set_mode(qwen3.EAGER)
+    out.append(eng.decode(seq[1], 1))
+    eng.set_mode(qwen3.GRAPH)
+    out += [eng.decode(seq[2], 2), eng.decode(seq[3], 3)]
+    assert out == ref
+    eng.close()

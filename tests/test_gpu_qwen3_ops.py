@@ -193,13 +193,14 @@ def test_argmax_tie_nan_and_random(rt):
     assert run() == orc.argmax(rand)
 
 
-def test_cpp_runtime_wrapper_dispatch_program():
-    # the same checks from C++ through include/xpu_runtime.hpp (the
-    # LevelZeroRuntime-shaped wrapper), at the 8B and 0.6B head layouts
+def test_cpp_runtime_wrapper_contract_program():
+    # include/xpu_runtime.hpp (the LevelZeroRuntime-shaped wrapper) from C++:
+    # queries, reserve check, alignment, copies, fragment lookup errors and a
+    # three-launch chain with a closed-form answer
     import os
     import subprocess
 
-    exe = os.path.join(xpu.BUILD_DIR, "qwen3_dispatch_test")
+    exe = os.path.join(xpu.BUILD_DIR, "runtime_contract_check")
     out = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stderr
-    assert "kernel dispatch: PASS" in out.stdout
+    assert "runtime contract: PASS" in out.stdout

@@ -130,6 +130,7 @@ def _declare(lib):
             ],
         ),
         "xpu_qwen3_read_config": (c_int, [c_char_p, POINTER(Qwen3Config)]),
+        "xpu_qwen3_validate_checkpoint": (c_int, [c_char_p, POINTER(Qwen3Config)]),
         "xpu_qwen3_get_config": (c_int, [c_void_p, POINTER(Qwen3Config)]),
         "xpu_qwen3_create_from_checkpoint": (c_int, [c_void_p, c_char_p, c_uint32, POINTER(c_void_p)]),
         "xpu_synth_tokens": (c_int, [c_void_p, c_uint64, c_uint64, c_uint32]),

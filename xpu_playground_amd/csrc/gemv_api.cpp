@@ -13,19 +13,8 @@
 
 namespace xpu {
 
-namespace {
-
-uint32_t env_u32(const char *name, uint32_t fallback) {
-  const char *v = std::getenv(name);
-  if (!v || !*v) return fallback;
-  return static_cast<uint32_t>(std::strtoul(v, nullptr, 10));
-}
-
-}  // namespace
-
 // Launch geometry of the GEMV kernels (kernels/gemv.hip): 256 threads, R rows
-// per wavefront, a grid-stride loop over 4R-row tiles with at most
-// blocks_per_cu resident blocks per compute unit.
+// per wavefront, a grid-stride loop over 4R-row tiles.
 struct GemvPlan {
   std::string kernel;
   uint32_t grid = 0, shared = 0;
@@ -35,25 +24,22 @@ int plan_gemv(const xpu_runtime &rt, int dtype, const void *A, const void *x, ui
               uint32_t K, uint64_t lda, GemvPlan &plan) {
   const bool vec = (reinterpret_cast<uintptr_t>(A) % 16 == 0) &&
                    (reinterpret_cast<uintptr_t>(x) % 16 == 0) && K % 8 == 0 && lda % 8 == 0;
-  uint32_t rows = env_u32("XPU_GEMV_R", 1);
-  uint32_t unroll = env_u32("XPU_GEMV_U", 4);
-  const bool known = (rows == 1 && (unroll == 4 || unroll == 8 || unroll == 16)) ||
-                     (rows == 2 && (unroll == 4 || unroll == 8)) || (rows == 4 && (unroll == 2 || unroll == 4));
-  if (!known) rows = 1, unroll = 8;
   const uint64_t kpad = (static_cast<uint64_t>(K) + 511u) & ~uint64_t{511};
   const bool global_x = kpad * 2 > rt.max_shared;
   if (global_x && !vec)
     return set_error(XPU_ERR_INVALID, "GEMV K=" + std::to_string(K) +
                                           " exceeds the LDS and needs 16-byte aligned A, x and K, lda "
                                           "multiples of 8");
-  if (global_x) rows = 1, unroll = 8;
-  if (!vec) rows = 1, unroll = 2;
+  // one row per wavefront; 512-column chunks per pipelined load batch: 4
+  // with the vector in LDS (82-84% of 8 TB/s at 16384^2 fp16, against 63-77%
+  // for 2 or 4 rows per wavefront), 8 when the vector is read from global
+  // memory, 2 for the 16-bit-load path of unaligned operands
+  const uint32_t rows = 1, unroll = !vec ? 2 : global_x ? 8 : 4;
   plan.shared = global_x ? 0 : static_cast<uint32_t>(kpad * 2);
-  const uint32_t per_cu_lds = std::max<uint32_t>(1, 163840u / std::max<uint32_t>(plan.shared, 4096));
-  const uint32_t blocks_per_cu = std::min<uint32_t>(env_u32("XPU_GEMV_BPC", 1), per_cu_lds);
+  // one block per compute unit, grid-stride over 4-row tiles: each block
+  // stages the vector once
   const uint64_t tiles = (static_cast<uint64_t>(M) + 4 * rows - 1) / (4 * rows);
-  plan.grid = static_cast<uint32_t>(
-      std::min<uint64_t>(tiles, static_cast<uint64_t>(rt.compute_units) * std::max(1u, blocks_per_cu)));
+  plan.grid = static_cast<uint32_t>(std::min<uint64_t>(tiles, rt.compute_units));
   plan.kernel = std::string("xpu_gemv_") + (dtype ? "fp16" : "bf16") + "_r" + std::to_string(rows) + "u" +
                 std::to_string(unroll) + (vec ? (global_x ? "_vecg" : "_vec") : "_any");
   return XPU_OK;
@@ -221,7 +207,6 @@ extern "C" int run_gemv(int argc, char **argv) {
     // against a sequential FP32 host sum (tolerance max(1, 1%)), plus FP64
     // error statistics in units of the output type's ulp.
     const uint32_t rows = std::min(o.m, o.check_rows);
-    bool valid = true;
     double err2 = 0, ref2 = 0, max_ulps = 0;
     if (rows) {
       std::vector<uint16_t> hy(rows), ha(static_cast<size_t>(rows) * o.k), hx(o.k);
@@ -239,7 +224,8 @@ extern "C" int run_gemv(int argc, char **argv) {
           exact += static_cast<double>(a) * xf[c];
         }
         const float actual = xpu::decode16(hy[r], o.dtype);
-        if (std::fabs(actual - expected) > std::max(1.0f, std::fabs(expected) * 0.01f)) valid = false;
+        if (std::fabs(actual - expected) > std::max(1.0f, std::fabs(expected) * 0.01f))
+          throw std::runtime_error("GEMV verification failed");  // gemv.cpp:135-136
         // error against the accumulated value rounded to the output type
         const double ref = xpu::decode16(xpu::encode16(static_cast<float>(exact), o.dtype), o.dtype);
         err2 += (actual - ref) * (actual - ref);
@@ -262,8 +248,8 @@ extern "C" int run_gemv(int argc, char **argv) {
               << ", max " << std::fixed << std::setprecision(2) << max_ulps
               << " ulp vs the FP64 sum rounded to the output type, over "
               << rows << " rows\n"
-              << "Verification: " << (valid ? "PASS" : "FAIL") << '\n';
-    return valid ? 0 : 2;
+              << "Verification: PASS\n";
+    return 0;
   } catch (const std::exception &error) {
     std::cerr << "Error: " << error.what() << '\n';
     return 1;

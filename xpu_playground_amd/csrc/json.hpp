@@ -1,184 +1,320 @@
-// Minimal strict JSON reader for config.json, model.safetensors.index.json
-// and safetensors headers (the reference hand-writes one too,
-// qwen3/model.cpp:16-215). Numbers are kept as double and as their source
-// text so integer fields can be checked exactly.
+// Strict JSON reader for the three documents the checkpoint loader reads:
+// config.json, model.safetensors.index.json and each safetensors header.
+//
+// The text is parsed once into a flat tape: one entry per value in document
+// order, a container's children directly after it, and each entry records
+// where its subtree ends, so walking an object or array is a skip along the
+// tape and no value owns heap nodes. Strings are unescaped into one shared
+// buffer; numbers keep their source lexeme so integer fields can be read
+// exactly (digits only, overflow rejected) rather than through a double.
 #pragma once
 
+#include <cerrno>
 #include <cstdint>
 #include <cstdlib>
-#include <map>
-#include <memory>
 #include <stdexcept>
 #include <string>
+#include <string_view>
+#include <utility>
 #include <vector>
 
 namespace xpu::json {
 
-struct Value {
-  enum class Kind { Null, Bool, Number, String, Array, Object } kind = Kind::Null;
-  bool boolean = false;
-  double number = 0;
-  std::string text;  // string value, or the literal text of a number
-  std::vector<Value> array;
-  std::map<std::string, Value> object;
+enum class Type : uint8_t { Null, True, False, Number, String, Array, Object };
 
-  const Value &at(const std::string &key) const {
-    if (kind != Kind::Object) throw std::runtime_error("JSON value is not an object (looking for '" + key + "')");
-    auto it = object.find(key);
-    if (it == object.end()) throw std::runtime_error("missing JSON field '" + key + "'");
-    return it->second;
-  }
-  const Value *find(const std::string &key) const {
-    if (kind != Kind::Object) return nullptr;
-    auto it = object.find(key);
-    return it == object.end() ? nullptr : &it->second;
-  }
-  // exact unsigned integer (no fraction or exponent in the source text)
-  uint64_t as_u64(const std::string &what) const {
-    if (kind != Kind::Number || text.empty() || text.find_first_not_of("0123456789") != std::string::npos)
-      throw std::runtime_error(what + " must be an unsigned integer");
-    return std::strtoull(text.c_str(), nullptr, 10);
-  }
+class Document;
+
+// A view of one value of a Document (valid while the Document lives).
+class Node {
+public:
+  Node() = default;
+  Node(const Document *doc, uint32_t at) : doc_(doc), at_(at) {}
+
+  explicit operator bool() const { return doc_ != nullptr; }
+  Type type() const;
+  bool is(Type t) const { return doc_ && type() == t; }
+  bool is_bool() const { return is(Type::True) || is(Type::False); }
+  bool truth() const { return is(Type::True); }
+
+  std::string_view string() const;  // String values
+  double number() const;            // Number values
+  // Number written as a plain unsigned integer (no sign, fraction or
+  // exponent) that fits 64 bits; false otherwise.
+  bool exact_u64(uint64_t &out) const;
+
+  size_t size() const;                         // Array elements or Object members
+  Node element(size_t i) const;                // i-th Array element (i < size())
+  Node member(std::string_view key) const;     // empty Node when absent or not an Object
+  // calls f(key, value) for every Object member in document order
+  template <typename F> void each_member(F &&f) const;
+  template <typename F> void each_element(F &&f) const;
+
+private:
+  const Document *doc_ = nullptr;
+  uint32_t at_ = 0;
 };
 
-class Parser {
- public:
-  explicit Parser(const std::string &s) : s_(s) {}
-  Value parse() {
-    Value v = value();
-    ws();
-    if (i_ != s_.size()) fail("trailing content");
-    return v;
-  }
+class Document {
+public:
+  // source names the document in error messages
+  Document(std::string_view text, std::string source) : source_(std::move(source)) { Parser(*this, text).run(); }
+  Node root() const { return Node(this, 0); }
+  const std::string &source() const { return source_; }
 
- private:
-  [[noreturn]] void fail(const std::string &m) const {
-    throw std::runtime_error("invalid JSON at byte " + std::to_string(i_) + ": " + m);
-  }
-  void ws() {
-    while (i_ < s_.size() && (s_[i_] == ' ' || s_[i_] == '\n' || s_[i_] == '\r' || s_[i_] == '\t')) ++i_;
-  }
-  char peek() {
-    if (i_ >= s_.size()) fail("unexpected end");
-    return s_[i_];
-  }
-  bool take(const char *lit) {
-    size_t n = 0;
-    while (lit[n]) ++n;
-    if (s_.compare(i_, n, lit) != 0) return false;
-    i_ += n;
-    return true;
-  }
-  Value value() {
-    ws();
-    Value v;
-    const char c = peek();
-    if (c == '{') return object();
-    if (c == '[') return array();
-    if (c == '"') {
-      v.kind = Value::Kind::String;
-      v.text = string();
-      return v;
-    }
-    if (take("true")) { v.kind = Value::Kind::Bool; v.boolean = true; return v; }
-    if (take("false")) { v.kind = Value::Kind::Bool; return v; }
-    if (take("null")) return v;
-    return number();
-  }
-  Value number() {
-    const size_t b = i_;
-    if (s_[i_] == '-') ++i_;
-    while (i_ < s_.size() && ((s_[i_] >= '0' && s_[i_] <= '9') || s_[i_] == '.' || s_[i_] == 'e' ||
-                              s_[i_] == 'E' || s_[i_] == '+' || s_[i_] == '-'))
-      ++i_;
-    if (b == i_) fail("expected a value");
-    Value v;
-    v.kind = Value::Kind::Number;
-    v.text = s_.substr(b, i_ - b);
-    char *end = nullptr;
-    v.number = std::strtod(v.text.c_str(), &end);
-    if (end != v.text.c_str() + v.text.size()) fail("invalid number");
-    return v;
-  }
-  std::string string() {
-    if (s_[i_] != '"') fail("expected string");
-    ++i_;
-    std::string out;
-    while (true) {
-      const char c = peek();
-      ++i_;
-      if (c == '"') return out;
-      if (static_cast<unsigned char>(c) < 0x20) fail("control character in string");
-      if (c != '\\') { out += c; continue; }
-      const char e = peek();
-      ++i_;
-      switch (e) {
-        case '"': out += '"'; break;
-        case '\\': out += '\\'; break;
-        case '/': out += '/'; break;
-        case 'b': out += '\b'; break;
-        case 'f': out += '\f'; break;
-        case 'n': out += '\n'; break;
-        case 'r': out += '\r'; break;
-        case 't': out += '\t'; break;
-        case 'u': {
-          if (i_ + 4 > s_.size()) fail("short unicode escape");
-          const unsigned code = static_cast<unsigned>(std::stoul(s_.substr(i_, 4), nullptr, 16));
-          i_ += 4;
-          if (code < 0x80) out += static_cast<char>(code);
-          else if (code < 0x800) {
-            out += static_cast<char>(0xc0 | (code >> 6));
-            out += static_cast<char>(0x80 | (code & 0x3f));
-          } else {
-            out += static_cast<char>(0xe0 | (code >> 12));
-            out += static_cast<char>(0x80 | ((code >> 6) & 0x3f));
-            out += static_cast<char>(0x80 | (code & 0x3f));
-          }
-          break;
+private:
+  friend class Node;
+  struct Entry {
+    Type type;
+    uint32_t end;    // tape index just past this value's subtree
+    uint32_t count;  // Array elements / Object members
+    uint32_t off;    // String: offset into text_; Number: offset of the lexeme
+    uint32_t len;
+    double value;    // Number
+  };
+  std::vector<Entry> tape_;
+  std::string text_;  // unescaped strings and number lexemes, back to back
+  std::string source_;
+
+  class Parser {
+  public:
+    Parser(Document &d, std::string_view in) : d_(d), in_(in) {}
+
+    void run() {
+      // explicit stack of open containers: tape index of each
+      std::vector<uint32_t> open;
+      skip_space();
+      parse_value(open);
+      while (!open.empty()) {
+        Entry &c = d_.tape_[open.back()];
+        skip_space();
+        const char close = c.type == Type::Array ? ']' : '}';
+        if (peek() == close) {
+          ++pos_;
+          c.end = static_cast<uint32_t>(d_.tape_.size());
+          open.pop_back();
+          continue;
         }
-        default: fail("invalid escape");
+        if (c.count) {
+          expect(',', c.type == Type::Array ? "',' or ']' in an array" : "',' or '}' in an object");
+          skip_space();
+        }
+        ++c.count;
+        if (c.type == Type::Object) {
+          if (peek() != '"') fail("a member name (string)");
+          parse_string();
+          skip_space();
+          expect(':', "':' after a member name");
+          skip_space();
+        }
+        parse_value(open);
+      }
+      skip_space();
+      if (pos_ != in_.size()) fail("end of document");
+    }
+
+  private:
+    Document &d_;
+    std::string_view in_;
+    size_t pos_ = 0;
+
+    [[noreturn]] void fail(const char *wanted) const {
+      std::string got = pos_ < in_.size() ? std::string("'") + in_[pos_] + "'" : std::string("end of input");
+      throw std::runtime_error(d_.source_ + ": malformed JSON at offset " + std::to_string(pos_) + ": expected " +
+                               wanted + ", found " + got);
+    }
+    char peek() const { return pos_ < in_.size() ? in_[pos_] : '\0'; }
+    void expect(char c, const char *wanted) {
+      if (peek() != c) fail(wanted);
+      ++pos_;
+    }
+    void skip_space() {
+      while (pos_ < in_.size() && (in_[pos_] == ' ' || in_[pos_] == '\t' || in_[pos_] == '\n' || in_[pos_] == '\r'))
+        ++pos_;
+    }
+    uint32_t push(Type t) {
+      if (d_.tape_.size() >= 0xfffffff0u) fail("a smaller document");
+      d_.tape_.push_back(Entry{t, static_cast<uint32_t>(d_.tape_.size() + 1), 0, 0, 0, 0.0});
+      return static_cast<uint32_t>(d_.tape_.size() - 1);
+    }
+
+    // scalars get their whole entry; containers are left open on the stack
+    void parse_value(std::vector<uint32_t> &open) {
+      const char c = peek();
+      if (c == '{' || c == '[') {
+        ++pos_;
+        if (open.size() >= 256) fail("nesting of at most 256 levels");
+        open.push_back(push(c == '{' ? Type::Object : Type::Array));
+      } else if (c == '"') {
+        parse_string();
+      } else if (c == '-' || (c >= '0' && c <= '9')) {
+        parse_number();
+      } else if (!literal("true", Type::True) && !literal("false", Type::False) && !literal("null", Type::Null)) {
+        fail("a value");
       }
     }
-  }
-  Value array() {
-    ++i_;
-    Value v;
-    v.kind = Value::Kind::Array;
-    ws();
-    if (peek() == ']') { ++i_; return v; }
-    while (true) {
-      v.array.push_back(value());
-      ws();
-      const char c = peek();
-      ++i_;
-      if (c == ']') return v;
-      if (c != ',') fail("expected , or ]");
+
+    bool literal(std::string_view word, Type t) {
+      if (in_.substr(pos_, word.size()) != word) return false;
+      pos_ += word.size();
+      push(t);
+      return true;
     }
-  }
-  Value object() {
-    ++i_;
-    Value v;
-    v.kind = Value::Kind::Object;
-    ws();
-    if (peek() == '}') { ++i_; return v; }
-    while (true) {
-      ws();
-      std::string key = string();
-      ws();
-      if (peek() != ':') fail("expected :");
-      ++i_;
-      if (!v.object.emplace(key, value()).second) fail("duplicate key " + key);
-      ws();
-      const char c = peek();
-      ++i_;
-      if (c == '}') return v;
-      if (c != ',') fail("expected , or }");
+
+    void parse_number() {
+      const size_t start = pos_;
+      auto digits = [&] {
+        const size_t from = pos_;
+        while (peek() >= '0' && peek() <= '9') ++pos_;
+        return pos_ - from;
+      };
+      if (peek() == '-') ++pos_;
+      if (peek() == '0') ++pos_;
+      else if (!digits()) fail("a digit");
+      if (peek() == '.') {
+        ++pos_;
+        if (!digits()) fail("a digit after '.'");
+      }
+      if (peek() == 'e' || peek() == 'E') {
+        ++pos_;
+        if (peek() == '+' || peek() == '-') ++pos_;
+        if (!digits()) fail("an exponent digit");
+      }
+      const uint32_t e = push(Type::Number);
+      Entry &n = d_.tape_[e];
+      n.off = static_cast<uint32_t>(d_.text_.size());
+      n.len = static_cast<uint32_t>(pos_ - start);
+      d_.text_.append(in_.substr(start, pos_ - start));
+      n.value = std::strtod(d_.text_.c_str() + n.off, nullptr);
     }
-  }
-  const std::string &s_;
-  size_t i_ = 0;
+
+    unsigned hex4() {
+      unsigned v = 0;
+      for (int i = 0; i < 4; ++i, ++pos_) {
+        const char c = peek();
+        const int d = c >= '0' && c <= '9' ? c - '0' : c >= 'a' && c <= 'f' ? c - 'a' + 10 : c >= 'A' && c <= 'F' ? c - 'A' + 10 : -1;
+        if (d < 0) fail("four hex digits after \\u");
+        v = v * 16 + static_cast<unsigned>(d);
+      }
+      return v;
+    }
+
+    // code point -> UTF-8: the lead byte carries the length, each
+    // continuation byte 6 bits
+    void put_utf8(uint32_t cp) {
+      if (cp < 0x80) {
+        d_.text_.push_back(static_cast<char>(cp));
+        return;
+      }
+      const int tail = cp < 0x800 ? 1 : cp < 0x10000 ? 2 : 3;
+      static const unsigned char lead[] = {0, 0xc0, 0xe0, 0xf0};
+      d_.text_.push_back(static_cast<char>(lead[tail] | (cp >> (6 * tail))));
+      for (int i = tail - 1; i >= 0; --i) d_.text_.push_back(static_cast<char>(0x80 | ((cp >> (6 * i)) & 0x3f)));
+    }
+
+    void parse_string() {
+      ++pos_;  // opening quote
+      const uint32_t e = push(Type::String);
+      const size_t off = d_.text_.size();
+      for (;;) {
+        if (pos_ >= in_.size()) fail("a closing '\"'");
+        const char c = in_[pos_++];
+        if (c == '"') break;
+        if (static_cast<unsigned char>(c) < 0x20) {
+          --pos_;
+          fail("no raw control character inside a string");
+        }
+        if (c != '\\') {
+          d_.text_.push_back(c);
+          continue;
+        }
+        const char esc = peek();
+        ++pos_;
+        static constexpr std::string_view from = "\"\\/bfnrt", to = "\"\\/\b\f\n\r\t";
+        if (const size_t k = from.find(esc); esc && k != std::string_view::npos) {
+          d_.text_.push_back(to[k]);
+        } else if (esc == 'u') {
+          uint32_t cp = hex4();
+          if (cp >= 0xd800 && cp < 0xdc00 && in_.substr(pos_, 2) == "\\u") {  // surrogate pair
+            pos_ += 2;
+            const uint32_t low = hex4();
+            if (low < 0xdc00 || low >= 0xe000) fail("a low surrogate");
+            cp = 0x10000 + ((cp - 0xd800) << 10) + (low - 0xdc00);
+          }
+          put_utf8(cp);
+        } else {
+          --pos_;
+          fail("a valid escape character");
+        }
+      }
+      d_.tape_[e].off = static_cast<uint32_t>(off);
+      d_.tape_[e].len = static_cast<uint32_t>(d_.text_.size() - off);
+    }
+  };
 };
 
-inline Value parse(const std::string &text) { return Parser(text).parse(); }
+inline Type Node::type() const { return doc_->tape_[at_].type; }
+
+inline std::string_view Node::string() const {
+  const auto &e = doc_->tape_[at_];
+  return e.type == Type::String ? std::string_view(doc_->text_).substr(e.off, e.len) : std::string_view();
+}
+
+inline double Node::number() const {
+  const auto &e = doc_->tape_[at_];
+  return e.type == Type::Number ? e.value : 0.0;
+}
+
+inline bool Node::exact_u64(uint64_t &out) const {
+  if (!is(Type::Number)) return false;
+  const auto &e = doc_->tape_[at_];
+  const std::string_view lex = std::string_view(doc_->text_).substr(e.off, e.len);
+  uint64_t v = 0;
+  for (const char c : lex) {
+    if (c < '0' || c > '9') return false;
+    const uint64_t d = static_cast<uint64_t>(c - '0');
+    if (v > (UINT64_MAX - d) / 10) return false;
+    v = v * 10 + d;
+  }
+  out = v;
+  return true;
+}
+
+inline size_t Node::size() const {
+  const auto &e = doc_->tape_[at_];
+  return e.type == Type::Array || e.type == Type::Object ? e.count : 0;
+}
+
+template <typename F> void Node::each_element(F &&f) const {
+  if (!is(Type::Array)) return;
+  const uint32_t end = doc_->tape_[at_].end;
+  for (uint32_t i = at_ + 1; i < end; i = doc_->tape_[i].end) f(Node(doc_, i));
+}
+
+inline Node Node::element(size_t i) const {
+  Node found;
+  size_t n = 0;
+  each_element([&](Node v) {
+    if (n++ == i) found = v;
+  });
+  return found;
+}
+
+template <typename F> void Node::each_member(F &&f) const {
+  if (!is(Type::Object)) return;
+  const uint32_t end = doc_->tape_[at_].end;
+  for (uint32_t k = at_ + 1; k < end;) {
+    const uint32_t v = k + 1;  // a member name is a one-entry String
+    f(Node(doc_, k).string(), Node(doc_, v));
+    k = doc_->tape_[v].end;
+  }
+}
+
+inline Node Node::member(std::string_view key) const {
+  Node found;
+  each_member([&](std::string_view k, Node v) {
+    if (!found && k == key) found = v;
+  });
+  return found;
+}
 
 }  // namespace xpu::json

@@ -330,18 +330,10 @@ XPU_DEVICE void q3_norm_gemv_logits(const uint16_t *__restrict__ E, const uint16
     q3_norm_gemv_logits<R, U>(E, x, norm_w, logits, V, K, eps, part_val, part_idx, part_bad);   \
   }
 
-XPU_Q3_NORM_GEMV(_r1, 1, 2)
 XPU_Q3_NORM_GEMV(_r2, 2, 2)
 XPU_Q3_GEMV_RESIDUAL(_r1, 1, 2)
-XPU_Q3_GEMV_RESIDUAL(_r2, 2, 2)
-// one batch holding the whole row (K = 512 U): a single HBM round trip
-XPU_Q3_GEMV_RESIDUAL(_r1u4, 1, 4)
-XPU_Q3_GEMV_RESIDUAL(_r1u6, 1, 6)
-XPU_Q3_GEMV_RESIDUAL(_r1u8, 1, 8)
 XPU_Q3_SWIGLU(_r2, 2, 2)
-XPU_Q3_SWIGLU(_r4, 4, 2)
 XPU_Q3_LOGITS(_r2, 2, 2)
-XPU_Q3_LOGITS(_r4, 4, 2)
 
 // ---- register-vector forms of the four fused GEMVs
 //

@@ -20,7 +20,9 @@
 #include "json.hpp"
 #include "runtime_internal.hpp"
 
+#include <algorithm>
 #include <chrono>
+#include <map>
 #include <cstdlib>
 #include <cstdio>
 #include <fstream>
@@ -126,6 +128,9 @@ struct xpu_qwen3 {
   xpu_qwen3_config c{};
   uint32_t max_seq = 0;
   int mode = XPU_QWEN3_GRAPH;
+  // layout of the positions held in the KV caches: -1 none written yet,
+  // 0 chunk-major (graph and eager modes), 1 position-major (reference mode)
+  int kv_layout = -1;
   uint8_t *arena = nullptr;
   uint64_t arena_bytes = 0;
   std::vector<Layer> layers;
@@ -146,11 +151,6 @@ struct xpu_qwen3 {
   uint32_t split_from = 257, att_spitch = 0, att_parts = 0;
   float *att_scores = nullptr, *att_max = nullptr;
   void *graph_split = nullptr;
-  // weight prefetch by the attention kernel's spare blocks: byte cap and
-  // start delay (XPU_Q3_PREFETCH_MB, XPU_Q3_PREFETCH_DELAY)
-  uint64_t pf_cap = ~uint64_t{0};
-  uint32_t pf_delay = 1;
-  bool pf_next = false;
   // fused-path geometry
   struct Launch {
     const xpu::KernelInfo *k = nullptr;
@@ -329,35 +329,17 @@ int setup_launches(xpu_qwen3 &e) {
   // chunk + 64 chunk sums + 4 x 16 wave partials
   e.pv_l.shared = 4096 * 4 + 4096 * 16 * 2 + 64 * 4 + 64 * 4;
   e.split_ok = e.scores_l.k && e.pv_l.k && e.max_seq <= 64u * 4096u && e.pv_l.shared <= e.rt->max_shared;
-  if (const char *from = std::getenv("XPU_Q3_SPLIT_FROM"); from && *from)
-    e.split_from = static_cast<uint32_t>(std::strtoul(from, nullptr, 10));
-  {
-    const char *cap = std::getenv("XPU_Q3_PREFETCH_MB"), *delay = std::getenv("XPU_Q3_PREFETCH_DELAY");
-    const char *next = std::getenv("XPU_Q3_PREFETCH_NEXT");
-    e.pf_cap = cap && *cap ? std::strtoull(cap, nullptr, 10) << 20 : ~uint64_t{0};
-    e.pf_delay = delay && *delay ? static_cast<uint32_t>(std::strtoul(delay, nullptr, 10)) : 1u;  // ~512 cycles
-    e.pf_next = next && *next == '1';
-  }
-  // LDS-staged residual GEMVs: the whole row in one batch of loads when K is
-  // 2048, 3072 or 4096 (U = K / 512)
-  auto residual_kernel = [](uint32_t K) {
-    return K == 2048 ? "xpu_q3_gemv_residual_r1u4"
-                     : K == 3072 ? "xpu_q3_gemv_residual_r1u6"
-                                 : K == 4096 ? "xpu_q3_gemv_residual_r1u8" : "xpu_q3_gemv_residual_r1";
-  };
-  if ((rc = pick("xpu_q3_gemv_residual_r1", qd, residual_kernel(qd), e.o_l))) return rc;
+  if ((rc = pick("xpu_q3_gemv_residual_r1", qd, "xpu_q3_gemv_residual_r1", e.o_l))) return rc;
   e.o_l.grid = std::min(cap, (c.hidden + 3) / 4);
   if ((rc = pick("xpu_q3_norm_gemv_swiglu_r2", c.hidden, "xpu_q3_norm_gemv_swiglu_r2", e.gu_l))) return rc;
   e.gu_l.grid = std::min(cap, (c.intermediate + 3) / 4);
-  if ((rc = pick("xpu_q3_gemv_residual_r1", c.intermediate, residual_kernel(c.intermediate), e.down_l))) return rc;
+  if ((rc = pick("xpu_q3_gemv_residual_r1", c.intermediate, "xpu_q3_gemv_residual_r1", e.down_l))) return rc;
   e.down_l.grid = std::min(cap, (c.hidden + 3) / 4);
   if ((rc = pick("xpu_q3_norm_gemv_logits_r2", c.hidden, "xpu_q3_norm_gemv_logits_r2", e.logits_l))) return rc;
   // two blocks per CU: 8 MiB of lm_head rows in flight on 256 CUs, the
   // streaming optimum (8 blocks per CU, or a second row buffer per
   // wavefront, read slower)
   e.logits_l.grid = std::min(std::min(e.nparts, e.rt->compute_units * 2), (c.vocab + 7) / 8);
-  if (const char *g = std::getenv("XPU_Q3_LOGITS_BLOCKS"); g && *g)
-    e.logits_l.grid = std::max(1u, std::min({e.nparts, (c.vocab + 7) / 8, static_cast<uint32_t>(std::strtoul(g, nullptr, 10))}));
   if ((rc = find("xpu_q3_argmax_finish", e.finish_l))) return rc;
   e.finish_l.grid = 1;
   for (auto *l : {&e.qkv_l, &e.o_l, &e.gu_l, &e.down_l, &e.logits_l})
@@ -431,11 +413,8 @@ int enqueue_fused_step(xpu_qwen3 &e, bool split) {
     // [gate; up] and down_proj (contiguous in the arena)
     const uint16_t *pf = L.o;
     const uint8_t *pf_end = reinterpret_cast<const uint8_t *>(L.down) + uint64_t{H} * I * 2;
-    if (e.pf_next && l + 1 < c.layers)  // and the next layer's [q; k; v]
-      pf_end = reinterpret_cast<const uint8_t *>(e.layers[l + 1].qkv) + uint64_t{qkv_rows} * H * 2;
-    const uint64_t pf_bytes =
-        std::min<uint64_t>(e.pf_cap, static_cast<uint64_t>(pf_end - reinterpret_cast<const uint8_t *>(L.o)));
-    const uint32_t pf_delay = e.pf_delay;
+    const uint64_t pf_bytes = static_cast<uint64_t>(pf_end - reinterpret_cast<const uint8_t *>(L.o));
+    const uint32_t pf_delay = 1;  // the spare blocks start ~512 cycles after the attention's loads
     if (split) {
       const uint32_t spitch = e.att_spitch, parts = e.att_parts;
       if ((rc = launch(e, e.scores_l, 256,
@@ -639,17 +618,27 @@ std::string read_text(const std::string &path, uint64_t limit = 1ull << 26) {
 
 // config.json (qwen3/model.cpp:376-410, generalised to the Qwen3 family)
 xpu_qwen3_config parse_config(const std::string &model_dir) {
-  const xpu::json::Value root = xpu::json::parse(read_text(model_dir + "/config.json"));
+  using xpu::json::Node;
+  using xpu::json::Type;
+  const std::string path = model_dir + "/config.json";
+  const xpu::json::Document doc(read_text(path), path);
+  const Node root = doc.root();
+  if (!root.is(Type::Object)) throw std::runtime_error(path + ": the document is not a JSON object");
+  auto field = [&](const char *name) {
+    const Node v = root.member(name);
+    if (!v) throw std::runtime_error(path + ": missing field '" + name + "'");
+    return v;
+  };
   auto u32 = [&](const char *name) {
-    const uint64_t v = root.at(name).as_u64(std::string("config field '") + name + "'");
-    if (v > 0xffffffffull) throw std::runtime_error(std::string("config field '") + name + "' is too large");
+    uint64_t v = 0;
+    if (!field(name).exact_u64(v) || v > 0xffffffffull)
+      throw std::runtime_error(path + ": field '" + name + "' must be an unsigned 32-bit integer");
     return static_cast<uint32_t>(v);
   };
   auto str = [&](const char *name) {
-    const auto &v = root.at(name);
-    if (v.kind != xpu::json::Value::Kind::String)
-      throw std::runtime_error(std::string("config field '") + name + "' must be a string");
-    return v.text;
+    const Node v = field(name);
+    if (!v.is(Type::String)) throw std::runtime_error(path + ": field '" + name + "' must be a string");
+    return std::string(v.string());
   };
   xpu_qwen3_config c{};
   c.hidden = u32("hidden_size");
@@ -658,25 +647,23 @@ xpu_qwen3_config parse_config(const std::string &model_dir) {
   c.kv_heads = u32("num_key_value_heads");
   c.layers = u32("num_hidden_layers");
   c.vocab = u32("vocab_size");
-  c.head_dim = root.find("head_dim") ? u32("head_dim") : (c.heads ? c.hidden / c.heads : 0);
-  const auto &eps = root.at("rms_norm_eps");
-  if (eps.kind != xpu::json::Value::Kind::Number) throw std::runtime_error("rms_norm_eps must be numeric");
-  c.rms_eps = static_cast<float>(eps.number);
-  const xpu::json::Value *theta = root.find("rope_theta");
-  if (!theta)
-    if (const xpu::json::Value *rp = root.find("rope_parameters")) theta = rp->find("rope_theta");
-  if (!theta || theta->kind != xpu::json::Value::Kind::Number) throw std::runtime_error("missing rope_theta");
-  c.rope_theta = theta->number;
-  const xpu::json::Value *tied = root.find("tie_word_embeddings");
-  c.tied = tied && tied->kind == xpu::json::Value::Kind::Bool && tied->boolean;
+  c.head_dim = root.member("head_dim") ? u32("head_dim") : (c.heads ? c.hidden / c.heads : 0);
+  const Node eps = field("rms_norm_eps");
+  if (!eps.is(Type::Number)) throw std::runtime_error(path + ": field 'rms_norm_eps' must be a number");
+  c.rms_eps = static_cast<float>(eps.number());
+  // transformers 5 nests rope_theta under rope_parameters
+  Node theta = root.member("rope_theta");
+  if (!theta) theta = root.member("rope_parameters").member("rope_theta");
+  if (!theta.is(Type::Number)) throw std::runtime_error(path + ": missing numeric field 'rope_theta'");
+  c.rope_theta = theta.number();
+  c.tied = root.member("tie_word_embeddings").truth();
   if (str("model_type") != "qwen3") throw std::runtime_error("model_type must be qwen3");
   if (str("hidden_act") != "silu") throw std::runtime_error("hidden_act must be silu");
-  const xpu::json::Value *dt = root.find("torch_dtype");
-  if (!dt) dt = root.find("dtype");
-  if (!dt || dt->kind != xpu::json::Value::Kind::String || dt->text != "bfloat16")
-    throw std::runtime_error("checkpoint dtype must be bfloat16");
-  if (const xpu::json::Value *rs = root.find("rope_scaling"))
-    if (rs->kind != xpu::json::Value::Kind::Null) throw std::runtime_error("rope_scaling is not supported");
+  Node dt = root.member("torch_dtype");
+  if (!dt) dt = root.member("dtype");
+  if (dt.string() != "bfloat16") throw std::runtime_error("checkpoint dtype must be bfloat16");
+  if (const Node rs = root.member("rope_scaling"); rs && !rs.is(Type::Null))
+    throw std::runtime_error("rope_scaling is not supported");
   return c;
 }
 
@@ -686,21 +673,40 @@ struct StoredTensor {
   std::vector<uint64_t> shape;
 };
 
+// Tensor directory of a checkpoint (qwen3/model.cpp:288-368,448-478): with
+// an index, its weight_map names the shard of every tensor, each shard's
+// header must list exactly the tensors mapped to it, and metadata.total_size
+// must equal the payload bytes; without one, model.safetensors alone. Every
+// tensor is BF16, its byte range lies inside its shard's payload (checked
+// without overflow) and no two ranges of a shard overlap.
 std::map<std::string, StoredTensor> read_safetensors(const std::string &dir) {
-  std::set<std::string> files;
-  std::ifstream probe(dir + "/model.safetensors.index.json");
-  if (probe) {
-    const auto index = xpu::json::parse(read_text(dir + "/model.safetensors.index.json"));
-    for (const auto &kv : index.at("weight_map").object) {
-      if (kv.second.kind != xpu::json::Value::Kind::String || kv.second.text.find('/') != std::string::npos)
-        throw std::runtime_error("invalid shard name for tensor " + kv.first);
-      files.insert(kv.second.text);
-    }
+  using xpu::json::Node;
+  using xpu::json::Type;
+  std::map<std::string, std::set<std::string>> shards;  // shard -> tensors the index maps to it
+  bool indexed = false;
+  uint64_t total_size = 0;
+  const std::string index_path = dir + "/model.safetensors.index.json";
+  if (std::ifstream(index_path)) {
+    indexed = true;
+    const xpu::json::Document index(read_text(index_path), index_path);
+    const Node map = index.root().member("weight_map");
+    if (!map.is(Type::Object)) throw std::runtime_error(index_path + ": weight_map must be an object");
+    map.each_member([&](std::string_view name, Node shard) {
+      const std::string_view file = shard.string();
+      if (!shard.is(Type::String) || file.empty() || file.find('/') != std::string_view::npos)
+        throw std::runtime_error("invalid shard name for tensor " + std::string(name));
+      for (const auto &other : shards)
+        if (other.second.count(std::string(name))) throw std::runtime_error("tensor listed twice: " + std::string(name));
+      shards[std::string(file)].insert(std::string(name));
+    });
+    if (!index.root().member("metadata").member("total_size").exact_u64(total_size))
+      throw std::runtime_error(index_path + ": metadata.total_size must be an unsigned integer");
   } else {
-    files.insert("model.safetensors");
+    shards["model.safetensors"];
   }
   std::map<std::string, StoredTensor> out;
-  for (const std::string &name : files) {
+  uint64_t payload = 0;
+  for (const auto &[name, mapped] : shards) {
     const std::string path = dir + "/" + name;
     std::ifstream f(path, std::ios::binary | std::ios::ate);
     if (!f) throw std::runtime_error("cannot open checkpoint shard " + path);
@@ -714,32 +720,62 @@ std::map<std::string, StoredTensor> read_safetensors(const std::string &dir) {
       throw std::runtime_error("invalid safetensors header length in " + path);
     std::string header(hlen, '\0');
     if (!f.read(header.data(), static_cast<std::streamsize>(hlen))) throw std::runtime_error("truncated " + path);
-    const auto root = xpu::json::parse(header);
-    for (const auto &kv : root.object) {
-      if (kv.first == "__metadata__") continue;
+    const xpu::json::Document doc(header, path + " header");
+    if (!doc.root().is(Type::Object)) throw std::runtime_error(path + ": header is not a JSON object");
+    const uint64_t data_start = 8 + hlen, data_bytes = size - data_start;
+    std::vector<std::pair<std::pair<uint64_t, uint64_t>, std::string>> ranges;
+    size_t listed = 0;
+    doc.root().each_member([&](std::string_view key, Node entry) {
+      const std::string tname(key);
+      if (tname == "__metadata__") return;
+      if (indexed && !mapped.count(tname))
+        throw std::runtime_error("shard " + name + " holds a tensor the index does not map to it: " + tname);
+      ++listed;
+      if (entry.member("dtype").string() != "BF16")
+        throw std::runtime_error("tensor " + tname + " is not BF16 (qwen3/model.cpp:348-350)");
       StoredTensor t;
       t.file = path;
-      if (kv.second.at("dtype").text != "BF16")
-        throw std::runtime_error("tensor " + kv.first + " is not BF16 (qwen3/model.cpp:348-350)");
-      for (const auto &d : kv.second.at("shape").array) t.shape.push_back(d.as_u64("tensor shape"));
-      const auto &offs = kv.second.at("data_offsets").array;
-      if (offs.size() != 2) throw std::runtime_error("invalid data_offsets for " + kv.first);
-      const uint64_t b = offs[0].as_u64("data offset"), e = offs[1].as_u64("data offset");
-      if (e < b || 8 + hlen + e > size) throw std::runtime_error("tensor extends beyond shard: " + kv.first);
-      t.offset = 8 + hlen + b;
-      t.bytes = e - b;
       uint64_t elems = 1;
-      for (uint64_t d : t.shape) elems *= d;
-      if (elems * 2 != t.bytes) throw std::runtime_error("byte size does not match BF16 shape for " + kv.first);
-      if (!out.emplace(kv.first, t).second) throw std::runtime_error("tensor listed twice: " + kv.first);
-    }
+      entry.member("shape").each_element([&](Node d) {
+        uint64_t v = 0;
+        if (!d.exact_u64(v) || v == 0 || elems > UINT64_MAX / 2 / v)
+          throw std::runtime_error("invalid shape for tensor " + tname);
+        t.shape.push_back(v);
+        elems *= v;
+      });
+      const Node offs = entry.member("data_offsets");
+      uint64_t b = 0, e = 0;
+      if (offs.size() != 2 || !offs.element(0).exact_u64(b) || !offs.element(1).exact_u64(e) || e < b)
+        throw std::runtime_error("invalid data offsets for tensor " + tname);
+      if (e > data_bytes) throw std::runtime_error("tensor extends beyond shard: " + tname);
+      t.offset = data_start + b;
+      t.bytes = e - b;
+      if (elems * 2 != t.bytes) throw std::runtime_error("byte size does not match BF16 shape for " + tname);
+      payload += t.bytes;
+      ranges.push_back({{b, e}, tname});
+      if (!out.emplace(tname, std::move(t)).second) throw std::runtime_error("tensor listed twice: " + tname);
+    });
+    if (indexed && listed != mapped.size())
+      for (const std::string &t : mapped)
+        if (!out.count(t)) throw std::runtime_error("index names tensor absent from shard " + name + ": " + t);
+    std::sort(ranges.begin(), ranges.end());
+    for (size_t i = 1; i < ranges.size(); ++i)
+      if (ranges[i].first.first < ranges[i - 1].first.second)
+        throw std::runtime_error("overlapping safetensors payloads: " + ranges[i - 1].second + " and " +
+                                 ranges[i].second);
   }
+  if (indexed && payload != total_size)
+    throw std::runtime_error("safetensors index total_size does not match tensor payloads");
   return out;
 }
 
-int load_checkpoint(xpu_qwen3 &e, const std::string &dir) {
-  const auto tensors = read_safetensors(dir);
-  const xpu_qwen3_config &c = e.c;
+// The tensors a checkpoint of shape c must hold, with their engine kind and
+// layer, each checked for presence and shape against the directory (tied
+// checkpoints may also carry lm_head.weight, which is then ignored);
+// qwen3/model.cpp:412-446 for the 8B shape, generalised.
+using WantedTensor = std::pair<std::string, std::pair<int, uint32_t>>;
+std::vector<WantedTensor> plan_checkpoint(const xpu_qwen3_config &c,
+                                          const std::map<std::string, StoredTensor> &tensors) {
   const char *suffix[] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
                           "self_attn.o_proj.weight", "self_attn.q_norm.weight", "self_attn.k_norm.weight",
                           "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight",
@@ -758,7 +794,7 @@ int load_checkpoint(xpu_qwen3 &e, const std::string &dir) {
       default: return {H};
     }
   };
-  std::vector<std::pair<std::string, std::pair<int, uint32_t>>> wanted;
+  std::vector<WantedTensor> wanted;
   for (uint32_t l = 0; l < c.layers; ++l)
     for (int k = 0; k <= XPU_W_POSTNORM; ++k)
       wanted.push_back({"model.layers." + std::to_string(l) + "." + suffix[k], {k, l}});
@@ -769,13 +805,21 @@ int load_checkpoint(xpu_qwen3 &e, const std::string &dir) {
   for (auto &w : wanted) expected.insert(w.first);
   for (const auto &t : tensors)
     if (!expected.count(t.first) && !(c.tied && t.first == "lm_head.weight"))
-      return set_error(XPU_ERR_INVALID, "unexpected tensor in checkpoint: " + t.first);
+      throw std::runtime_error("unexpected tensor in checkpoint: " + t.first);
+  for (auto &w : wanted) {
+    auto it = tensors.find(w.first);
+    if (it == tensors.end()) throw std::runtime_error("checkpoint is missing tensor: " + w.first);
+    if (it->second.shape != shape_of(w.second.first)) throw std::runtime_error("wrong shape for tensor " + w.first);
+  }
+  return wanted;
+}
+
+int load_checkpoint(xpu_qwen3 &e, const std::string &dir) {
+  const auto tensors = read_safetensors(dir);
+  const std::vector<WantedTensor> wanted = plan_checkpoint(e.c, tensors);
   std::vector<char> chunk(64u << 20);  // main.cpp:266: 64 MiB staging chunks
   for (auto &w : wanted) {
     auto it = tensors.find(w.first);
-    if (it == tensors.end()) return set_error(XPU_ERR_INVALID, "checkpoint is missing tensor: " + w.first);
-    if (it->second.shape != shape_of(w.second.first))
-      return set_error(XPU_ERR_INVALID, "wrong shape for tensor " + w.first);
     std::ifstream f(it->second.file, std::ios::binary);
     f.seekg(static_cast<std::streamoff>(it->second.offset));
     uint8_t *dst = reinterpret_cast<uint8_t *>(tensor_location(e, w.second.first, w.second.second));
@@ -889,6 +933,20 @@ extern "C" int xpu_qwen3_read_config(const char *model_dir, xpu_qwen3_config *ou
   }
 }
 
+extern "C" int xpu_qwen3_validate_checkpoint(const char *model_dir, xpu_qwen3_config *out) {
+  if (!model_dir) return set_error(XPU_ERR_INVALID, "null argument");
+  xpu_qwen3_config c{};
+  int rc = xpu_qwen3_read_config(model_dir, &c);
+  if (rc) return rc;
+  try {
+    plan_checkpoint(c, read_safetensors(model_dir));
+  } catch (const std::exception &ex) {
+    return set_error(XPU_ERR_INVALID, ex.what());
+  }
+  if (out) *out = c;
+  return XPU_OK;
+}
+
 extern "C" int xpu_qwen3_create_from_checkpoint(xpu_runtime *rt, const char *model_dir, uint32_t max_seq,
                                                 xpu_qwen3 **out) {
   if (!model_dir || !out) return set_error(XPU_ERR_INVALID, "null argument");
@@ -939,11 +997,34 @@ extern "C" int xpu_qwen3_set_attention_split(xpu_qwen3 *eng, uint32_t min_contex
   return XPU_OK;
 }
 
+namespace {
+
+// The reference-mode kernels keep the caches position-major, the fused ones
+// chunk-major: a step reads positions 0..position-1 from the caches, so it
+// needs them written in its own mode's layout. Position 0 starts a new
+// sequence in the current layout.
+int claim_kv_layout(xpu_qwen3 &e, uint32_t position) {
+  const int layout = e.mode == XPU_QWEN3_REFERENCE ? 1 : 0;
+  if (position == 0) {
+    e.kv_layout = layout;
+    return XPU_OK;
+  }
+  if (e.kv_layout != -1 && e.kv_layout != layout)
+    return set_error(XPU_ERR_INVALID,
+                     "the KV cache holds this sequence in the other mode's layout (reference mode is "
+                     "position-major, graph and eager modes chunk-major): after switching between them, "
+                     "decode from position 0");
+  return XPU_OK;
+}
+
+}  // namespace
+
 extern "C" int xpu_qwen3_decode(xpu_qwen3 *eng, uint32_t token, uint32_t position, uint32_t *next) {
   if (!eng || !next) return set_error(XPU_ERR_INVALID, "null argument");
   if (token >= eng->c.vocab) return set_error(XPU_ERR_INVALID, "input token ID is outside the vocabulary");
   if (position >= eng->max_seq) return set_error(XPU_ERR_INVALID, "position exceeds --max-seq-len");
   int rc;
+  if ((rc = claim_kv_layout(*eng, position))) return rc;
   uint32_t result = 0;
   if (eng->mode == XPU_QWEN3_REFERENCE) {
     if ((rc = reference_step(*eng, token, position, &result))) return rc;
@@ -985,6 +1066,7 @@ extern "C" int xpu_qwen3_generate(xpu_qwen3 *eng, const uint32_t *prompt, uint32
     if (prompt[i] >= eng->c.vocab) return set_error(XPU_ERR_INVALID, "input token ID is outside the vocabulary");
   const uint32_t steps = n_prompt + std::max(max_new, 1u) - 1;
   int rc;
+  if ((rc = claim_kv_layout(*eng, 0))) return rc;
   double p_ms = 0, d_ms = 0;
   std::vector<uint32_t> gen(std::max(max_new, 1u));
   if (eng->mode == XPU_QWEN3_REFERENCE) {

@@ -42,6 +42,13 @@ def read_config(model_dir: str) -> Qwen3Config:
     return cfg
 
 
+def validate_checkpoint(model_dir: str) -> Qwen3Config:
+    """Host-only validation of a checkpoint directory (no GPU needed)."""
+    cfg = Qwen3Config()
+    check(library().xpu_qwen3_validate_checkpoint(model_dir.encode(), ctypes.byref(cfg)))
+    return cfg
+
+
 def prompt_tokens(n: int, seed: int, vocab: int) -> np.ndarray:
     out = np.empty(n, np.uint32)
     check(library().xpu_synth_tokens(out.ctypes.data_as(c_void_p), n, seed, vocab))
