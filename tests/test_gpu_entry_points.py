@@ -86,7 +86,8 @@ def test_run_gemm(args, type_, shape):
     out = run("gemm", args + ["--iterations", "3", "--warmups", "1"])
     dev, shp, median, best, _ = check_output(out, GEMM_LINES)
     assert shp.groups() == (type_,) + tuple(map(str, shape))
-    assert float(median.group(1)) > 0 and float(best.group(1)) >= float(median.group(1))
+    # two decimals of TFLOP/s: a tiny product prints 0.00
+    assert float(best.group(1)) >= float(median.group(1)) >= 0
     if shape == (4096, 4096, 4096):
         assert float(median.group(1)) > 200.0
 
