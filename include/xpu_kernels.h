@@ -39,6 +39,24 @@ int xpu_gemv(xpu_runtime *rt, int dtype, const void *A, const void *x, void *y,
 int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
              uint32_t M, uint32_t N, uint32_t K);
 
+/* Size of the scratch array behind xpu_gemm_noalloc: 32 MiB per GPU. */
+#define XPU_GEMM_NOALLOC_SCRATCH_BYTES (32ull << 20)
+
+/* xpu_gemm without allocation. No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same kernels and results
+ * as xpu_gemm, bit for bit; the zero-padded copies of operands whose rows are
+ * not 16-byte aligned (K or N not a multiple of 8, or a misaligned pointer)
+ * go into a fixed device array of XPU_GEMM_NOALLOC_SCRATCH_BYTES per GPU,
+ * set up when the first runtime on that GPU is created and held until the
+ * process ends, instead of the runtime's workspace. Needs of more than that
+ * (rows x padded columns x 2 bytes, A and B together) fail with
+ * XPU_ERR_INVALID before any launch; aligned operands need none. Calls no
+ * hipMalloc/hipFree. All calls on one GPU share the array: calls that
+ * overlap on one GPU (other streams or runtimes) race. */
+int xpu_gemm_noalloc(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
+                     uint32_t M, uint32_t N, uint32_t K);
+
 /* Seeded U[-1,1) synthetic data written on the device: element i is
  * encode(dtype, (2u - 2^24) / 2^24) with u the top 24 bits of
  * splitmix64(splitmix64(seed) + (i + 1) * 0x9e3779b97f4a7c15). The same

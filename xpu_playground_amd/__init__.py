@@ -98,6 +98,7 @@ def _declare(lib):
     }
     optional = {
         "xpu_gemm": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]),
+        "xpu_gemm_noalloc": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]),
         "xpu_qwen3_preset": (c_int, [c_char_p, POINTER(Qwen3Config)]),
         "xpu_qwen3_fill_tensor": (
             c_int,

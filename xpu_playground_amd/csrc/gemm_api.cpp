@@ -47,8 +47,10 @@ int pad_rows2(xpu_runtime *rt, const void *src_a, uint64_t ld_a, uint32_t rows_a
 
 }  // namespace
 
-extern "C" int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
-                        uint32_t M, uint32_t N, uint32_t K) {
+namespace xpu {
+
+int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, uint32_t M, uint32_t N, uint32_t K,
+             void *fixed_workspace, uint64_t fixed_capacity) {
   if (!rt || !A || !B || !C) return set_error(XPU_ERR_INVALID, "xpu_gemm: null argument");
   if (dtype != XPU_DTYPE_BF16 && dtype != XPU_DTYPE_FP16)
     return set_error(XPU_ERR_INVALID, "xpu_gemm: dtype must be bf16 (0) or fp16 (1)");
@@ -65,8 +67,14 @@ extern "C" int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B
   const uint64_t b_bytes = b_direct ? 0 : static_cast<uint64_t>(K) * np * 2;
   const void *a_use = A, *b_use = B;
   if (a_bytes + b_bytes) {
-    void *ws = nullptr;
-    int rc = rt->scratch(a_bytes + b_bytes, &ws);
+    void *ws = fixed_workspace;
+    int rc = XPU_OK;
+    if (!ws) rc = rt->scratch(a_bytes + b_bytes, &ws);
+    else if (a_bytes + b_bytes > fixed_capacity)
+      rc = set_error(XPU_ERR_INVALID, "xpu_gemm_noalloc: the operands need " + std::to_string(a_bytes + b_bytes) +
+                                          " bytes of padded copies, above the " + std::to_string(fixed_capacity) +
+                                          "-byte scratch array (A rows need K % 8 == 0 and 16-byte alignment, B "
+                                          "rows N % 8 == 0, to be read in place)");
     if (rc) return rc;
     void *bp = static_cast<char *>(ws) + a_bytes;
     if (!a_direct && !b_direct) {
@@ -92,6 +100,13 @@ extern "C" int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B
   const xpu_kernel_arg args[] = {{8, &a_use}, {8, &b_use}, {8, &C},   {4, &M},     {4, &n_run},
                                  {4, &k_run}, {4, &kb},    {4, &ldc}, {4, &n_out}};
   return rt->launch(*k, static_cast<uint32_t>(tiles), 1, 256, 0, args, 9);
+}
+
+}  // namespace xpu
+
+extern "C" int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
+                        uint32_t M, uint32_t N, uint32_t K) {
+  return xpu::gemm_run(rt, dtype, A, B, C, M, N, K, nullptr, 0);
 }
 
 namespace {

@@ -187,6 +187,7 @@ int xpu_rt_create(const char *module_path, int device, xpu_runtime **out) {
     return set_error(XPU_ERR_DEVICE, "unsupported GPU '" + rt->name + "' (" + rt->arch +
                                          "): kernels are built for gfx950 (MI355X)");
   XPU_HIP_RETURN(hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking));
+  if (int rc = xpu::noalloc_scratch_setup(device)) return rc;
 
   std::string path;
   if (module_path && *module_path) path = module_path;

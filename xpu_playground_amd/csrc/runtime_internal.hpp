@@ -44,6 +44,18 @@ template <typename T> T arg_value(const xpu_kernel_arg *args, uint32_t index) {
   return *static_cast<const T *>(args[index].value);
 }
 
+// The GEMM launch behind xpu_gemm and xpu_gemm_noalloc: operands whose rows
+// are not 16-byte aligned are first copied, zero-padded to a multiple of 8
+// columns, into a workspace: the runtime's grow-only one when
+// fixed_workspace is null, else fixed_workspace (fixed_capacity bytes; a
+// larger need fails with XPU_ERR_INVALID before any launch).
+int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, uint32_t M, uint32_t N, uint32_t K,
+             void *fixed_workspace, uint64_t fixed_capacity);
+
+// Device address of the no-allocation scratch array on `device` (the
+// current device), looked up once per device; called by xpu_rt_create.
+int noalloc_scratch_setup(int device);
+
 }  // namespace xpu
 
 struct xpu_runtime {
