@@ -14,7 +14,10 @@ same decode after a 2048-id prompt (the attention split over compute units).
 
 cpu_baseline: the CPU oracle's reference-order GEMV (gemv.cpp:126-134,
 sequential FP32 sum per row) over the same 16384 x 16384 fp16 matrix on all
-host threads, repeated for about 10 s.
+host threads (plus one thread, and the reference's 64-row check size); each
+secondary line carries its own: the oracle's blocked FP32 GEMM, and its
+Qwen3 decode over a bounded number of steps. All CPU work runs after the
+GPU measurements.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--no-secondary]
 """
@@ -174,29 +177,119 @@ def qwen3_decode(xpu, n_prompt=128, max_seq=256):
         rt.close()
 
 
-def cpu_baseline(m, k, dtype):
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def oracle():
     sys.path.insert(0, os.path.join(REPO, "tests"))
-    import numpy as np
     import oracle_lib as orc
 
-    threads = len(os.sched_getaffinity(0))
+    return orc
+
+
+def host_threads() -> int:
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(m, k, dtype):
+    """The headline's CPU baseline: the oracle's reference-order GEMV
+    (gemv.cpp:126-134, sequential FP32 sum per row) on all host threads over
+    the full matrix (repeated for about 5 s), one full pass on one thread,
+    and the reference's own check size (its first 64 rows, one thread)."""
+    import numpy as np
+
+    orc = oracle()
+    threads = host_threads()
     a = orc.uniform(m * k, 3, dtype)
     x = orc.uniform(k, 4, dtype)
     y = np.empty(m, np.float32)
     times = []
-    t_end = time.perf_counter() + 10.0
-    while time.perf_counter() < t_end and len(times) < 50:
+    t_end = time.perf_counter() + 5.0
+    while time.perf_counter() < t_end and len(times) < 30:
         times.append(orc.lib().orc_time_gemv_seq(orc.ptr(a), orc.ptr(x), orc.ptr(y), m, k, dtype, threads))
     times.sort()
     med = times[len(times) // 2]
+    one = orc.lib().orc_time_gemv_seq(orc.ptr(a), orc.ptr(x), orc.ptr(y), m, k, dtype, 1)
+    rows64 = sorted(orc.lib().orc_time_gemv_seq(orc.ptr(a), orc.ptr(x), orc.ptr(y), 64, k, dtype, 1)
+                    for _ in range(9))[4]
+    alg = 2.0 * m * k + 2.0 * k + 2.0 * m
     return {
-        "value": round((2.0 * m * k + 2.0 * k + 2.0 * m) / med / 1e9, 2),
+        "value": round(alg / med / 1e9, 2),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
+        "cpu_model": cpu_model(),
+        "one_thread_value": round(alg / one / 1e9, 2),
+        "reference_64_row_check_ms": round(rows64 * 1e3, 3),
         "sample": f"{len(times)} full passes of the {m}x{k} fp16 GEMV, reference order "
-        f"(gemv.cpp:126-134, sequential FP32 per row), rows split over {threads} threads; median pass "
-        f"{med * 1e3:.1f} ms",
+        f"(gemv.cpp:126-134, sequential FP32 per row), rows split over {threads} threads, median pass "
+        f"{med * 1e3:.1f} ms; one_thread_value: one full pass on 1 thread ({one:.2f} s); "
+        f"reference_64_row_check_ms: the reference's own host check size, rows 0-63 on 1 thread",
+    }
+
+
+def cpu_gemm_baseline(m, n, k, dtype, one_thread_rows):
+    """FP32 blocked GEMM of the oracle (each element's K products summed in
+    ascending k, the order of gemm.cpp's FP32 check) on all host threads over
+    the full product, once; plus one_thread_rows rows of it on one thread."""
+    import numpy as np
+
+    orc = oracle()
+    threads = host_threads()
+    a = orc.uniform(m * k, 5, dtype)
+    b = orc.uniform(k * n, 6, dtype)
+    c = np.empty((m, n), np.float32)
+    t = orc.lib().orc_time_gemm_blocked(orc.ptr(a), orc.ptr(b), orc.ptr(c), m, n, k, dtype, threads)
+    t1 = orc.lib().orc_time_gemm_blocked(orc.ptr(a), orc.ptr(b), orc.ptr(c), one_thread_rows, n, k, dtype, 1)
+    return {
+        "value": round(2.0 * m * n * k / t / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "cpu_model": cpu_model(),
+        "one_thread_value": round(2.0 * one_thread_rows * n * k / t1 / 1e12, 4),
+        "sample": f"one full {m}x{n}x{k} product ({t:.2f} s) in FP32, 64x512x256 cache blocks over "
+        f"{threads} threads; one_thread_value: the first {one_thread_rows} rows on 1 thread ({t1:.2f} s)",
+    }
+
+
+def cpu_decode_baseline(position, steps=4):
+    """The oracle's Qwen3-0.6B-shape decode (the BASELINE weights: seed 0,
+    unit gains) on all host threads: `steps` greedy decode steps timed at
+    positions position .. position + steps - 1. The cache below `position`
+    is left zero instead of being filled by a prompt: a step's arithmetic
+    (its attention reads every position) is that of a real history of the
+    same length, and the oracle's 128 prompt steps would take minutes."""
+    orc = oracle()
+    threads = host_threads()
+    orc.set_threads(threads)
+    cfg = orc.config("qwen3-0.6b")
+    m = orc.Model(cfg, seed=0, gain_std=0.0, max_seq=position + steps + 1)
+    try:
+        tok = int(orc.tokens(1, 1, cfg.vocab)[0])
+        t0 = time.perf_counter()
+        for s in range(steps):
+            tok = m.decode(tok if tok < cfg.vocab else 0, position + s)
+        dt = time.perf_counter() - t0
+    finally:
+        m.close()
+    return {
+        "value": round(steps / dt, 3),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "cpu_model": cpu_model(),
+        "sample": f"{steps} greedy decode steps of the CPU oracle at positions {position}-{position + steps - 1} "
+        f"(the cache of the positions below zero-filled), {threads} threads, {dt:.2f} s",
     }
 
 
@@ -308,11 +401,24 @@ def main() -> int:
                 "attention": "split over compute units from 257 positions"}
             log(f"Qwen3 decode after 2048 prompt ids {q['decode_tok_s']:.1f} tok/s")
 
+    # CPU baselines, after every GPU measurement (none overlaps a timed GPU region)
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (oracle GEMV, reference order)")
         cpu = cpu_baseline(m, k, dtype)
-        log(f"CPU {cpu['value']} GB/s on {cpu['cores']} threads")
+        log(f"CPU {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['one_thread_value']} on 1)")
+        if "gemm_bf16_4096" in secondary:
+            log("CPU baseline GEMM bf16 4096^3 (oracle, blocked FP32)")
+            secondary["gemm_bf16_4096"]["cpu_baseline"] = cpu_gemm_baseline(4096, 4096, 4096, xpu.BF16, 128)
+        if "gemm_fp16_3000x4097x2050" in secondary:
+            log("CPU baseline GEMM fp16 3000x4097x2050")
+            secondary["gemm_fp16_3000x4097x2050"]["cpu_baseline"] = cpu_gemm_baseline(3000, 4097, 2050, xpu.FP16, 128)
+        if "qwen3_0.6b_decode" in secondary:
+            log("CPU baseline Qwen3-0.6B decode (oracle)")
+            secondary["qwen3_0.6b_decode"]["cpu_baseline"] = cpu_decode_baseline(128)
+        if "qwen3_0.6b_decode_after_2048_prompt" in secondary:
+            log("CPU baseline Qwen3-0.6B decode at positions 2048+ (oracle)")
+            secondary["qwen3_0.6b_decode_after_2048_prompt"]["cpu_baseline"] = cpu_decode_baseline(2048)
 
     line = {
         "metric": "GEMV HBM GB/s (% of 8 TB/s); GEMM TFLOP/s; Qwen3-0.6B decode tok/s",

@@ -357,6 +357,51 @@ void orc_gemm_f32_rows(const uint16_t *a, const uint16_t *b, float *c, uint32_t 
   free(bf);
 }
 
+/* The same sums (each C element accumulates its K products in ascending k,
+ * FP32, no contraction) with the loops blocked for the host caches: a
+ * 64-row x 512-column C tile stays in L2 while 256-deep panels of A and B
+ * stream through it. Bitwise equal to orc_gemm_f32_rows; the CPU baseline of
+ * the GEMM lines (BASELINE plan: blocked FP32, all host threads). */
+void orc_gemm_f32_blocked(const uint16_t *a, const uint16_t *b, float *c, uint32_t m,
+                          uint32_t n, uint32_t k, int dtype) {
+  enum { RB = 64, CB = 512, KB = 256 };
+  float *bf = (float *)malloc(sizeof(float) * (uint64_t)k * n + 4);
+  orc_decode_n(b, bf, (uint64_t)k * n, dtype);
+  const int64_t row_blocks = ((int64_t)m + RB - 1) / RB, col_blocks = ((int64_t)n + CB - 1) / CB;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(orc_get_threads())
+  for (int64_t t = 0; t < row_blocks * col_blocks; ++t) {
+    const uint32_t r0 = (uint32_t)(t / col_blocks) * RB, c0 = (uint32_t)(t % col_blocks) * CB;
+    const uint32_t r1 = r0 + RB < m ? r0 + RB : m, c1 = c0 + CB < n ? c0 + CB : n;
+    float arow[KB];
+    for (uint32_t r = r0; r < r1; ++r)
+      for (uint32_t j = c0; j < c1; ++j) c[(uint64_t)r * n + j] = 0.0f;
+    for (uint32_t k0 = 0; k0 < k; k0 += KB) {
+      const uint32_t k1 = k0 + KB < k ? k0 + KB : k;
+      for (uint32_t r = r0; r < r1; ++r) {
+        for (uint32_t kk = k0; kk < k1; ++kk) arow[kk - k0] = orc_decode(a[(uint64_t)r * k + kk], dtype);
+        float *crow = c + (uint64_t)r * n;
+        for (uint32_t kk = k0; kk < k1; ++kk) {
+          const float av = arow[kk - k0];
+          const float *brow = bf + (uint64_t)kk * n;
+          for (uint32_t j = c0; j < c1; ++j) crow[j] = crow[j] + av * brow[j];
+        }
+      }
+    }
+  }
+  free(bf);
+}
+
+double orc_time_gemm_blocked(const uint16_t *a, const uint16_t *b, float *c, uint32_t m,
+                             uint32_t n, uint32_t k, int dtype, int threads) {
+  const int saved = g_threads;
+  g_threads = threads;
+  const double t0 = now_seconds();
+  orc_gemm_f32_blocked(a, b, c, m, n, k, dtype);
+  const double t1 = now_seconds();
+  g_threads = saved;
+  return t1 - t0;
+}
+
 double orc_time_gemm_f32(const uint16_t *a, const uint16_t *b, float *c,
                          uint32_t m, uint32_t n, uint32_t k, int dtype,
                          uint32_t row_limit, int threads) {

@@ -93,6 +93,12 @@ void orc_gemm_f64(const uint16_t *a, const uint16_t *b, double *c, uint32_t m,
 void orc_gemm_f32_rows(const uint16_t *a, const uint16_t *b, float *c, uint32_t m,
                        uint32_t n, uint32_t k, int dtype, const uint32_t *rows,
                        uint32_t nrows);
+/* same sums as orc_gemm_f32_rows (all m rows), cache-blocked; bitwise equal */
+void orc_gemm_f32_blocked(const uint16_t *a, const uint16_t *b, float *c, uint32_t m,
+                          uint32_t n, uint32_t k, int dtype);
+/* wall seconds of orc_gemm_f32_blocked on `threads` threads */
+double orc_time_gemm_blocked(const uint16_t *a, const uint16_t *b, float *c, uint32_t m,
+                             uint32_t n, uint32_t k, int dtype, int threads);
 double orc_time_gemm_f32(const uint16_t *a, const uint16_t *b, float *c,
                          uint32_t m, uint32_t n, uint32_t k, int dtype,
                          uint32_t row_limit, int threads);

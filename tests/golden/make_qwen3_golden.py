@@ -11,16 +11,25 @@ same in both versions) for a shape of the Qwen3 family, loads the synthetic
 weights of the CPU oracle's generator (N(0, 0.02^2) matrices, norm gains
 1 + N(0, gain_std^2)), and records:
   * hf_generate: model.generate(prompt, greedy, no EOS stop) - the batched
-    prompt path reference.py takes;
+    prompt path reference.py takes - with its raw logits per step
+    (output_logits=True);
   * hf_steps: the same prompt fed one position at a time with the KV cache
     (the engine's order, qwen3/main.cpp:343-352), its greedy tokens and, per
     step, the top-16 logits (index, value);
-  * oracle: the CPU oracle's tokens and top-16 logits for the same steps.
+  * oracle: the CPU oracle's tokens and top-16 logits for the same steps;
+  * logit_stats, for each of the first logit steps, over the full
+    vocabulary: max |oracle - generate|, max |oracle - steps|,
+    transformers' own max |generate - steps|, the number of entries where
+    the oracle differs from each, and the top-1 / top-2 margins;
+  * oracle_logits_sha256: the SHA-256 of each oracle logits row (bf16
+    codes, little endian), so a test that reproduces the rows bit for bit
+    (the GPU engine, the oracle) is known to have the statistics above.
 
-Usage: python tests/golden/make_qwen3_golden.py [tiny|qwen3-0.6b ...]
+Usage: python tests/golden/make_qwen3_golden.py [tiny|qwen3-0.6b|... ]
 """
 from __future__ import annotations
 
+import hashlib
 import json
 import os
 import sys
@@ -35,7 +44,19 @@ import oracle_lib as orc  # noqa: E402
 CASES = {
     # name: (preset, weight seed, gain_std, prompt seed, prompt length, new tokens, logit steps)
     "tiny": ("tiny", 5, 0.1, 1, 16, 32, 32),
+    # the BASELINE workload: unit norm gains; its greedy stream
+    # is almost one repeated token
     "qwen3-0.6b": ("qwen3-0.6b", 0, 0.0, 1, 128, 128, 32),
+    # greedy streams that change at almost every step, so token identity
+    # with transformers discriminates (picked by scanning seeds and gain
+    # spreads with the oracle). At the 0.6B vocabulary of 151936 ids the
+    # top two logits tie exactly in bf16 in 1-9 of the first 32 steps for
+    # every seed and gain spread tried, and varied streams part from
+    # transformers within 32 steps (transformers' own generate and step
+    # paths included); the 4096-id vocabulary of the small shape does not
+    "small-varied": ("small", 2, 1.0, 3, 16, 32, 32),
+    "small-varied-b": ("small", 3, 0.5, 4, 16, 32, 32),
+    "tiny-varied": ("tiny", 1, 1.0, 2, 16, 32, 32),
 }
 
 
@@ -88,6 +109,10 @@ def topk(values: np.ndarray, k: int = 16):
     return [[int(i), float(values[i])] for i in idx]
 
 
+def row_hash(codes: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(codes, dtype="<u2").tobytes()).hexdigest()
+
+
 def make(name: str) -> dict:
     import torch
     import transformers
@@ -99,21 +124,24 @@ def make(name: str) -> dict:
     prompt = orc.tokens(n_prompt, pseed, vocab)
     with torch.no_grad():
         gen = model.generate(torch.from_numpy(prompt.astype(np.int64))[None], max_new_tokens=n_new,
-                             do_sample=False, use_cache=True, eos_token_id=None, pad_token_id=0)
-        hf_generate = gen[0, n_prompt:].tolist()
+                             do_sample=False, use_cache=True, eos_token_id=None, pad_token_id=0,
+                             output_logits=True, return_dict_in_generate=True)
+        hf_generate = gen.sequences[0, n_prompt:].tolist()
+        gen_rows = [gen.logits[i][0].float().numpy() for i in range(n_logits)]
+        del gen
         print(f"[{name}] generate done {time.time() - t0:.1f}s", flush=True)
         out = None
         past = None
         for p in range(n_prompt):
             out = model(input_ids=torch.tensor([[int(prompt[p])]]), past_key_values=past, use_cache=True)
             past = out.past_key_values
-        steps, logits = [], []
+        steps, step_rows = [], []
         for i in range(n_new):
             row = out.logits[0, -1].float().numpy()
             nxt = int(np.argmax(row))
             steps.append(nxt)
             if i < n_logits:
-                logits.append(topk(row))
+                step_rows.append(row.copy())
             if i + 1 == n_new:
                 break
             out = model(input_ids=torch.tensor([[nxt]]), past_key_values=past, use_cache=True)
@@ -122,8 +150,32 @@ def make(name: str) -> dict:
     m = orc.Model(orc.config(preset), seed=seed, gain_std=gain_std, max_seq=n_prompt + n_new)
     o_tokens, o_logits = m.generate(prompt, n_new, logit_steps=n_logits)
     m.close()
-    o_top = [topk(orc.decode(o_logits[i], 0)) for i in range(n_logits)]
     print(f"[{name}] oracle done {time.time() - t0:.1f}s", flush=True)
+    def ulps(x, y):
+        # max |x - y| in bf16 ulps of the row's largest magnitude (the
+        # spacing of the logits that decide the argmax)
+        mag = max(float(np.max(np.abs(x))), float(np.max(np.abs(y))))
+        return float(np.max(np.abs(x - y)) / 2.0 ** (np.floor(np.log2(mag)) - 7))
+
+    stats = []
+    for i in range(n_logits):
+        o = orc.decode(o_logits[i], 0).astype(np.float64)
+        g, st = gen_rows[i].astype(np.float64), step_rows[i].astype(np.float64)
+        top2 = np.sort(o)[-2:]
+        top2s = np.sort(st)[-2:]
+        stats.append({
+            "oracle_vs_generate": float(np.max(np.abs(o - g))),
+            "oracle_vs_steps": float(np.max(np.abs(o - st))),
+            "generate_vs_steps": float(np.max(np.abs(g - st))),
+            "oracle_vs_generate_ulps": ulps(o, g),
+            "oracle_vs_steps_ulps": ulps(o, st),
+            "generate_vs_steps_ulps": ulps(g, st),
+            "oracle_differs_generate": int(np.count_nonzero(o != g)),
+            "oracle_differs_steps": int(np.count_nonzero(o != st)),
+            "oracle_margin": float(top2[1] - top2[0]),
+            "steps_margin": float(top2s[1] - top2s[0]),
+            "argmax": [int(np.argmax(o)), int(np.argmax(g)), int(np.argmax(st))],
+        })
     return {
         "case": name,
         "preset": preset,
@@ -132,13 +184,17 @@ def make(name: str) -> dict:
         "prompt_seed": pseed,
         "prompt": prompt.tolist(),
         "new_tokens": n_new,
+        "logit_steps": n_logits,
         "transformers_version": transformers.__version__,
         "torch_version": torch.__version__,
         "hf_generate": hf_generate,
         "hf_steps": steps,
-        "hf_steps_top16": logits,
+        "hf_steps_top16": [topk(r) for r in step_rows],
+        "hf_generate_top16": [topk(r) for r in gen_rows],
         "oracle_tokens": o_tokens.tolist(),
-        "oracle_top16": o_top,
+        "oracle_top16": [topk(orc.decode(o_logits[i], 0)) for i in range(n_logits)],
+        "oracle_logits_sha256": [row_hash(o_logits[i]) for i in range(n_logits)],
+        "logit_stats": stats,
     }
 
 
@@ -150,6 +206,10 @@ def main() -> None:
         with open(path, "w") as f:
             json.dump(fixture, f, separators=(",", ":"))
         same = sum(a == b for a, b in zip(fixture["hf_steps"], fixture["oracle_tokens"]))
+        worst = max(max(st["oracle_vs_generate"], st["oracle_vs_steps"]) for st in fixture["logit_stats"])
+        print(f"  {len(set(fixture['oracle_tokens'][:32]))} distinct tokens in 32 steps; max |logit diff| over "
+              f"{fixture['logit_steps']} steps {worst}; transformers self-difference "
+              f"{max(st['generate_vs_steps'] for st in fixture['logit_stats'])}", flush=True)
         print(f"wrote {path}: oracle == hf_steps for {same}/{len(fixture['hf_steps'])} tokens; "
               f"hf_generate == hf_steps for "
               f"{sum(a == b for a, b in zip(fixture['hf_generate'], fixture['hf_steps']))}", flush=True)

@@ -92,6 +92,8 @@ def lib():
             "orc_gemm_f64": (None, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_int, c_void_p, c_uint32]),
             "orc_gemm_f32_rows": (None, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_int, c_void_p, c_uint32]),
             "orc_time_gemm_f32": (c_double, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_int, c_uint32, c_int]),
+            "orc_gemm_f32_blocked": (None, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_int]),
+            "orc_time_gemm_blocked": (c_double, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_int, c_int]),
             "orc_exp": (c_float, [c_float]),
             "orc_rmsnorm": (None, [c_void_p, c_void_p, c_void_p, c_uint32, c_float]),
             "orc_rope_tables": (None, [c_void_p, c_void_p, c_uint32, c_uint32, c_double]),

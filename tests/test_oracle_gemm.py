@@ -48,3 +48,15 @@ def test_f32_rows_sequential_order():
     for i in range(m):
         for j in range(n):
             assert got[i, j] == np.cumsum((fa[i] * fb[:, j]).astype(np.float32), dtype=np.float32)[-1]
+
+
+def test_blocked_f32_equals_the_row_order_bitwise():
+    # the GEMM CPU baseline (orc_gemm_f32_blocked) performs the row version's
+    # sums: ascending k per element, FP32, across the 64 x 512 x 256 blocks
+    for dtype, (m, n, k) in [(0, (70, 600, 300)), (1, (65, 513, 257)), (0, (1, 3, 1))]:
+        a = orc.uniform(m * k, 7, dtype)
+        b = orc.uniform(k * n, 8, dtype)
+        rows = orc.gemm_f32_rows(a, b, m, n, k, dtype, np.arange(m))
+        blocked = np.empty((m, n), np.float32)
+        orc.lib().orc_gemm_f32_blocked(orc.ptr(a), orc.ptr(b), orc.ptr(blocked), m, n, k, dtype)
+        assert np.array_equal(rows, blocked)

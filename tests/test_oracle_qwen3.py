@@ -12,8 +12,8 @@ import numpy as np
 import pytest
 
 import oracle_lib as orc
+import qwen3_fixtures as qf
 
-GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
 def b(v):
@@ -177,39 +177,44 @@ def test_engine_step_by_step_equals_generate():
     assert np.all(np.isfinite(f(m2.hidden())))
 
 
-def load_fixture(name):
-    path = os.path.join(GOLDEN, f"qwen3_{name}.json")
-    if not os.path.exists(path):
-        pytest.skip(f"{path} not generated")
-    return json.load(open(path))
+@pytest.mark.parametrize("name", qf.NAMES)
+def test_oracle_meets_the_decode_bar_against_transformers(name):
+    # tokens: the oracle's greedy stream equals transformers' generate (the
+    # reference.py path) and step-by-step streams for the first 32 steps
+    # (the 0.6B fixture: all 128 equal the step path; transformers' own two
+    # paths part at step 102 there)
+    fx = qf.load(name)
+    n = min(32, fx["new_tokens"])
+    assert fx["oracle_tokens"][:n] == fx["hf_generate"][:n] == fx["hf_steps"][:n]
+    if name == "qwen3-0.6b":
+        assert fx["oracle_tokens"] == fx["hf_steps"]
+    if name in qf.VARIED:
+        assert len(set(fx["oracle_tokens"][:n])) >= 16  # a stream that changes
+    # logits over the full vocabulary, per step (qwen3_fixtures.py states the bar)
+    assert len(fx["logit_stats"]) == fx["logit_steps"] == 32
+    for step, st in enumerate(fx["logit_stats"]):
+        assert qf.step_within_bar(st), (name, step, st)
+        assert st["argmax"] == [fx["oracle_tokens"][step], fx["hf_generate"][step], fx["hf_steps"][step]]
+        # the recorded maxima bound the recorded top-16 entries
+        for top, key in (("hf_steps_top16", "oracle_vs_steps"), ("hf_generate_top16", "oracle_vs_generate")):
+            ovals = dict(map(tuple, fx["oracle_top16"][step]))
+            for i, v in fx[top][step]:
+                if i in ovals:
+                    assert abs(ovals[i] - v) <= st[key] + 1e-9
 
 
-@pytest.mark.parametrize("name", ["tiny", "qwen3-0.6b"])
-def test_oracle_matches_transformers_fixture(name):
-    # the decode bar: identical greedy tokens for the first 32 steps (here:
-    # every recorded step); logits within 2e-2 or 2 bf16 ulps of
-    # transformers' value, whichever is larger, on its top-16 entries of the
-    # first 32 steps (transformers' own batched-prompt and step paths differ
-    # by 2 ulps at |logit| in [2, 4) on the 0.6B weights)
-    fx = load_fixture(name)
-    assert fx["oracle_tokens"] == fx["hf_steps"]
-    assert fx["hf_generate"][:32] == fx["hf_steps"][:32]
-    for hf_row, or_row in zip(fx["hf_steps_top16"], fx["oracle_top16"]):
-        ovals = dict((i, v) for i, v in or_row)
-        for i, v in hf_row:
-            if i in ovals:
-                assert abs(ovals[i] - v) <= max(2e-2, 2.0 * orc.bf16_ulp(v))
-        # the top entry is the same token
-        assert hf_row[0][0] == or_row[0][0]
-
-
-def test_oracle_reproduces_tiny_fixture_live():
-    fx = load_fixture("tiny")
+@pytest.mark.parametrize("name", ["tiny", "tiny-varied", "small-varied", "small-varied-b"])
+def test_oracle_reproduces_the_measured_logit_rows(name):
+    # the live oracle computes the rows whose statistics the fixture holds,
+    # bit for bit (SHA-256 of each bf16 row)
+    fx = qf.load(name)
     cfg = orc.config(fx["preset"])
     m = orc.Model(cfg, seed=fx["weight_seed"], gain_std=fx["gain_std"], max_seq=len(fx["prompt"]) + fx["new_tokens"])
-    tokens, logits = m.generate(np.array(fx["prompt"], np.uint32), fx["new_tokens"], logit_steps=4)
+    tokens, logits = m.generate(np.array(fx["prompt"], np.uint32), fx["new_tokens"], logit_steps=fx["logit_steps"])
+    m.close()
     assert tokens.tolist() == fx["oracle_tokens"]
-    for step in range(4):
+    assert [qf.row_hash(r) for r in logits] == fx["oracle_logits_sha256"]
+    for step in range(fx["logit_steps"]):
         row = f(logits[step])
         for i, v in fx["oracle_top16"][step]:
             assert row[i] == np.float32(v)
