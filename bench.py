@@ -63,11 +63,12 @@ def timed_gemv(rt, xpu, dtype, m, k, steps, warmup):
 
 def timed_gemm(rt, dtype, m, n, k, steps, warmup, settle_ms=40.0):
     """Average ms per GEMM over `steps` back-to-back launches after `warmup`
-    launches, twice: first straight after the allocation (`cold`), then
-    after `settle_ms` of back-to-back launches. MI355X raises its shader
-    clock over the first tens of milliseconds of sustained MFMA load (about
-    1.6 -> 1.9 GHz on this kernel), so the settled figure is the steady
-    state a sequence of GEMMs runs at. Returns (settled_ms, cold_ms)."""
+    launches (the configs' "5 warmups and 20 timed", reported), then again
+    after `settle_ms` more of back-to-back launches (reported beside it).
+    MI355X power-manages the shader clock under sustained MFMA load: the
+    kernel's cycle count is fixed (~162.6K per wave at 4096^3) while the
+    clock of each XCD moves between ~1.2 and ~1.75 GHz over milliseconds
+    (profiles/gemm_bf16_4096_counters.md). Returns (settled_ms, cold_ms)."""
     a, b, c = rt.alloc(m * k * 2), rt.alloc(k * n * 2), rt.alloc(m * n * 2)
     rt.fill_uniform(dtype, a, m * k, 5)
     rt.fill_uniform(dtype, b, k * n, 6)
@@ -363,23 +364,28 @@ def main() -> int:
     secondary = {}
     if not args.no_secondary:
         if hasattr(xpu.library(), "xpu_gemm"):
-            log("GEMM bf16 4096^3: 5 warmups, 20 timed (cold, then after 40 ms of settling)")
+            log("GEMM bf16 4096^3: 5 warmups, 20 timed (then again after 40 ms of settling)")
             gms, gcold = timed_gemm(rt, xpu.BF16, 4096, 4096, 4096, 20, 5)
             flop = 2.0 * 4096**3
             tflops = flop / (gms * 1e-3) / 1e12
+            cold_tf = flop / (gcold * 1e-3) / 1e12
             secondary["gemm_bf16_4096"] = {
-                "value": round(tflops, 1), "unit": "TFLOP/s", "ms": round(gms, 4),
-                "roofline_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-                "cold_value": round(flop / (gcold * 1e-3) / 1e12, 1), "cold_ms": round(gcold, 4)}
-            log(f"GEMM {gms * 1e3:.1f} us, {tflops:.1f} TFLOP/s (cold {gcold * 1e3:.1f} us)")
+                "value": round(cold_tf, 1), "unit": "TFLOP/s", "ms": round(gcold, 4),
+                "roofline_frac": round(cold_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                "timing": "configs[2]: 5 warmups, then the average of 20 back-to-back launches",
+                "settled_value": round(tflops, 1), "settled_ms": round(gms, 4),
+                "settled_timing": "the same 20 launches again after 40 ms of back-to-back launches"}
+            log(f"GEMM {gcold * 1e3:.1f} us, {cold_tf:.1f} TFLOP/s (after settling {gms * 1e3:.1f} us)")
             gms2, gcold2 = timed_gemm(rt, xpu.FP16, 3000, 4097, 2050, 20, 5)
             flop2 = 2.0 * 3000 * 4097 * 2050
             tf2 = flop2 / (gms2 * 1e-3) / 1e12
+            cold_tf2 = flop2 / (gcold2 * 1e-3) / 1e12
             secondary["gemm_fp16_3000x4097x2050"] = {
-                "value": round(tf2, 1), "unit": "TFLOP/s", "ms": round(gms2, 4),
-                "roofline_frac": round(tf2 / MFMA_BF16_PEAK_TFLOPS, 4),
-                "cold_value": round(flop2 / (gcold2 * 1e-3) / 1e12, 1)}
-            log(f"GEMM ragged {gms2 * 1e3:.1f} us, {tf2:.1f} TFLOP/s (cold {gcold2 * 1e3:.1f} us)")
+                "value": round(cold_tf2, 1), "unit": "TFLOP/s", "ms": round(gcold2, 4),
+                "roofline_frac": round(cold_tf2 / MFMA_BF16_PEAK_TFLOPS, 4),
+                "timing": "5 warmups, then the average of 20 back-to-back launches (padding copy included)",
+                "settled_value": round(tf2, 1), "settled_ms": round(gms2, 4)}
+            log(f"GEMM ragged {gcold2 * 1e3:.1f} us, {cold_tf2:.1f} TFLOP/s (after settling {gms2 * 1e3:.1f} us)")
         if hasattr(xpu.library(), "xpu_peak_mfma"):
             secondary["measured_peaks"] = measured_peaks(rt)
             log(f"peaks {secondary['measured_peaks']}")

@@ -98,6 +98,12 @@ int xpu_module_kernel_names(const char *path, char *buf, size_t len);
 int xpu_rt_kernel_count(const xpu_runtime *rt, uint32_t *count);
 int xpu_rt_kernel_name(const xpu_runtime *rt, uint32_t index, char *buf, size_t len);
 
+/* Device address and size of a global variable of the loaded code object
+ * (hipModuleGetGlobal), e.g. the timestamp rings of the XPU_STAMPS build;
+ * XPU_ERR_NOT_FOUND when the module has no such symbol. No reference
+ * counterpart (a profiling aid). */
+int xpu_rt_module_global(xpu_runtime *rt, const char *name, void **dptr, uint64_t *bytes);
+
 int xpu_rt_synchronize(xpu_runtime *rt);
 /* The runtime's hipStream_t, as an opaque pointer. */
 void *xpu_rt_stream(xpu_runtime *rt);

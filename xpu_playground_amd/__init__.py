@@ -78,6 +78,7 @@ def _declare(lib):
         ),
         "xpu_module_kernel_names": (c_int, [c_char_p, c_char_p, c_size_t]),
         "xpu_rt_kernel_count": (c_int, [c_void_p, POINTER(c_uint32)]),
+        "xpu_rt_module_global": (c_int, [c_void_p, c_char_p, POINTER(c_void_p), POINTER(c_uint64)]),
         "xpu_rt_kernel_name": (c_int, [c_void_p, c_uint32, c_char_p, c_size_t]),
         "xpu_rt_synchronize": (c_int, [c_void_p]),
         "xpu_rt_stream": (c_void_p, [c_void_p]),

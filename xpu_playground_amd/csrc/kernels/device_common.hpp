@@ -200,3 +200,68 @@ XPU_DEVICE uint32_t lds_addr(const void *p) {
 }
 
 }  // namespace xpu
+
+// ---- Opt-in per-wave timestamps (code object built with -DXPU_STAMPS:
+// build/xpu_kernels_stamps.hsaco). A kernel that starts with
+// XPU_STAMP(id) has lane 0 of each wave record, when the wave leaves the
+// kernel, the constant 100 MHz clock (s_memrealtime) at entry, the elapsed
+// constant-clock and shader-clock (s_memtime) ticks, the kernel id, the
+// block and the XCD. Records go to a ring per (block, wave) slot, indexed by
+// that slot's own sequence counter: only one wave occupies a slot at a time
+// (launches on a stream do not overlap), so no atomics perturb the timing.
+// xpu_playground_amd/timeline.py reads and groups them. Without XPU_STAMPS
+// the macro is empty.
+#ifdef XPU_STAMPS
+namespace xpu {
+// (block, wave) slots: up to 1024 blocks of 4 waves (the decode GEMVs' grid
+// cap); 2048 records each (a decode token launches 142 kernels)
+constexpr uint32_t kStampSlots = 4096, kStampRing = 2048;
+struct StampRecord {
+  uint32_t start_lo;     // s_memrealtime at entry, low 32 bits (100 MHz)
+  uint32_t real_ticks;   // constant-clock ticks from entry to exit
+  uint32_t clock_ticks;  // shader-clock ticks (s_memtime) from entry to exit
+  uint32_t tag;          // kernel id << 24 | XCD << 20 | wave << 16 | block
+};
+}  // namespace xpu
+extern "C" __device__ uint32_t xpu_stamp_seq[xpu::kStampSlots];
+extern "C" __device__ xpu::StampRecord xpu_stamp_ring[xpu::kStampSlots * xpu::kStampRing];
+namespace xpu {
+struct StampGuard {
+  uint64_t r0, c0;
+  uint32_t id;
+  XPU_DEVICE explicit StampGuard(uint32_t kernel_id) : id(kernel_id) {
+    r0 = __builtin_amdgcn_s_memrealtime();
+    c0 = __builtin_amdgcn_s_memtime();
+  }
+  XPU_DEVICE ~StampGuard() {
+    const uint64_t c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    if ((threadIdx.x & 63u) != 0) return;
+    const uint32_t wave = threadIdx.x >> 6, slot = blockIdx.x * (blockDim.x >> 6) + wave;
+    if (slot >= kStampSlots) return;
+    // HW_REG_XCC_ID (hwreg 20), bits [3:0]
+    const uint32_t xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u;
+    const uint32_t seq = xpu_stamp_seq[slot];
+    xpu_stamp_seq[slot] = seq + 1;
+    StampRecord rec;
+    rec.start_lo = static_cast<uint32_t>(r0);
+    rec.real_ticks = static_cast<uint32_t>(r1 - r0);
+    rec.clock_ticks = static_cast<uint32_t>(c1 - c0);
+    rec.tag = (id << 24) | (xcc << 20) | ((wave & 15u) << 16) | (blockIdx.x & 0xffffu);
+    xpu_stamp_ring[slot * kStampRing + seq % kStampRing] = rec;
+  }
+};
+}  // namespace xpu
+#define XPU_STAMP(id) const ::xpu::StampGuard xpu_stamp_guard_(id)
+#else
+#define XPU_STAMP(id) \
+  do {                \
+  } while (0)
+#endif
+
+namespace xpu {
+// kernel ids of the stamps (xpu_playground_amd/timeline.py names them)
+enum : uint32_t {
+  kStampGemv = 1, kStampGemm = 2, kStampQ3Qkv = 10, kStampQ3Attention = 11, kStampQ3Scores = 12, kStampQ3Pv = 13,
+  kStampQ3Residual = 14, kStampQ3Swiglu = 15, kStampQ3Logits = 16, kStampQ3Finish = 17
+};
+}  // namespace xpu

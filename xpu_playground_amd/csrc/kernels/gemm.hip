@@ -403,6 +403,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   extern "C" __global__ __launch_bounds__(256, MINB) void NAME(                               \
       const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C, \
       uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {         \
+    XPU_STAMP(xpu::kStampGemm);                                                                 \
     xpu::dma::body<DT, NJ, BK, S, P, D, C16>(A, B, C, M, N, K, kb, ldc, n_out);                \
   }
 

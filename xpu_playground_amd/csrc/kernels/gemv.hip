@@ -48,6 +48,7 @@ XPU_DEVICE void gemv_entry(const uint16_t *__restrict__ A, const uint16_t *__res
   extern "C" __global__ __launch_bounds__(256) void NAME(                                  \
       const uint16_t *__restrict__ A, const uint16_t *__restrict__ x,                      \
       uint16_t *__restrict__ y, uint32_t M, uint32_t K, uint64_t lda) {                    \
+    XPU_STAMP(xpu::kStampGemv);                                                            \
     xpu::gemv_entry<DT, R, U, VEC, XG>(A, x, y, M, K, lda);                                \
   }
 

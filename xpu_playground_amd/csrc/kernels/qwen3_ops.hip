@@ -306,12 +306,14 @@ XPU_DEVICE void q3_norm_gemv_logits(const uint16_t *__restrict__ E, const uint16
       const uint16_t *__restrict__ W, uint16_t *x, const uint16_t *__restrict__ norm_w,         \
       uint16_t *__restrict__ out, uint32_t M, uint32_t K, float eps,                            \
       const uint16_t *__restrict__ embed, const uint32_t *__restrict__ state, uint32_t vocab) { \
+    XPU_STAMP(xpu::kStampQ3Qkv);                                                                \
     q3_norm_gemv<R, U>(W, x, norm_w, out, M, K, eps, embed, state, vocab);                      \
   }
 #define XPU_Q3_GEMV_RESIDUAL(SUFFIX, R, U)                                                      \
   extern "C" __global__ __launch_bounds__(256) void xpu_q3_gemv_residual##SUFFIX(               \
       const uint16_t *__restrict__ W, const uint16_t *__restrict__ v, uint16_t *x, uint32_t M,  \
       uint32_t K) {                                                                             \
+    XPU_STAMP(xpu::kStampQ3Residual);                                                           \
     q3_gemv_residual<R, U>(W, v, x, M, K);                                                      \
   }
 #define XPU_Q3_SWIGLU(SUFFIX, R, U)                                                             \
@@ -319,6 +321,7 @@ XPU_DEVICE void q3_norm_gemv_logits(const uint16_t *__restrict__ E, const uint16
       const uint16_t *__restrict__ Wgu, const uint16_t *__restrict__ x,                         \
       const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ h, uint32_t I, uint32_t K,    \
       float eps) {                                                                              \
+    XPU_STAMP(xpu::kStampQ3Swiglu);                                                             \
     q3_norm_gemv_swiglu<R, U>(Wgu, x, norm_w, h, I, K, eps);                                    \
   }
 #define XPU_Q3_LOGITS(SUFFIX, R, U)                                                             \
@@ -327,6 +330,7 @@ XPU_DEVICE void q3_norm_gemv_logits(const uint16_t *__restrict__ E, const uint16
       const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ logits, uint32_t V,           \
       uint32_t K, float eps, float *__restrict__ part_val, uint32_t *__restrict__ part_idx,     \
       uint32_t *__restrict__ part_bad) {                                                        \
+    XPU_STAMP(xpu::kStampQ3Logits);                                                             \
     q3_norm_gemv_logits<R, U>(E, x, norm_w, logits, V, K, eps, part_val, part_idx, part_bad);   \
   }
 
@@ -591,21 +595,25 @@ XPU_DEVICE void q3_norm_gemv_logits_reg(const uint16_t *__restrict__ E, const ui
       const uint16_t *__restrict__ W, uint16_t *x, const uint16_t *__restrict__ norm_w,                       \
       uint16_t *__restrict__ out, uint32_t M, uint32_t K, float eps, const uint16_t *__restrict__ embed,      \
       const uint32_t *__restrict__ state, uint32_t vocab) {                                                   \
+    XPU_STAMP(xpu::kStampQ3Qkv);                                                                              \
     q3_norm_gemv_reg<2, NC>(W, x, norm_w, out, M, K, eps, embed, state, vocab);                               \
   }                                                                                                           \
   extern "C" __global__ __launch_bounds__(256) void xpu_q3_gemv_residual_r1_v##NC(                            \
       const uint16_t *__restrict__ W, const uint16_t *__restrict__ v, uint16_t *x, uint32_t M, uint32_t K) {  \
+    XPU_STAMP(xpu::kStampQ3Residual);                                                                         \
     q3_gemv_residual_reg<1, NC>(W, v, x, M, K);                                                               \
   }                                                                                                           \
   extern "C" __global__ __launch_bounds__(256) void xpu_q3_norm_gemv_swiglu_r2_v##NC(                         \
       const uint16_t *__restrict__ Wgu, const uint16_t *__restrict__ x, const uint16_t *__restrict__ norm_w,  \
       uint16_t *__restrict__ h, uint32_t I, uint32_t K, float eps) {                                          \
+    XPU_STAMP(xpu::kStampQ3Swiglu);                                                                           \
     q3_norm_gemv_swiglu_reg<2, NC>(Wgu, x, norm_w, h, I, K, eps);                                             \
   }                                                                                                           \
   extern "C" __global__ __launch_bounds__(256) void xpu_q3_norm_gemv_logits_r2_v##NC(                         \
       const uint16_t *__restrict__ E, const uint16_t *__restrict__ x, const uint16_t *__restrict__ norm_w,    \
       uint16_t *__restrict__ logits, uint32_t V, uint32_t K, float eps, float *__restrict__ part_val,         \
       uint32_t *__restrict__ part_idx, uint32_t *__restrict__ part_bad) {                                     \
+    XPU_STAMP(xpu::kStampQ3Logits);                                                                           \
     q3_norm_gemv_logits_reg<2, NC>(E, x, norm_w, logits, V, K, eps, part_val, part_idx, part_bad);            \
   }
 
@@ -644,6 +652,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
     uint16_t *__restrict__ vcache, uint16_t *__restrict__ out, const uint32_t *__restrict__ state,
     uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float eps, float scale,
     const uint16_t *__restrict__ prefetch, uint64_t prefetch_bytes, uint32_t prefetch_delay) {
+  XPU_STAMP(xpu::kStampQ3Attention);
   __shared__ float sbuf[xpu::kAttnChunk];
   __shared__ float red[4 * xpu::kHeadDim];
   __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
@@ -812,6 +821,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_scores(
     uint16_t *__restrict__ vcache, float *__restrict__ scores, float *__restrict__ maxima,
     const uint32_t *__restrict__ state, uint32_t heads, uint32_t kv_heads, uint32_t max_seq,
     uint32_t spitch, uint32_t parts, float eps, float scale) {
+  XPU_STAMP(xpu::kStampQ3Scores);
   __shared__ float red[4];
   __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
   __shared__ __align__(16) uint16_t ks[xpu::kHeadDim];
@@ -893,6 +903,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_pv(
     const float *__restrict__ scores, const float *__restrict__ maxima, const uint16_t *__restrict__ vcache,
     uint16_t *__restrict__ out, const uint32_t *__restrict__ state, uint32_t heads, uint32_t kv_heads,
     uint32_t max_seq, uint32_t spitch, uint32_t parts) {
+  XPU_STAMP(xpu::kStampQ3Pv);
   constexpr uint32_t kDims = 16, kChunk = xpu::kAttnChunk, kTile = 1024, kRows = kTile / 128, kMaxChunks = 64;
   constexpr uint32_t kPer = kChunk / 256, kBatch = 16;
   extern __shared__ __align__(16) uint8_t pv_lds[];
@@ -1040,6 +1051,7 @@ extern "C" __global__ __launch_bounds__(1024) void xpu_q3_argmax_finish(
     const uint32_t *__restrict__ prompt, uint32_t *__restrict__ gen, uint32_t gen_capacity,
     const uint16_t *__restrict__ rope_cos, const uint16_t *__restrict__ rope_sin,
     uint16_t *__restrict__ rope_row, uint32_t max_seq) {
+  XPU_STAMP(xpu::kStampQ3Finish);
   constexpr uint32_t kBlock = 1024;  // launched with 1024 threads
   __shared__ float redv[16];
   __shared__ uint32_t redi[16], redb[16];

@@ -402,6 +402,18 @@ int xpu_rt_kernel_name(const xpu_runtime *rt, uint32_t index, char *buf, size_t 
   return copy_string(rt->kernels[index].name, buf, len);
 }
 
+int xpu_rt_module_global(xpu_runtime *rt, const char *name, void **dptr, uint64_t *bytes) {
+  if (!rt || !name || !dptr || !bytes) return set_error(XPU_ERR_INVALID, "null argument");
+  XPU_HIP_RETURN(hipSetDevice(rt->device));
+  hipDeviceptr_t p = nullptr;
+  size_t n = 0;
+  if (hipModuleGetGlobal(&p, &n, rt->module, name) != hipSuccess || !p)
+    return set_error(XPU_ERR_NOT_FOUND, std::string("code object has no global ") + name);
+  *dptr = reinterpret_cast<void *>(p);
+  *bytes = n;
+  return XPU_OK;
+}
+
 int xpu_rt_synchronize(xpu_runtime *rt) {
   if (!rt) return set_error(XPU_ERR_INVALID, "null runtime");
   XPU_HIP_RETURN(hipStreamSynchronize(rt->stream));
