@@ -114,6 +114,7 @@ def _declare(lib):
         "xpu_qwen3_set_mode": (c_int, [c_void_p, c_int]),
         "xpu_qwen3_set_prefill": (c_int, [c_void_p, c_int]),
         "xpu_qwen3_set_attention_split": (c_int, [c_void_p, c_uint32]),
+        "xpu_qwen3_set_persist_wait_limit": (c_int, [c_void_p, c_uint32]),
         "xpu_qwen3_decode": (c_int, [c_void_p, c_uint32, c_uint32, POINTER(c_uint32)]),
         "xpu_qwen3_logits": (c_int, [c_void_p, c_void_p, c_uint64]),
         "xpu_qwen3_hidden": (c_int, [c_void_p, c_void_p, c_uint64]),

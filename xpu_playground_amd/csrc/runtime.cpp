@@ -128,7 +128,7 @@ int xpu_runtime::scratch(uint64_t bytes, void **out) {
 }
 
 int xpu_runtime::launch(const xpu::KernelInfo &k, uint32_t gx, uint32_t gy, uint32_t bx,
-                        uint32_t shared, const xpu_kernel_arg *args, uint32_t nargs) {
+                        uint32_t shared, const xpu_kernel_arg *args, uint32_t nargs, bool cooperative) {
   using xpu::set_error;
   if (gx == 0 || gy == 0 || bx == 0 || bx > 1024)
     return set_error(XPU_ERR_INVALID, "invalid launch geometry for " + k.name);
@@ -143,8 +143,10 @@ int xpu_runtime::launch(const xpu::KernelInfo &k, uint32_t gx, uint32_t gy, uint
       return set_error(XPU_ERR_INVALID, "null kernel argument " + std::to_string(i));
     params[i] = const_cast<void *>(args[i].value);
   }
-  XPU_HIP_RETURN(hipModuleLaunchKernel(k.function, gx, gy, 1, bx, 1, 1, shared, stream, params,
-                                       nullptr));
+  if (cooperative)
+    XPU_HIP_RETURN(hipModuleLaunchCooperativeKernel(k.function, gx, gy, 1, bx, 1, 1, shared, stream, params));
+  else
+    XPU_HIP_RETURN(hipModuleLaunchKernel(k.function, gx, gy, 1, bx, 1, 1, shared, stream, params, nullptr));
   return XPU_OK;
 }
 

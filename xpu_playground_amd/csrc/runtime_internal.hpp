@@ -76,8 +76,10 @@ struct xpu_runtime {
   xpu_runtime &operator=(const xpu_runtime &) = delete;
   ~xpu_runtime();
   const xpu::KernelInfo *find_exact(const std::string &name) const;
+  // cooperative: every block resident at once (hipModuleLaunchCooperativeKernel
+  // fails the launch otherwise), for kernels whose blocks wait on each other
   int launch(const xpu::KernelInfo &k, uint32_t gx, uint32_t gy, uint32_t bx, uint32_t shared,
-             const xpu_kernel_arg *args, uint32_t nargs);
+             const xpu_kernel_arg *args, uint32_t nargs, bool cooperative = false);
   // at least `bytes` of device scratch, 256-byte aligned; contents undefined
   int scratch(uint64_t bytes, void **out);
 };
