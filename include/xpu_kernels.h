@@ -101,6 +101,14 @@ int xpu_peak_read(xpu_runtime *rt, const void *input, uint64_t bytes, void *sink
 int run_peak_compute(int argc, char **argv);
 int run_peak_mem(int argc, char **argv);
 
+/* run_peak_sync (no reference counterpart): the cost of one dependent step
+ *   between launches of one block per compute unit: a kernel boundary on a
+ *   stream and in a graph (--launches N empty kernels, default 2000), and an
+ *   all-to-all handoff inside one cooperative launch in four publication
+ *   forms (--stages N, default 500). 0 on success, 1 on error or when the
+ *   in-kernel data check fails. */
+int run_peak_sync(int argc, char **argv);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,11 +15,8 @@
  * captured HIP graph (decode position and token live in device memory);
  * XPU_QWEN3_EAGER launches the same fused kernels one by one;
  * XPU_QWEN3_REFERENCE runs the reference's eight kernel entries with
- * blocking launches in the reference's order (main.cpp:159-226);
- * XPU_QWEN3_PERSISTENT runs a range of decode steps in one cooperative
- * launch of one block per compute unit, the kernel boundaries of the fused
- * step replaced by flags in device memory (contexts past the attention
- * split point continue as graph steps). All modes produce identical bits.
+ * blocking launches in the reference's order (main.cpp:159-226). All modes
+ * produce identical bits.
  */
 #ifndef XPU_QWEN3_H
 #define XPU_QWEN3_H
@@ -43,7 +40,6 @@ typedef struct {
 #define XPU_QWEN3_GRAPH 0
 #define XPU_QWEN3_EAGER 1
 #define XPU_QWEN3_REFERENCE 2
-#define XPU_QWEN3_PERSISTENT 3
 
 /* Tensor kinds for the synthetic generator (one seed stream each);
  * XPU_W_LMHEAD only exists for untied configs. */
@@ -110,8 +106,7 @@ int xpu_qwen3_create_from_checkpoint(xpu_runtime *rt, const char *model_dir, uin
 void xpu_qwen3_destroy(xpu_qwen3 *eng);
 int xpu_qwen3_get_config(const xpu_qwen3 *eng, xpu_qwen3_config *out);
 
-/* Select the mode for the following calls (XPU_QWEN3_PERSISTENT:
- * XPU_ERR_INVALID when the module has no persistent kernel for the shape). Reference mode keeps the KV
+/* Select the mode for the following calls. Reference mode keeps the KV
  * caches position-major ([layer][position][kv_head][128], as
  * qwen3/main.cpp:131-137), graph and eager modes chunk-major, in the same
  * buffers; graph and eager modes may alternate within a sequence. A decode
@@ -139,13 +134,6 @@ int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int batched);
  * per head. XPU_ERR_INVALID when the module lacks the kernels. */
 int xpu_qwen3_set_attention_split(xpu_qwen3 *eng, uint32_t min_context);
 
-/* Bound of each wait in the persistent decode kernel, in polls of about a
- * microsecond (default 1 << 22). A wait that passes it stops the whole
- * grid and the call fails with XPU_ERR_DEVICE; 0 gives up at the first poll
- * that finds a producer unfinished (used to test that exit). No reference
- * counterpart. */
-int xpu_qwen3_set_persist_wait_limit(xpu_qwen3 *eng, uint32_t polls);
-
 /* One forward step at `position` for input `token`; *next = greedy token
  * (Engine::decode, main.cpp:159-226). A non-finite logit fails with
  * XPU_ERR_VERIFY ("model produced a NaN or infinity", main.cpp:223-224). */
@@ -167,7 +155,7 @@ int xpu_qwen3_generate(xpu_qwen3 *eng, const uint32_t *prompt, uint32_t n_prompt
 /* Command line with the reference's flags (main.cpp:17-72):
  *   --model-dir DIR | --synthetic PRESET [--seed N] [--gain-std X]
  *   --input-ids FILE|- --max-new-tokens N [--max-seq-len N]
- *   [--mode graph|eager|reference|persistent] [--prefill batched|stepwise] [--no-eos-stop]
+ *   [--mode graph|eager|reference] [--prefill batched|stepwise] [--no-eos-stop]
  * prints {"generated_ids":[...]} on stdout, diagnostics on stderr. */
 int run_qwen3(int argc, char **argv);
 

@@ -61,7 +61,8 @@ def test_runtime_errors_cross_the_abi_as_codes():
     assert lib.xpu_module_kernel_names(b"/nonexistent.hsaco", ctypes.create_string_buffer(16), 16) == 3
 
 
-@pytest.mark.parametrize("program", ["gemv", "gemm", "qwen3_hip", "peak compute", "peak mem", "peak gemm"])
+@pytest.mark.parametrize("program", ["gemv", "gemm", "qwen3_hip", "peak compute", "peak mem", "peak gemm",
+                                     "peak sync"])
 def test_cli_rejects_bad_flags_without_touching_a_gpu(program):
     program, *mode = program.split()
     exe = [os.path.join(xpu.BUILD_DIR, program)] + mode

@@ -36,3 +36,20 @@ def test_peak_read_rate():
     gbs = float(re.search(r"Median read bandwidth: ([0-9.]+)", out).group(1))
     print(out)
     assert 1000.0 < gbs < 9000.0
+
+
+def test_peak_sync_handoff_costs():
+    # a kernel boundary against in-kernel all-to-all handoffs (peak sync):
+    # every variant completes its stages with the data it waited for
+    import re
+
+    exe = os.path.join(xpu.BUILD_DIR, "peak")
+    out = subprocess.run([exe, "sync", "--launches", "200", "--stages", "100"], capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert "Data check: PASS" in out.stdout
+    m = re.search(r"Kernel boundary, \d+ blocks per launch: ([0-9.]+) us .* ([0-9.]+) us in a graph", out.stdout)
+    assert m and 0 < float(m.group(2)) < 50
+    costs = re.findall(r"In-kernel all-to-all handoff, .*: ([0-9.]+) us per stage", out.stdout)
+    assert len(costs) == 4 and all(0 < float(c) < 1000 for c in costs)
+    print(out.stdout)

@@ -324,88 +324,3 @@ def test_mode_switch_mid_sequence_is_rejected(rt):
     out += [eng.decode(seq[2], 2), eng.decode(seq[3], 3)]
     assert out == ref
     eng.close()
-
-
-# ---- persistent decode (one cooperative launch per range of steps)
-
-def test_persistent_decode_steps_match_oracle_bitwise(rt):
-    # one launch per decode() call, positions 0..39 of the tiny shape
-    cfg = orc.config("tiny")
-    m = orc.Model(cfg, seed=5, gain_std=0.1, max_seq=48)
-    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=48, seed=5, gain_std=0.1, runtime=rt)
-    eng.set_mode(qwen3.PERSISTENT)
-    prompt = orc.tokens(20, 9, cfg.vocab)
-    token = int(prompt[0])
-    for pos in range(40):
-        print(f"persistent pos={pos}", flush=True)
-        ref_tok, ref_logits = m.decode(token, pos, want_logits=True)
-        tok = eng.decode(token, pos)
-        assert np.array_equal(eng.logits(), ref_logits), pos
-        assert np.array_equal(eng.hidden(), m.hidden()), pos
-        assert tok == ref_tok
-        token = int(prompt[pos + 1]) if pos + 1 < len(prompt) else tok
-    eng.close()
-
-
-@pytest.mark.parametrize("preset,n_prompt,new,batched", [("small", 24, 48, True), ("small", 24, 48, False),
-                                                        ("tiny", 5, 40, False), ("small", 250, 16, True)])
-def test_persistent_generate_matches_oracle(rt, preset, n_prompt, new, batched):
-    # a whole prompt + generation in one or two launches; ("small", 250, 16)
-    # crosses position 256, where the engine continues with graph steps (the
-    # attention split over compute units)
-    cfg = orc.config(preset)
-    max_seq = n_prompt + new
-    prompt = orc.tokens(n_prompt, 4, cfg.vocab)
-    m = orc.Model(cfg, seed=3, gain_std=0.05, max_seq=max_seq)
-    ref, ref_logits = m.generate(prompt, new, logit_steps=new)
-    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=max_seq, seed=3, gain_std=0.05, runtime=rt)
-    if batched:
-        eng.set_prefill(True)
-    else:
-        try:
-            eng.set_prefill(False)
-        except xpu.XpuError:
-            pass
-    eng.set_mode(qwen3.PERSISTENT)
-    print(f"persistent generate {preset} prompt={n_prompt} new={new} batched={batched}", flush=True)
-    out, pm, dm = eng.generate(prompt, new, stop_on_eos=False)
-    assert out.tolist() == ref.tolist()
-    assert np.array_equal(eng.logits(), ref_logits[new - 1])
-    assert np.array_equal(eng.hidden(), m.hidden())
-    print(f"prompt {pm:.2f} ms, decode {dm:.2f} ms")
-    eng.close()
-
-
-def test_persistent_baseline_workload_and_fixture_rows(rt):
-    # BASELINE configs[4] in one launch: the 128 tokens of the fixture, and
-    # the logits rows whose distance to transformers the fixture records
-    fx = qf.load("qwen3-0.6b")
-    cfg = qwen3.preset("qwen3-0.6b")
-    eng = qwen3.Engine(cfg, max_seq=256, seed=fx["weight_seed"], gain_std=fx["gain_std"], runtime=rt)
-    eng.set_mode(qwen3.PERSISTENT)
-    prompt = np.array(fx["prompt"], np.uint32)
-    out, pm, dm = eng.generate(prompt, fx["new_tokens"], stop_on_eos=False)
-    print(f"persistent 0.6B: prompt {pm:.2f} ms, decode {dm:.2f} ms ({(len(out) - 1) / dm * 1e3:.1f} tok/s)")
-    assert out.tolist() == fx["oracle_tokens"]
-    rows = engine_logit_rows(eng, fx)
-    assert [qf.row_hash(r) for r in rows] == fx["oracle_logits_sha256"]
-    eng.close()
-
-
-def test_persistent_wait_bound_stops_the_grid(rt):
-    # a wait bound of zero polls: the first wait that finds a producer
-    # unfinished stops every block (no hang), the call fails, and the engine
-    # decodes correctly again once the bound is restored
-    cfg = orc.config("small", layers=2)
-    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=64, seed=2, gain_std=0.1, runtime=rt)
-    eng.set_mode(qwen3.PERSISTENT)
-    prompt = orc.tokens(8, 2, cfg.vocab)
-    eng.set_persist_wait_limit(0)
-    with pytest.raises(xpu.XpuError, match="persistent decode stopped"):
-        eng.generate(prompt, 32, stop_on_eos=False)
-    eng.set_persist_wait_limit(1 << 22)
-    m = orc.Model(cfg, seed=2, gain_std=0.1, max_seq=64)
-    ref, _ = m.generate(prompt, 32)
-    out, _, _ = eng.generate(prompt, 32, stop_on_eos=False)
-    assert out.tolist() == ref.tolist()
-    eng.close()

@@ -114,7 +114,6 @@ def _declare(lib):
         "xpu_qwen3_set_mode": (c_int, [c_void_p, c_int]),
         "xpu_qwen3_set_prefill": (c_int, [c_void_p, c_int]),
         "xpu_qwen3_set_attention_split": (c_int, [c_void_p, c_uint32]),
-        "xpu_qwen3_set_persist_wait_limit": (c_int, [c_void_p, c_uint32]),
         "xpu_qwen3_decode": (c_int, [c_void_p, c_uint32, c_uint32, POINTER(c_uint32)]),
         "xpu_qwen3_logits": (c_int, [c_void_p, c_void_p, c_uint64]),
         "xpu_qwen3_hidden": (c_int, [c_void_p, c_void_p, c_uint64]),
@@ -142,6 +141,7 @@ def _declare(lib):
         "xpu_peak_mfma": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]),
         "xpu_peak_read": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_uint32]),
         "run_peak_compute": (c_int, [c_int, POINTER(c_char_p)]),
+        "run_peak_sync": (c_int, [c_int, POINTER(c_char_p)]),
         "run_peak_mem": (c_int, [c_int, POINTER(c_char_p)]),
         "run_qwen3": (c_int, [c_int, POINTER(c_char_p)]),
     }

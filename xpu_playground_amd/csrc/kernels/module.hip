@@ -10,6 +10,5 @@ __device__ xpu::StampRecord xpu_stamp_ring[xpu::kStampSlots * xpu::kStampRing];
 #include "gemv.hip"
 #include "synth.hip"
 #include "qwen3_ops.hip"
-#include "qwen3_persist.hip"
 #include "gemm.hip"
 #include "peak.hip"

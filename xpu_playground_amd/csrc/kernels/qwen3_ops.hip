@@ -426,41 +426,23 @@ XPU_DEVICE void dot_rows(const u32x4 (&a)[NC][R], const u32x4 (&xv)[NC], float (
   for (int r = 0; r < R; ++r) out[r] = xpu::wave_butterfly(xpu::fold8(acc[r]));
 }
 
-// The blocks a GEMV's rows are spread over: block bid of nblocks (a kernel's
-// own grid, or a persistent kernel's share of it). wait() runs between the
-// first batch of weight loads and the vector loads: a persistent kernel waits
-// there for the producer of the vector, with its weights already in flight.
-struct GridSpan {
-  uint32_t bid, nblocks;
-};
-struct NoWait {
-  XPU_DEVICE void operator()() const {}
-};
-XPU_DEVICE GridSpan own_grid() { return GridSpan{blockIdx.x, gridDim.x}; }
-
 // Grid-stride loop over output units (rows, or row pairs when PAIRED), one
 // unit group of R rows per wavefront per step. vec_load(first unit) issues
 // the vector loads (and any other early load), vec_finish turns them into
-// xv; body(unit0, out[R]). Without a wait the vector loads go out before the
-// first weight rows; with one, after the weights and the wait.
-template <int R, int NC, bool PAIRED, typename VecLoad, typename VecFinish, typename Body, typename Wait = NoWait>
+// xv; body(unit0, out[R]).
+template <int R, int NC, bool PAIRED, typename VecLoad, typename VecFinish, typename Body>
 XPU_DEVICE void reg_gemv(const uint16_t *__restrict__ W, uint32_t units, uint32_t K, VecLoad vec_load,
-                         VecFinish vec_finish, Body body, GridSpan g = own_grid(), Wait wait = Wait()) {
-  constexpr bool kWaits = !__is_same(Wait, NoWait);
+                         VecFinish vec_finish, Body body) {
   constexpr uint32_t per_wave = PAIRED ? R / 2 : R;
   constexpr uint32_t waves = kRegBlock / 64;  // launched with kRegBlock threads
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t rows_total = PAIRED ? 2 * units : units;
   const uint32_t pair_offset = PAIRED ? units : 0;
-  const uint32_t stride = g.nblocks * waves * per_wave;
-  uint32_t u0 = (g.bid * waves + wave) * per_wave;
-  if constexpr (!kWaits) vec_load(u0);
+  const uint32_t stride = gridDim.x * waves * per_wave;
+  uint32_t u0 = (blockIdx.x * waves + wave) * per_wave;
+  vec_load(u0);
   u32x4 a[NC][R];
   load_rows<R, NC, PAIRED>(W, K, rows_total, u0 < units ? u0 : 0, pair_offset, a);
-  if constexpr (kWaits) {
-    wait();
-    vec_load(u0);
-  }
   u32x4 xv[NC];
   vec_finish(xv);
   for (; u0 < units; u0 += stride) {
@@ -473,17 +455,14 @@ XPU_DEVICE void reg_gemv(const uint16_t *__restrict__ W, uint32_t units, uint32_
 
 }  // namespace
 
-// embed != nullptr (layer 0): the vector is row `token` of embed (read from
-// state[1] when token_in is ~0u), which block 0 of the span also writes to x.
-template <int R, int NC, typename Wait = NoWait>
+template <int R, int NC>
 XPU_DEVICE void q3_norm_gemv_reg(const uint16_t *__restrict__ W, uint16_t *x, const uint16_t *__restrict__ norm_w,
                                  uint16_t *__restrict__ out, uint32_t M, uint32_t K, float eps,
                                  const uint16_t *__restrict__ embed, const uint32_t *__restrict__ state,
-                                 uint32_t vocab, GridSpan g = own_grid(), Wait wait = Wait(),
-                                 uint32_t token_in = ~0u) {
+                                 uint32_t vocab) {
   const uint16_t *src = x;
   if (embed) {
-    uint32_t token = token_in == ~0u ? state[1] : token_in;
+    uint32_t token = state[1];
     if (token >= vocab) token = 0;
     src = embed + static_cast<uint64_t>(token) * K;
   }
@@ -496,7 +475,7 @@ XPU_DEVICE void q3_norm_gemv_reg(const uint16_t *__restrict__ W, uint16_t *x, co
         load_slices<NC>(norm_w, K, wr);
       },
       [&](u32x4 (&xv)[NC]) {
-        if (embed && g.bid == 0 && threadIdx.x < 64) {  // the residual stream starts as the embedding row
+        if (embed && blockIdx.x == 0 && threadIdx.x < 64) {  // the residual stream starts as the embedding row
 #pragma unroll
           for (int c = 0; c < NC; ++c)
             if (c * 512u + lane * 8u < K) *reinterpret_cast<u32x4 *>(x + c * 512u + lane * 8u) = xr[c];
@@ -510,13 +489,12 @@ XPU_DEVICE void q3_norm_gemv_reg(const uint16_t *__restrict__ W, uint16_t *x, co
         for (int r = 0; r < R; ++r)
           if (lane == static_cast<uint32_t>(r) && row0 + r < M)
             out[row0 + r] = static_cast<uint16_t>(xpu::f32_to_bf16(o[r]));
-      },
-      g, wait);
+      });
 }
 
-template <int R, int NC, typename Wait = NoWait>
+template <int R, int NC>
 XPU_DEVICE void q3_gemv_residual_reg(const uint16_t *__restrict__ W, const uint16_t *__restrict__ v, uint16_t *x,
-                                     uint32_t M, uint32_t K, GridSpan g = own_grid(), Wait wait = Wait()) {
+                                     uint32_t M, uint32_t K) {
   const uint32_t lane = xpu::lane_id();
   u32x4 vr[NC];
   // residual input of the first unit's rows (lane r: row u0 + r), loaded
@@ -541,14 +519,13 @@ XPU_DEVICE void q3_gemv_residual_reg(const uint16_t *__restrict__ W, const uint1
             const float sum = xpu::bf16_to_f32(old) + xpu::round_bf16(o[r]);
             x[row0 + r] = static_cast<uint16_t>(xpu::f32_to_bf16(sum));
           }
-      },
-      g, wait);
+      });
 }
 
-template <int R, int NC, typename Wait = NoWait>
+template <int R, int NC>
 XPU_DEVICE void q3_norm_gemv_swiglu_reg(const uint16_t *__restrict__ Wgu, const uint16_t *__restrict__ x,
                                         const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ h, uint32_t I,
-                                        uint32_t K, float eps, GridSpan g = own_grid(), Wait wait = Wait()) {
+                                        uint32_t K, float eps) {
   static_assert(R % 2 == 0, "gate/up rows come in pairs");
   constexpr int P = R / 2;
   const uint32_t lane = xpu::lane_id();
@@ -569,16 +546,14 @@ XPU_DEVICE void q3_norm_gemv_swiglu_reg(const uint16_t *__restrict__ Wgu, const 
         for (int p = 0; p < P; ++p)
           if (lane == static_cast<uint32_t>(p) && i0 + p < I)
             h[i0 + p] = static_cast<uint16_t>(silu_mul_code(xpu::round_bf16(o[p]), xpu::round_bf16(o[P + p])));
-      },
-      g, wait);
+      });
 }
 
-template <int R, int NC, typename Wait = NoWait>
+template <int R, int NC>
 XPU_DEVICE void q3_norm_gemv_logits_reg(const uint16_t *__restrict__ E, const uint16_t *__restrict__ x,
                                         const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ logits,
                                         uint32_t V, uint32_t K, float eps, float *__restrict__ part_val,
-                                        uint32_t *__restrict__ part_idx, uint32_t *__restrict__ part_bad,
-                                        GridSpan g = own_grid(), Wait wait = Wait()) {
+                                        uint32_t *__restrict__ part_idx, uint32_t *__restrict__ part_bad) {
   __shared__ float redv[4];
   __shared__ uint32_t redi[4], redb[4];
   const uint32_t lane = xpu::lane_id();
@@ -606,13 +581,12 @@ XPU_DEVICE void q3_norm_gemv_logits_reg(const uint16_t *__restrict__ E, const ui
           if (!xpu::finite_f(v)) bad = 1;
           xpu::argmax_merge(best, best_index, v, row0 + r);
         }
-      },
-      g, wait);
+      });
   xpu::block_argmax(best, best_index, bad, redv, redi, redb);
   if (threadIdx.x == 0) {
-    part_val[g.bid] = best;
-    part_idx[g.bid] = best_index;
-    part_bad[g.bid] = bad;
+    part_val[blockIdx.x] = best;
+    part_idx[blockIdx.x] = best_index;
+    part_bad[blockIdx.x] = bad;
   }
 }
 
@@ -671,25 +645,43 @@ XPU_Q3_REG_SET(8)
 // class tree across the 16 lanes of a chunk. Same operations in the same
 // order as attention_tail_short. Longer contexts use attention_head, or the
 // split kernels below.
-// The attention of one query head at the decode position pos_of() (read
-// after the first barrier, so a caller may supply it late): QK-norm / RoPE
-// of the head's q and its kv head's k, the new k / v into the chunk-major
-// caches (the first head of each kv group), then the scores and P.V of
-// positions 0..pos into out[head]. Used by xpu_q3_attention (head =
-// blockIdx.x) and by the persistent decode kernel.
-template <typename PosOf>
-XPU_DEVICE void attention_decode_head(uint32_t head, const uint16_t *__restrict__ qkv,
-                                      const uint16_t *__restrict__ qnorm_w, const uint16_t *__restrict__ knorm_w,
-                                      const uint16_t *__restrict__ cos_row, const uint16_t *__restrict__ sin_row,
-                                      uint16_t *__restrict__ kcache, uint16_t *__restrict__ vcache,
-                                      uint16_t *__restrict__ out, PosOf pos_of, uint32_t heads, uint32_t kv_heads,
-                                      uint32_t max_seq, float eps, float scale) {
+extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
+    const uint16_t *__restrict__ qkv, const uint16_t *__restrict__ qnorm_w,
+    const uint16_t *__restrict__ knorm_w, const uint16_t *__restrict__ cos_row,
+    const uint16_t *__restrict__ sin_row, uint16_t *__restrict__ kcache,
+    uint16_t *__restrict__ vcache, uint16_t *__restrict__ out, const uint32_t *__restrict__ state,
+    uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float eps, float scale,
+    const uint16_t *__restrict__ prefetch, uint64_t prefetch_bytes, uint32_t prefetch_delay) {
+  XPU_STAMP(xpu::kStampQ3Attention);
   __shared__ float sbuf[xpu::kAttnChunk];
   __shared__ float red[4 * xpu::kHeadDim];
   __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
   __shared__ __align__(16) uint16_t ks[xpu::kHeadDim];
   __shared__ __align__(16) uint16_t junk[2 * xpu::kHeadDim];
   __shared__ __align__(16) uint16_t vtile[xpu::kAttnTile * xpu::kVPitch];
+  const uint32_t head = blockIdx.x;
+  if (head >= heads) {
+    // Blocks past the query heads read [prefetch, prefetch + prefetch_bytes)
+    // (the weights of the kernels that follow) so that they come from the
+    // Infinity Cache, not HBM, when those kernels run; the attention itself
+    // occupies only `heads` compute units for its latency-bound duration.
+    // start after prefetch_delay x 64 x 8 cycles, behind the attention's
+    // own loads
+    for (uint32_t d = 0; d < prefetch_delay; ++d) __builtin_amdgcn_s_sleep(8);
+    const uint64_t n16 = prefetch_bytes / 16u;
+    const u32x4 *p = reinterpret_cast<const u32x4 *>(prefetch);
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x - heads) * blockDim.x;
+    uint32_t acc = 0;
+    for (uint64_t i = static_cast<uint64_t>(head - heads) * blockDim.x + threadIdx.x; i < n16; i += 4 * stride) {
+      u32x4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = i + u * stride < n16 ? p[i + u * stride] : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].w;
+    }
+    asm volatile("" : : "v"(acc));  // keeps the loads
+    return;
+  }
   const uint32_t group = heads / kv_heads;
   const uint32_t kv = head / group;
   const uint16_t *qsrc = qkv + head * xpu::kHeadDim;
@@ -720,7 +712,7 @@ XPU_DEVICE void attention_decode_head(uint32_t head, const uint16_t *__restrict_
                             wave == 0 ? qs : wave == 1 ? ks : junk + (wave - 2) * xpu::kHeadDim);
   }
   __syncthreads();  // 1: qs, ks
-  const uint32_t pos = pos_of();
+  const uint32_t pos = state[0];
   if (pos >= max_seq) return;  // the reference skips the step (kernels.hpp:74-75)
   const uint32_t n = pos + 1;
   const bool short_ctx = n <= xpu::kAttnTile;
@@ -794,41 +786,6 @@ XPU_DEVICE void attention_decode_head(uint32_t head, const uint16_t *__restrict_
   if (cls == 0)
     *reinterpret_cast<u32x4 *>(out + head * xpu::kHeadDim + vch * 8u) =
         u32x4{code[0] | (code[1] << 16), code[2] | (code[3] << 16), code[4] | (code[5] << 16), code[6] | (code[7] << 16)};
-}
-
-extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
-    const uint16_t *__restrict__ qkv, const uint16_t *__restrict__ qnorm_w,
-    const uint16_t *__restrict__ knorm_w, const uint16_t *__restrict__ cos_row,
-    const uint16_t *__restrict__ sin_row, uint16_t *__restrict__ kcache,
-    uint16_t *__restrict__ vcache, uint16_t *__restrict__ out, const uint32_t *__restrict__ state,
-    uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float eps, float scale,
-    const uint16_t *__restrict__ prefetch, uint64_t prefetch_bytes, uint32_t prefetch_delay) {
-  XPU_STAMP(xpu::kStampQ3Attention);
-  const uint32_t head = blockIdx.x;
-  if (head >= heads) {
-    // Blocks past the query heads read [prefetch, prefetch + prefetch_bytes)
-    // (the weights of the kernels that follow) so that they come from the
-    // Infinity Cache, not HBM, when those kernels run; the attention itself
-    // occupies only `heads` compute units for its latency-bound duration.
-    // start after prefetch_delay x 64 x 8 cycles, behind the attention's
-    // own loads
-    for (uint32_t d = 0; d < prefetch_delay; ++d) __builtin_amdgcn_s_sleep(8);
-    const uint64_t n16 = prefetch_bytes / 16u;
-    const u32x4 *p = reinterpret_cast<const u32x4 *>(prefetch);
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x - heads) * blockDim.x;
-    uint32_t acc = 0;
-    for (uint64_t i = static_cast<uint64_t>(head - heads) * blockDim.x + threadIdx.x; i < n16; i += 4 * stride) {
-      u32x4 v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = i + u * stride < n16 ? p[i + u * stride] : u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].w;
-    }
-    asm volatile("" : : "v"(acc));  // keeps the loads
-    return;
-  }
-  attention_decode_head(head, qkv, qnorm_w, knorm_w, cos_row, sin_row, kcache, vcache, out,
-                        [&] { return state[0]; }, heads, kv_heads, max_seq, eps, scale);
 }
 
 // Attention split over compute units (two kernels, for long contexts): the

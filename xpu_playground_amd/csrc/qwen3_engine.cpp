@@ -18,7 +18,6 @@
 #include "../../include/xpu_kernels.h"
 #include "host_common.hpp"
 #include "json.hpp"
-#include "kernels/persist_abi.h"
 #include "runtime_internal.hpp"
 
 #include <algorithm>
@@ -167,23 +166,13 @@ struct xpu_qwen3 {
   const xpu::KernelInfo *pf_attn_short_k = nullptr;  // chunks whose contexts stay within 256 positions
   const xpu::KernelInfo *pf_embed_k = nullptr, *pf_norm_k = nullptr, *pf_rope_k = nullptr, *pf_attn_k = nullptr,
                         *pf_qkv_k = nullptr, *pf_o_k = nullptr, *pf_gu_k = nullptr, *pf_down_k = nullptr;
-  // persistent decode (kernels/qwen3_persist.hip): its kernel for this shape,
-  // one device block holding the argument block, the per-layer pointers,
-  // the stage flags (one word per block and stage) and the error word; the
-  // next stage tick; the wait bound
-  const xpu::KernelInfo *persist_k = nullptr;
-  void *persist_block = nullptr;
-  xpu_persist_args *persist_args = nullptr;
-  uint32_t *persist_error = nullptr;
-  uint32_t persist_tick = 1, persist_spin_limit = 1u << 22;
 
   ~xpu_qwen3() {
     if (graph) xpu_rt_graph_destroy(graph);
     if (graph_split) xpu_rt_graph_destroy(graph_split);
     if (rt) {
       for (void *p : {static_cast<void *>(arena), static_cast<void *>(kcache), static_cast<void *>(vcache),
-                      static_cast<void *>(cos_t), static_cast<void *>(sin_t), static_cast<void *>(x), pf_block,
-                      persist_block})
+                      static_cast<void *>(cos_t), static_cast<void *>(sin_t), static_cast<void *>(x), pf_block})
         if (p) xpu_rt_free(rt, p);
       if (owns_rt) xpu_rt_destroy(rt);
     }
@@ -594,102 +583,6 @@ int reference_step(xpu_qwen3 &e, uint32_t token, uint32_t position, uint32_t *ne
   return xpu_rt_copy_from_device(rt, next, e.ref_token, 4);
 }
 
-// Persistent decode needs the kernel instantiated for the shape's
-// register-vector widths (hidden, heads * 128, intermediate) and a compute
-// unit per query head. Without it the mode is unavailable.
-int setup_persist(xpu_qwen3 &e) {
-  const xpu_qwen3_config &c = e.c;
-  auto nc = [](uint32_t K) -> uint32_t {
-    for (uint32_t n : {1u, 2u, 4u, 6u, 8u})
-      if (K <= 512u * n) return n;
-    return 0;
-  };
-  const uint32_t qd = c.heads * c.head_dim;
-  const uint32_t nh = nc(c.hidden), nq = nc(qd), ni = nc(c.intermediate);
-  if (!nh || !nq || !ni || c.heads > e.rt->compute_units) return XPU_OK;
-  e.persist_k = e.rt->find_exact("xpu_q3_persist_h" + std::to_string(nh) + "_q" + std::to_string(nq) + "_i" +
-                                 std::to_string(ni));
-  if (!e.persist_k) return XPU_OK;
-  const uint32_t nb = e.rt->compute_units;
-  const uint64_t layers_bytes = (uint64_t{c.layers} * sizeof(xpu_persist_layer) + 255) & ~uint64_t{255};
-  const uint64_t args_bytes = (sizeof(xpu_persist_args) + 255) & ~uint64_t{255};
-  const uint64_t flags_bytes = (6ull * nb * 4 + 255) & ~uint64_t{255};
-  int rc = xpu_rt_alloc(e.rt, layers_bytes + args_bytes + flags_bytes + 256, 4096, &e.persist_block);
-  if (rc) return rc;
-  uint8_t *base = static_cast<uint8_t *>(e.persist_block);
-  auto *layers_dev = reinterpret_cast<xpu_persist_layer *>(base);
-  e.persist_args = reinterpret_cast<xpu_persist_args *>(base + layers_bytes);
-  auto *flags = reinterpret_cast<uint32_t *>(base + layers_bytes + args_bytes);
-  e.persist_error = reinterpret_cast<uint32_t *>(base + layers_bytes + args_bytes + flags_bytes);
-  if ((rc = xpu_rt_memset(e.rt, e.persist_block, 0, layers_bytes + args_bytes + flags_bytes + 256))) return rc;
-  const uint64_t cache_layer = uint64_t{c.kv_heads} * e.max_seq * c.head_dim;
-  std::vector<xpu_persist_layer> layers(c.layers);
-  for (uint32_t l = 0; l < c.layers; ++l) {
-    const Layer &L = e.layers[l];
-    layers[l] = {L.qkv, L.o, L.gu, L.down, L.in_norm, L.post_norm, L.q_norm, L.k_norm,
-                 e.kcache + l * cache_layer, e.vcache + l * cache_layer};
-  }
-  xpu_persist_args a{};
-  a.layers = layers_dev;
-  a.embed = e.embed;
-  a.final_norm = e.final_norm;
-  a.lm_head = e.lm_head;
-  a.cos_t = e.cos_t;
-  a.sin_t = e.sin_t;
-  a.x = e.x;
-  a.qkv = e.qkv;
-  a.attn = e.attn;
-  a.h = e.h;
-  a.logits = e.logits;
-  a.part_val = e.part_val;
-  a.part_idx = e.part_idx;
-  a.part_bad = e.part_bad;
-  a.state = e.state;
-  a.prompt = e.prompt;
-  a.gen = e.gen;
-  a.flags = flags;
-  a.error = e.persist_error;
-  a.layers_n = c.layers;
-  a.hidden = c.hidden;
-  a.inter = c.intermediate;
-  a.vocab = c.vocab;
-  a.heads = c.heads;
-  a.kv_heads = c.kv_heads;
-  a.max_seq = e.max_seq;
-  a.gen_capacity = e.max_seq;
-  a.eps = c.rms_eps;
-  a.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
-  a.spin_limit = e.persist_spin_limit;
-  if (nb > e.nparts) return set_error(XPU_ERR_INVALID, "persistent decode: more blocks than argmax partials");
-  if ((rc = xpu_rt_copy_to_device(e.rt, layers_dev, layers.data(), layers.size() * sizeof(xpu_persist_layer))))
-    return rc;
-  return xpu_rt_copy_to_device(e.rt, e.persist_args, &a, sizeof(a));
-}
-
-// Decode steps at positions [p_begin, p_end) in one persistent launch
-// (state[1] holds the input token of p_begin, state[3] the prompt length).
-int run_persist(xpu_qwen3 &e, uint32_t p_begin, uint32_t p_end) {
-  if (p_end <= p_begin) return XPU_OK;
-  uint32_t tick = e.persist_tick;
-  const xpu_kernel_arg args[] = {{8, &e.persist_args}, {4, &p_begin}, {4, &p_end}, {4, &tick}};
-  const int rc = e.rt->launch(*e.persist_k, e.rt->compute_units, 1, 256, 0, args, 4, true);
-  if (rc) return rc;
-  e.persist_tick += (p_end - p_begin) * (e.c.layers + 1);
-  return XPU_OK;
-}
-
-// The error word of the last persistent launches (waits on the stream).
-int check_persist(xpu_qwen3 &e) {
-  uint32_t err = 0;
-  int rc = xpu_rt_copy_from_device(e.rt, &err, e.persist_error, 4);
-  if (rc) return rc;
-  if (err) {
-    xpu_rt_memset(e.rt, e.persist_error, 0, 4);
-    return set_error(XPU_ERR_DEVICE, "persistent decode stopped: a block's wait for another passed its bound");
-  }
-  return XPU_OK;
-}
-
 int init_engine(xpu_qwen3 &e, xpu_runtime *rt, const xpu_qwen3_config &cfg, uint32_t max_seq) {
   int rc = validate_config(cfg);
   if (rc) return rc;
@@ -707,8 +600,7 @@ int init_engine(xpu_qwen3 &e, xpu_runtime *rt, const xpu_qwen3_config &cfg, uint
   if ((rc = allocate_buffers(e))) return rc;
   plan_arena(e, e.arena);
   if ((rc = setup_launches(e))) return rc;
-  if ((rc = setup_prefill(e))) return rc;
-  return setup_persist(e);
+  return setup_prefill(e);
 }
 
 // ---------------------------------------------------------------- checkpoint
@@ -1083,11 +975,8 @@ extern "C" int xpu_qwen3_get_config(const xpu_qwen3 *eng, xpu_qwen3_config *out)
 
 extern "C" int xpu_qwen3_set_mode(xpu_qwen3 *eng, int mode) {
   if (!eng) return set_error(XPU_ERR_INVALID, "null engine");
-  if (mode != XPU_QWEN3_GRAPH && mode != XPU_QWEN3_EAGER && mode != XPU_QWEN3_REFERENCE &&
-      mode != XPU_QWEN3_PERSISTENT)
+  if (mode != XPU_QWEN3_GRAPH && mode != XPU_QWEN3_EAGER && mode != XPU_QWEN3_REFERENCE)
     return set_error(XPU_ERR_INVALID, "unknown Qwen3 mode");
-  if (mode == XPU_QWEN3_PERSISTENT && !eng->persist_k)
-    return set_error(XPU_ERR_INVALID, "persistent decode has no kernel for this model shape");
   eng->mode = mode;
   return XPU_OK;
 }
@@ -1098,13 +987,6 @@ extern "C" int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int batched) {
     return set_error(XPU_ERR_INVALID, "batched prefill has no kernels for this model shape");
   eng->batched_prefill = batched != 0;
   return XPU_OK;
-}
-
-extern "C" int xpu_qwen3_set_persist_wait_limit(xpu_qwen3 *eng, uint32_t polls) {
-  if (!eng) return set_error(XPU_ERR_INVALID, "null engine");
-  if (!eng->persist_k) return set_error(XPU_ERR_INVALID, "persistent decode has no kernel for this model shape");
-  eng->persist_spin_limit = polls;
-  return xpu_rt_copy_to_device(eng->rt, &eng->persist_args->spin_limit, &polls, 4);
 }
 
 extern "C" int xpu_qwen3_set_attention_split(xpu_qwen3 *eng, uint32_t min_context) {
@@ -1149,13 +1031,8 @@ extern "C" int xpu_qwen3_decode(xpu_qwen3 *eng, uint32_t token, uint32_t positio
   } else {
     const uint32_t st[4] = {position, token, 0, 0};
     if ((rc = xpu_rt_copy_to_device(eng->rt, eng->state, st, sizeof(st)))) return rc;
-    if (eng->mode == XPU_QWEN3_PERSISTENT) {
-      if ((rc = run_persist(*eng, position, position + 1))) return rc;
-      if ((rc = check_persist(*eng))) return rc;
-    } else {
-      if ((rc = set_rope_row(*eng, position))) return rc;
-      if ((rc = run_fused_step(*eng, position))) return rc;
-    }
+    if ((rc = set_rope_row(*eng, position))) return rc;
+    if ((rc = run_fused_step(*eng, position))) return rc;
     uint32_t back[4];
     if ((rc = xpu_rt_copy_from_device(eng->rt, back, eng->state, sizeof(back)))) return rc;
     result = back[2];
@@ -1222,29 +1099,11 @@ extern "C" int xpu_qwen3_generate(xpu_qwen3 *eng, const uint32_t *prompt, uint32
       if ((rc = xpu_rt_event_create(eng->rt, &v))) return rc;
     rc = xpu_rt_event_record(eng->rt, ev[0]);
     if (!rc && first) rc = run_prefill(*eng, first);
-    if (eng->mode == XPU_QWEN3_PERSISTENT) {
-      // persistent launches while the context fits the one-block-per-head
-      // attention's short range (below the split point), graph steps after
-      const uint32_t limit = eng->split_ok && eng->split_from ? eng->split_from - 1 : steps;
-      auto span = [&](uint32_t a, uint32_t b) -> int {  // positions [a, b)
-        const uint32_t mid = std::min(b, std::max(a, limit));
-        int r = run_persist(*eng, a, mid);
-        if (!r && mid < b) r = set_rope_row(*eng, mid);
-        for (uint32_t s = mid; !r && s < b; ++s) r = run_fused_step(*eng, s);
-        return r;
-      };
-      if (!rc) rc = span(first, n_prompt);
-      if (!rc) rc = xpu_rt_event_record(eng->rt, ev[1]);
-      if (!rc) rc = span(n_prompt, steps);
-      if (!rc) rc = xpu_rt_event_record(eng->rt, ev[2]);
-      if (!rc) rc = check_persist(*eng);
-    } else {
-      for (uint32_t s = first; !rc && s < steps; ++s) {
-        rc = run_fused_step(*eng, s);
-        if (!rc && s + 1 == n_prompt) rc = xpu_rt_event_record(eng->rt, ev[1]);
-      }
-      if (!rc) rc = xpu_rt_event_record(eng->rt, ev[2]);
+    for (uint32_t s = first; !rc && s < steps; ++s) {
+      rc = run_fused_step(*eng, s);
+      if (!rc && s + 1 == n_prompt) rc = xpu_rt_event_record(eng->rt, ev[1]);
     }
+    if (!rc) rc = xpu_rt_event_record(eng->rt, ev[2]);
     float a = 0, b = 0;
     if (!rc) rc = xpu_rt_event_elapsed_ms(ev[0], ev[1], &a);
     if (!rc) rc = xpu_rt_event_elapsed_ms(ev[1], ev[2], &b);
@@ -1309,7 +1168,7 @@ QwenOptions parse_qwen(int argc, char **argv) {
       std::cout << "Usage: " << argv[0]
                 << " --model-dir DIR | --synthetic qwen3-0.6b|qwen3-8b|tiny|small [--seed N] [--gain-std X]\n"
                    "       --input-ids FILE|- --max-new-tokens N [--max-seq-len N]\n"
-                   "       [--mode graph|eager|reference|persistent] [--prefill batched|stepwise] [--no-eos-stop]\n";
+                   "       [--mode graph|eager|reference] [--prefill batched|stepwise] [--no-eos-stop]\n";
       std::exit(0);
     }
     if (opt == "--no-eos-stop") { o.stop_on_eos = false; continue; }
@@ -1326,8 +1185,7 @@ QwenOptions parse_qwen(int argc, char **argv) {
       if (v == "graph") o.mode = XPU_QWEN3_GRAPH;
       else if (v == "eager") o.mode = XPU_QWEN3_EAGER;
       else if (v == "reference") o.mode = XPU_QWEN3_REFERENCE;
-      else if (v == "persistent") o.mode = XPU_QWEN3_PERSISTENT;
-      else qwen_usage_error("--mode must be graph, eager, reference or persistent");
+      else qwen_usage_error("--mode must be graph, eager or reference");
     } else if (opt == "--prefill") {
       if (v == "batched") o.prefill = 1;
       else if (v == "stepwise") o.prefill = 0;

@@ -14,7 +14,7 @@ import numpy as np
 
 from . import Qwen3Config, Runtime, check, library
 
-GRAPH, EAGER, REFERENCE, PERSISTENT = 0, 1, 2, 3
+GRAPH, EAGER, REFERENCE = 0, 1, 2
 EOS_TOKENS = (151645, 151643)  # qwen3/model.hpp:19-20
 
 
@@ -113,9 +113,6 @@ class Engine:
     def set_prefill(self, batched: bool) -> None:
         """Batched (default) or stepwise prompt processing in generate."""
         check(self.lib.xpu_qwen3_set_prefill(self.handle, 1 if batched else 0))
-
-    def set_persist_wait_limit(self, polls: int) -> None:
-        check(self.lib.xpu_qwen3_set_persist_wait_limit(self.handle, c_uint32(polls)))
 
     def set_attention_split(self, min_context: int) -> None:
         """Split the attention over compute units for contexts of at least

@@ -87,9 +87,11 @@ def launches(recs: np.ndarray) -> list[dict]:
         start, end = int(r["real_start"]), int(r["real_start"]) + int(r["real_ticks"])
         if cur is None or r["kernel"] != cur["kernel"] or start >= cur["end"]:
             cur = {"kernel": int(r["kernel"]), "start": start, "end": end, "waves": 0, "clock": defaultdict(list),
-                   "residency": []}
+                   "residency": [], "block_end": {}}
             out.append(cur)
         cur["end"] = max(cur["end"], end)
+        b = int(r["block"])
+        cur["block_end"][b] = max(cur["block_end"].get(b, 0), end)
         cur["waves"] += 1
         if r["real_ticks"]:
             cur["clock"][int(r["xcc"])].append(r["clock_ticks"] / (r["real_ticks"] * TICK_NS))
@@ -167,11 +169,20 @@ def run_decode(args) -> dict:
     first = finishes[-(len(out) - 1) - 1] + 1 if len(finishes) >= len(out) else 0
     steps = lns[first:]
     token_us = (steps[-1]["end"] - steps[0]["start"]) * TICK_NS / 1e3 / max(1, len(out) - 1)
+    # the attention kernel: its query-head blocks against the blocks that
+    # prefetch the layer's remaining weights
+    att = [ln for ln in steps if ln["name"] == "attention"]
+    heads_us = [(max(v for b, v in ln["block_end"].items() if b < cfg.heads) - ln["start"]) * TICK_NS / 1e3
+                for ln in att]
+    rest_us = [(max((v for b, v in ln["block_end"].items() if b >= cfg.heads), default=ln["start"]) - ln["start"])
+               * TICK_NS / 1e3 for ln in att]
     eng.close()
     rt.close()
     return {"workload": f"{args.preset} decode, {args.prompt} prompt ids, {args.new} new tokens, {args.mode} mode",
             "decode_ms_events": round(dm, 3), "tok_s_events": round((len(out) - 1) / dm * 1e3, 1),
             "token_us_stamps": round(token_us, 2), "kernels_per_token": len(steps) / max(1, len(out) - 1),
+            "attention_head_blocks_mean_us": round(float(np.mean(heads_us)), 3) if heads_us else None,
+            "attention_prefetch_blocks_mean_us": round(float(np.mean(rest_us)), 3) if rest_us else None,
             "per_kernel": summarize(steps)}
 
 
