@@ -668,16 +668,21 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
     // start after prefetch_delay x 64 x 8 cycles, behind the attention's
     // own loads
     for (uint32_t d = 0; d < prefetch_delay; ++d) __builtin_amdgcn_s_sleep(8);
+    // 8 16-byte loads in flight per thread, branch-free (indices past the
+    // range re-read its last word): the prefetch then ends before the query
+    // heads (4 loads in flight outlasted them by ~1 us, 16 slowed them)
+    constexpr int kUnroll = 8;
     const uint64_t n16 = prefetch_bytes / 16u;
+    if (n16 == 0) return;
     const u32x4 *p = reinterpret_cast<const u32x4 *>(prefetch);
     const uint64_t stride = static_cast<uint64_t>(gridDim.x - heads) * blockDim.x;
     uint32_t acc = 0;
-    for (uint64_t i = static_cast<uint64_t>(head - heads) * blockDim.x + threadIdx.x; i < n16; i += 4 * stride) {
-      u32x4 v[4];
+    for (uint64_t i = static_cast<uint64_t>(head - heads) * blockDim.x + threadIdx.x; i < n16; i += kUnroll * stride) {
+      u32x4 v[kUnroll];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = i + u * stride < n16 ? p[i + u * stride] : u32x4{0, 0, 0, 0};
+      for (int u = 0; u < kUnroll; ++u) v[u] = p[min(i + u * stride, n16 - 1)];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].w;
+      for (int u = 0; u < kUnroll; ++u) acc ^= v[u].x ^ v[u].w;
     }
     asm volatile("" : : "v"(acc));  // keeps the loads
     return;

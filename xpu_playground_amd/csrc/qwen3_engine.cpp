@@ -291,6 +291,7 @@ uint16_t *tensor_location(xpu_qwen3 &e, int kind, uint32_t layer) {
 
 int setup_launches(xpu_qwen3 &e) {
   const xpu_qwen3_config &c = e.c;
+  // at most 4 blocks per CU for the decode GEMVs (2 measured the same, 1 slower)
   const uint32_t cap = e.rt->compute_units * 4;
   auto find = [&](const char *name, xpu_qwen3::Launch &l) -> int {
     l.k = e.rt->find_exact(name);

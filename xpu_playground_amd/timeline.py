@@ -129,7 +129,7 @@ def summarize(lns: list[dict]) -> dict:
 
 
 def run_gemm(args) -> dict:
-    rt = Runtime(module_path=STAMPS_MODULE)
+    rt = Runtime(module_path=args.module)
     st = Stamps(rt)
     dt = FP16 if args.type == "fp16" else BF16
     m, n, k = (args.size,) * 3 if args.size else (args.m, args.n, args.k)
@@ -153,7 +153,7 @@ def run_gemm(args) -> dict:
 def run_decode(args) -> dict:
     from . import qwen3
 
-    rt = Runtime(module_path=STAMPS_MODULE)
+    rt = Runtime(module_path=args.module)
     st = Stamps(rt)
     cfg = qwen3.preset(args.preset)
     max_seq = args.prompt + args.new
@@ -201,9 +201,11 @@ def main(argv=None) -> int:
     d.add_argument("--prompt", type=int, default=128)
     d.add_argument("--new", type=int, default=12)
     d.add_argument("--mode", choices=["graph", "eager"], default="graph")
+    for p in (g, d):
+        p.add_argument("--module", default=STAMPS_MODULE, help="a code object built with -DXPU_STAMPS")
     args = ap.parse_args(argv)
-    if not os.path.exists(STAMPS_MODULE):
-        print(f"{STAMPS_MODULE} is missing: build it (make -C xpu_playground_amd/csrc)", file=sys.stderr)
+    if not os.path.exists(args.module):
+        print(f"{args.module} is missing: build it (make -C xpu_playground_amd/csrc)", file=sys.stderr)
         return 1
     if args.what == "gemm" and (args.m or args.n or args.k):
         args.size = 0
