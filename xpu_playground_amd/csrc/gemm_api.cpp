@@ -18,9 +18,11 @@ uint64_t round_up8(uint64_t v) { return (v + 7) & ~uint64_t{7}; }
 // Copies a rows x cols matrix (row stride src_ld) into dst with dst_cols
 // columns, zero-filling columns cols..dst_cols-1 (kernels/gemm.hip
 // xpu_pad_rows).
+// blocks of 256 threads, each thread 4 chunks per step (kernels/gemm.hip
+// kPadUnroll), at most 8 resident blocks per compute unit
 uint32_t pad_grid(const xpu_runtime *rt, uint32_t rows, uint32_t dst_cols) {
-  const uint64_t threads = static_cast<uint64_t>(rows) * (dst_cols / 8);
-  return std::max(1u, static_cast<uint32_t>(std::min<uint64_t>((threads + 255) / 256, rt->compute_units * 16ull)));
+  const uint64_t threads = (static_cast<uint64_t>(rows) * (dst_cols / 8) + 3) / 4;
+  return std::max(1u, static_cast<uint32_t>(std::min<uint64_t>((threads + 255) / 256, rt->compute_units * 8ull)));
 }
 
 int pad_rows(xpu_runtime *rt, const void *src, uint64_t src_ld, uint32_t rows, uint32_t cols, void *dst,

@@ -424,37 +424,51 @@ XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dmau, xpu::kFp16, 4, 64, 2, 4, 2, 1, false)
 // The chunk holding the row's end is read element by element, so no load
 // reaches past the last element of a row.
 namespace xpu {
-// Blocks block0 .. block0 + nblocks - 1 of the grid copy one matrix.
+// One 16-byte destination chunk (8 elements from column c0 of src row p).
+XPU_DEVICE xpu::u32x4 pad_chunk(const uint16_t *__restrict__ p, uint32_t c0, uint32_t cols) {
+  if (c0 + 8u <= cols) {
+    if ((reinterpret_cast<uintptr_t>(p) & 3u) == 0) return *reinterpret_cast<const xpu::u32x4 *>(p);
+    const xpu::u32x4 d = *reinterpret_cast<const xpu::u32x4 *>(p - 1);  // elements -1..6
+    const uint32_t last = p[7];
+    return xpu::u32x4{__builtin_amdgcn_alignbit(d.y, d.x, 16), __builtin_amdgcn_alignbit(d.z, d.y, 16),
+                      __builtin_amdgcn_alignbit(d.w, d.z, 16), __builtin_amdgcn_alignbit(last, d.w, 16)};
+  }
+  uint32_t w[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t lo = c0 + 2 * q < cols ? p[2 * q] : 0u;
+    const uint32_t hi = c0 + 2 * q + 1 < cols ? p[2 * q + 1] : 0u;
+    w[q] = lo | (hi << 16);
+  }
+  return xpu::u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// Blocks block0 .. block0 + nblocks - 1 of the grid copy one matrix; each
+// thread takes kPadUnroll chunks a grid stride apart per step, all loads
+// issued before the stores.
+constexpr int kPadUnroll = 4;
 XPU_DEVICE void pad_rows(const uint16_t *__restrict__ src, uint64_t src_ld, uint32_t rows, uint32_t cols,
                          uint16_t *__restrict__ dst, uint32_t dst_cols, uint32_t block0, uint32_t nblocks) {
   const uint64_t chunks_per_row = dst_cols / 8u;
   const uint64_t total = static_cast<uint64_t>(rows) * chunks_per_row;
+  const uint64_t stride = static_cast<uint64_t>(nblocks) * blockDim.x;
   for (uint64_t idx = static_cast<uint64_t>(blockIdx.x - block0) * blockDim.x + threadIdx.x; idx < total;
-       idx += static_cast<uint64_t>(nblocks) * blockDim.x) {
-    const uint64_t r = idx / chunks_per_row;
-    const uint32_t c0 = static_cast<uint32_t>(idx % chunks_per_row) * 8u;
-    const uint16_t *p = src + r * src_ld + c0;
-    xpu::u32x4 v;
-    if (c0 + 8u <= cols) {
-      if ((reinterpret_cast<uintptr_t>(p) & 3u) == 0) {
-        v = *reinterpret_cast<const xpu::u32x4 *>(p);
-      } else {
-        const xpu::u32x4 d = *reinterpret_cast<const xpu::u32x4 *>(p - 1);  // elements -1..6
-        const uint32_t last = p[7];
-        v = xpu::u32x4{__builtin_amdgcn_alignbit(d.y, d.x, 16), __builtin_amdgcn_alignbit(d.z, d.y, 16),
-                       __builtin_amdgcn_alignbit(d.w, d.z, 16), __builtin_amdgcn_alignbit(last, d.w, 16)};
-      }
-    } else {
-      uint32_t w[4];
+       idx += kPadUnroll * stride) {
+    xpu::u32x4 v[kPadUnroll];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t lo = c0 + 2 * q < cols ? p[2 * q] : 0u;
-        const uint32_t hi = c0 + 2 * q + 1 < cols ? p[2 * q + 1] : 0u;
-        w[q] = lo | (hi << 16);
+    for (int u = 0; u < kPadUnroll; ++u) {
+      const uint64_t i = idx + u * stride;
+      if (i < total) {
+        const uint64_t r = i / chunks_per_row;
+        const uint32_t c0 = static_cast<uint32_t>(i % chunks_per_row) * 8u;
+        v[u] = pad_chunk(src + r * src_ld + c0, c0, cols);
       }
-      v = xpu::u32x4{w[0], w[1], w[2], w[3]};
     }
-    *reinterpret_cast<xpu::u32x4 *>(dst + r * dst_cols + c0) = v;
+#pragma unroll
+    for (int u = 0; u < kPadUnroll; ++u) {
+      const uint64_t i = idx + u * stride;
+      if (i < total) *reinterpret_cast<xpu::u32x4 *>(dst + (i / chunks_per_row) * dst_cols + (i % chunks_per_row) * 8u) = v[u];
+    }
   }
 }
 }  // namespace xpu
