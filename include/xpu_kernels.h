@@ -35,9 +35,17 @@ int xpu_gemv(xpu_runtime *rt, int dtype, const void *A, const void *x, void *y,
 
 /* C[M x N] = A[M x K] . B[K x N], row-major, FP32 accumulation on MFMA.
  * Replaces gemm::Kernel<T, Large> (gemm_kernel.hpp:25-143) launched by
- * gemm.cpp:243-246 / peak_l0.cpp:929-934. */
+ * gemm.cpp:243-246 / peak_l0.cpp:929-934, and the choice between its large
+ * and small tile (gemm.cpp:145): the block tile (256x256, 128x256 or
+ * 128x128) is the one with the least estimated time at this shape on this
+ * GPU's compute units (xpu_gemm_tile). */
 int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
              uint32_t M, uint32_t N, uint32_t K);
+
+/* The block tile xpu_gemm uses for an M x N output on this runtime's GPU:
+ * *rows x *cols. No device work. The reference's counterpart is the
+ * large_tile expression of gemm.cpp:145. */
+int xpu_gemm_tile(const xpu_runtime *rt, uint32_t M, uint32_t N, uint32_t *rows, uint32_t *cols);
 
 /* Size of the scratch array behind xpu_gemm_noalloc: 32 MiB per GPU. */
 #define XPU_GEMM_NOALLOC_SCRATCH_BYTES (32ull << 20)

@@ -1,0 +1,88 @@
+"""The GEMM's three block tiles (256x256; 128x256, the reference's small tile
+of gemm_kernel.hpp:26-27; 128x128) launched by name on the same shapes, each
+against the FP64 oracle at the GEMM bar, with 16-byte and 2-byte-offset C;
+and the tile xpu_gemm picks (gemm.cpp:145's choice, made here by compute-unit
+fill)."""
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+import xpu_playground_amd as xpu
+from test_gpu_gemm import check, gpu_gemm
+from xpu_playground_amd import Args
+
+pytestmark = pytest.mark.gpu
+
+TILES = {"": (256, 256), "_m128": (128, 256), "_t128": (128, 128)}
+GUARD = 0x7E7E
+
+
+def launch_tile(rt, tag, dtype, a, b, m, n, k, c_offset):
+    """One launch of a tile variant. The kernels read A and B in place, so K
+    and N are multiples of 8 here (xpu_gemm pads other shapes first); C
+    starts c_offset bytes past a 16-byte boundary (the _dmau stores for 2)."""
+    assert k % 8 == 0 and n % 8 == 0 and a.size == m * k and b.size == k * n
+    bm, bn = TILES[tag]
+    words = m * n + 32
+    da, db, dc = rt.upload(a), rt.upload(b), rt.alloc(words * 2)
+    try:
+        rt.copy_to(dc, np.full(words, GUARD, np.uint16))
+        name = f"xpu_gemm_{'fp16' if dtype else 'bf16'}{tag}_{'dmau' if c_offset else 'dma'}"
+        args = Args().ptr(da).ptr(db).ptr(dc + c_offset).u32(m).u32(n).u32(k).u32(k).u32(n).u32(n)
+        grid = ((m + bm - 1) // bm) * ((n + bn - 1) // bn)
+        print(f"{name} {m}x{n}x{k} grid {grid}", flush=True)
+        rt.launch_grid(name, grid, 256, 0, args)
+        rt.synchronize()
+        out = rt.download(dc, words, np.uint16)
+    finally:
+        for p in (da, db, dc):
+            rt.free(p)
+    off = c_offset // 2
+    assert np.all(out[:off] == GUARD) and np.all(out[off + m * n:] == GUARD), "store outside C"
+    return out[off:off + m * n].reshape(m, n)
+
+
+@pytest.mark.parametrize("tag", list(TILES))
+@pytest.mark.parametrize("dtype", [xpu.BF16, xpu.FP16])
+@pytest.mark.parametrize("c_offset", [0, 2])
+@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (255, 264, 72), (37, 56, 8), (300, 8, 16), (513, 392, 1032),
+                                   (1000, 600, 520)])
+def test_tile_variant(rt, tag, dtype, c_offset, m, n, k):
+    a = orc.uniform(m * k, 50 + m, dtype)
+    b = orc.uniform(k * n, 60 + n, dtype)
+    check(launch_tile(rt, tag, dtype, a, b, m, n, k, c_offset), a, b, m, n, k, dtype)
+
+
+def test_tiles_same_bits(rt):
+    # every tile runs the same k-order in each MFMA chain, so all three give
+    # the same output bits
+    m, n, k = 700, 520, 1000
+    a = orc.uniform(m * k, 71, xpu.BF16)
+    b = orc.uniform(k * n, 72, xpu.BF16)
+    outs = [launch_tile(rt, tag, xpu.BF16, a, b, m, n, k, 0) for tag in TILES]
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+def test_tile_choice(rt):
+    if rt.compute_units != 256:
+        pytest.skip("the expected choices are for MI355X's 256 compute units")
+    # configs[2] and configs[3] keep the large tile (it already gives every
+    # compute unit at most one block); outputs that leave most units idle
+    # with it take a small one
+    assert rt.gemm_tile(4096, 4096) == (256, 256)
+    assert rt.gemm_tile(3000, 4097) == (256, 256)
+    assert rt.gemm_tile(8192, 8192) == (256, 256)
+    assert rt.gemm_tile(2048, 4096) == (128, 256)
+    assert rt.gemm_tile(1000, 4097) == (128, 256)
+    assert rt.gemm_tile(2048, 2048) == (128, 128)
+    assert rt.gemm_tile(1024, 1024) == (128, 128)
+    assert rt.gemm_tile(1, 1) == (128, 128)
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 1024, 1024), (2048, 4096, 256), (1000, 4097, 520), (777, 1001, 300)])
+def test_small_tile_shapes_through_xpu_gemm(rt, m, n, k):
+    # aligned operands read in place, and padded copies with unaligned C
+    print(f"xpu_gemm {m}x{n}x{k} tile {rt.gemm_tile(m, n)}", flush=True)
+    a = orc.uniform(m * k, 80 + m, xpu.BF16)
+    b = orc.uniform(k * n, 90 + n, xpu.BF16)
+    check(gpu_gemm(rt, a, b, m, n, k, xpu.BF16), a, b, m, n, k, xpu.BF16)

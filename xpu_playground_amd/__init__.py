@@ -100,6 +100,7 @@ def _declare(lib):
     optional = {
         "xpu_gemm": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]),
         "xpu_gemm_noalloc": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]),
+        "xpu_gemm_tile": (c_int, [c_void_p, c_uint32, c_uint32, POINTER(c_uint32), POINTER(c_uint32)]),
         "xpu_qwen3_preset": (c_int, [c_char_p, POINTER(Qwen3Config)]),
         "xpu_qwen3_fill_tensor": (
             c_int,
@@ -339,6 +340,12 @@ class Runtime:
 
     def gemm(self, dtype: int, a: int, b: int, c: int, m: int, n: int, k: int) -> None:
         check(self.lib.xpu_gemm(self.handle, dtype, c_void_p(a), c_void_p(b), c_void_p(c), m, n, k))
+
+    def gemm_tile(self, m: int, n: int) -> tuple[int, int]:
+        """The block tile (rows, cols) that gemm() uses for an m x n output."""
+        rows, cols = ctypes.c_uint32(), ctypes.c_uint32()
+        check(self.lib.xpu_gemm_tile(self.handle, m, n, ctypes.byref(rows), ctypes.byref(cols)))
+        return rows.value, cols.value
 
     def fill_uniform(self, dtype: int, ptr: int, count: int, seed: int) -> None:
         check(self.lib.xpu_fill_uniform(self.handle, dtype, c_void_p(ptr), count, seed))

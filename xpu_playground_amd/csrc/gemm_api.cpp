@@ -47,6 +47,48 @@ int pad_rows2(xpu_runtime *rt, const void *src_a, uint64_t ld_a, uint32_t rows_a
   return rt->launch(*k, blocks_a + blocks_b, 1, 256, 0, args, 13);
 }
 
+// Block tiles of the MFMA kernels (kernels/gemm.hip), largest first. Rates
+// are FLOP per compute unit relative to the large tile, measured at shapes
+// where every compute unit is busy: a 128 x 256 block alone on a unit runs at
+// 0.85; a 128 x 128 block alone at 0.59, and two of them sharing a unit (its
+// LDS holds two) at 0.82 together.
+struct GemmTile {
+  const char *tag;  // kernel name part: xpu_gemm_<type><tag>_dma[u]
+  uint32_t rows, cols;
+  uint32_t per_cu;   // blocks one compute unit holds at once
+  double solo_rate;  // one block on a unit
+  double pair_rate;  // two blocks on a unit, together (per_cu == 2)
+};
+constexpr GemmTile kTiles[] = {{"", 256, 256, 1, 1.0, 0.0},
+                               {"_m128", 128, 256, 1, 0.85, 0.0},
+                               {"_t128", 128, 128, 2, 0.59, 0.82}};
+
+// The tile with the least estimated time. The blocks spread evenly over the
+// compute units, so the busiest unit gets w = ceil(tiles / CUs) of them and
+// runs them in pairs where it holds two. The larger tile wins ties. The
+// reference takes its small tile when M or N is below 2560 (gemm.cpp:145);
+// here the 256 x 256 tile stays wherever it already fills the chip (4096^3,
+// 3000 x 4097), and outputs that leave most compute units idle with it take
+// a smaller one.
+const GemmTile &choose_tile(uint32_t compute_units, uint32_t M, uint32_t n_cols) {
+  const GemmTile *best = &kTiles[0];
+  double best_cost = 0;
+  for (const GemmTile &t : kTiles) {
+    const uint64_t tiles = ((static_cast<uint64_t>(M) + t.rows - 1) / t.rows) *
+                           ((static_cast<uint64_t>(n_cols) + t.cols - 1) / t.cols);
+    const uint64_t w = (tiles + compute_units - 1) / std::max(1u, compute_units);
+    const double area = static_cast<double>(t.rows) * t.cols;
+    const double cost = t.per_cu == 2 ? static_cast<double>(w / 2) * 2.0 * area / t.pair_rate +
+                                            static_cast<double>(w % 2) * area / t.solo_rate
+                                      : static_cast<double>(w) * area / t.solo_rate;
+    if (&t == &kTiles[0] || cost < best_cost) {
+      best = &t;
+      best_cost = cost;
+    }
+  }
+  return *best;
+}
+
 }  // namespace
 
 namespace xpu {
@@ -93,10 +135,13 @@ int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, 
   const uint32_t k_run = static_cast<uint32_t>(a_direct ? K : kp);  // reduction length seen by the kernel
   const uint32_t n_run = static_cast<uint32_t>(b_direct ? N : np);  // columns of the B operand
   const bool c16 = reinterpret_cast<uintptr_t>(C) % 16 == 0 && N % 8 == 0;
-  const std::string name = std::string("xpu_gemm_") + (dtype ? "fp16" : "bf16") + (c16 ? "_dma" : "_dmau");
+  const GemmTile &tile = choose_tile(rt->compute_units, M, n_run);
+  const std::string name =
+      std::string("xpu_gemm_") + (dtype ? "fp16" : "bf16") + tile.tag + (c16 ? "_dma" : "_dmau");
   const xpu::KernelInfo *k = rt->find_exact(name);
   if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: " + name);
-  const uint64_t tiles = ((static_cast<uint64_t>(M) + 255) / 256) * ((static_cast<uint64_t>(n_run) + 255) / 256);
+  const uint64_t tiles = ((static_cast<uint64_t>(M) + tile.rows - 1) / tile.rows) *
+                         ((static_cast<uint64_t>(n_run) + tile.cols - 1) / tile.cols);
   if (tiles > 0x7fffffffu) return set_error(XPU_ERR_INVALID, "xpu_gemm: too many tiles");
   const uint32_t kb = K, ldc = N, n_out = N;
   const xpu_kernel_arg args[] = {{8, &a_use}, {8, &b_use}, {8, &C},   {4, &M},     {4, &n_run},
@@ -109,6 +154,15 @@ int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, 
 extern "C" int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
                         uint32_t M, uint32_t N, uint32_t K) {
   return xpu::gemm_run(rt, dtype, A, B, C, M, N, K, nullptr, 0);
+}
+
+extern "C" int xpu_gemm_tile(const xpu_runtime *rt, uint32_t M, uint32_t N, uint32_t *rows, uint32_t *cols) {
+  if (!rt || !rows || !cols) return set_error(XPU_ERR_INVALID, "xpu_gemm_tile: null argument");
+  if (M == 0 || N == 0) return set_error(XPU_ERR_INVALID, "xpu_gemm_tile: M and N must be positive");
+  const GemmTile &t = choose_tile(rt->compute_units, M, static_cast<uint32_t>(round_up8(N)));
+  *rows = t.rows;
+  *cols = t.cols;
+  return XPU_OK;
 }
 
 namespace {

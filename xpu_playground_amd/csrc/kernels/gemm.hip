@@ -3,10 +3,13 @@
 // gemm_kernel.hpp:25-143, argument order (a, b, c, m, n, k) of
 // level_zero/gem_spv_entry.cpp:28-60).
 //
-// Block tile 256 x 256, K-slice BK (64 or 32), S LDS stages, 256 threads:
-// four wavefronts in a 2 x 2 arrangement, each owning 128 x 128 of C as
-// 4 x 4 tiles of v_mfma_f32_32x32x16_{bf16,f16} (256 FP32 accumulators per
-// lane).
+// Block tile (64 MI) x (64 NJ), K-slice BK (64 or 32), S LDS stages, 256
+// threads: four wavefronts in a 2 x 2 arrangement, each owning 32 MI x 32 NJ
+// of C as MI x NJ tiles of v_mfma_f32_32x32x16_{bf16,f16}. The large tile is
+// 256 x 256 (MI = NJ = 4, 256 FP32 accumulators per lane). The small tiles,
+// 128 x 256 (the reference's small tile, gemm_kernel.hpp:26-27) and
+// 128 x 128, cut shapes that fill few compute units with the large tile
+// into more blocks; the host picks the tile by compute-unit fill.
 //
 // Operands go from global memory straight into LDS with buffer_load_dwordx4
 // ... lds (the LDS-DMA form: lane t's 16 bytes land at M0 + 16 t), so no
@@ -48,7 +51,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-constexpr uint32_t kBM = 256;
 constexpr uint32_t kOob = 0x80000000u;  // any offset >= the descriptor range reads 0
 
 template <int DT>
@@ -102,41 +104,45 @@ template <int DT> XPU_DEVICE uint32_t cvt_pack(float lo, float hi) {
            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
 }
 
-// NJ: 32 x 32 MFMA tiles per wavefront along N (wavefront tile 128 x 32 NJ,
-// block tile 256 x 64 NJ); BK: K-slice; S: LDS stages.
-template <int NJ, int BK, int S> struct Cfg {
+// MI, NJ: 32 x 32 MFMA tiles per wavefront along M and N (wavefront tile
+// 32 MI x 32 NJ, block tile 64 MI x 64 NJ); BK: K-slice; S: LDS stages.
+template <int MI, int NJ, int BK, int S> struct Cfg {
+  static constexpr uint32_t kBMW = 32u * MI;                 // rows per wavefront
+  static constexpr uint32_t kBM = 2u * kBMW;                 // block tile rows
   static constexpr uint32_t kBNW = 32u * NJ;                 // columns per wavefront
   static constexpr uint32_t kBN = 2u * kBNW;                 // block tile columns
   static constexpr uint32_t kKs = BK / 16;                   // k-steps per slice
-  static constexpr uint32_t kABytes = 512u * BK;             // 256 rows x 2 BK bytes
+  static constexpr uint32_t kABytes = kBM * 2u * BK;         // kBM rows x 2 BK bytes
   static constexpr uint32_t kBRow = 2u * kBN;                // bytes per B row in LDS
   static constexpr uint32_t kStage = kABytes + BK * kBRow;   // A then B
   static constexpr uint32_t kCpr = BK / 8;                   // 16-byte chunks per A row
   static constexpr uint32_t kRpi = 64 / kCpr;                // A rows per DMA instruction
   static constexpr uint32_t kBCpr = kBN / 8;                 // 16-byte chunks per B row
   static constexpr uint32_t kBRpi = 64 / kBCpr;              // B rows per DMA instruction
-  static constexpr uint32_t kDmaA = 256 / kRpi / 4;          // A DMA instructions per wave per slice
+  static constexpr uint32_t kDmaA = kBM / kRpi / 4;          // A DMA instructions per wave per slice
   static constexpr uint32_t kDmaB = BK / kBRpi / 4;          // B DMA instructions per wave per slice
   static constexpr uint32_t kDma = kDmaA + kDmaB;
-  static constexpr uint32_t kMf = 4u * NJ;                   // MFMAs per k-step
-  static constexpr uint32_t kReads = 4u + 2u * NJ;           // fragment reads per k-step
+  static constexpr uint32_t kMf = MI * NJ;                   // MFMAs per k-step
+  static constexpr uint32_t kReads = MI + 2u * NJ;           // fragment reads per k-step
   static constexpr uint32_t kEpPitch = kBNW + 4;             // epilogue staging pitch (floats)
   static constexpr uint32_t kEpBytes = 4u * 64u * kEpPitch * 4u;
   static constexpr uint32_t kLds = S * kStage > kEpBytes ? S * kStage : kEpBytes;
   static_assert(kLds <= 160u * 1024u, "LDS");
   static_assert(kBCpr == 16 || kBCpr == 32, "B rows of 16 or 32 chunks (the swizzle permutes 16)");
+  static_assert(MI == 2 || MI == 4, "64-row epilogue bands");
+  static_assert(kDmaA >= 1, "every wave issues A DMA");
 };
 
-template <int DT, int NJ, int BK, int S, int P, int D, bool C16>
+template <int DT, int MI, int NJ, int BK, int S, int P, int D, bool C16>
 XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
                      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {
-  using G = Cfg<NJ, BK, S>;
+  using G = Cfg<MI, NJ, BK, S>;
   __shared__ __align__(1024) uint8_t lds[G::kLds];
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + G::kBN - 1) / G::kBN;
+  const uint32_t tiles_m = (M + G::kBM - 1) / G::kBM, tiles_n = (N + G::kBN - 1) / G::kBN;
   const TileCoord tc = tile_of_block(blockIdx.x, tiles_m, tiles_n);
-  const uint32_t m0 = tc.tm * kBM, n0 = tc.tn * G::kBN;
+  const uint32_t m0 = tc.tm * G::kBM, n0 = tc.tn * G::kBN;
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
 
   // DMA lane maps. A: instruction i of this wave fills tile rows
@@ -178,7 +184,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
             b_voff + (op - G::kDmaA) * b_istride);
   };
 
-  // Fragment addresses (bytes within a stage). A: row wm*128 + 32 i + l%32,
+  // Fragment addresses (bytes within a stage). A: row wm*kBMW + 32 i + l%32,
   // logical chunk 2 ks + l/32. B: k-row 16 ks + 8 (l/32) + 4 h + (l%16)/4,
   // column wn*kBNW + 32 j + 16 ((l/16) % 2) + 4 (l % 4): the 4-element row
   // that lane l contributes to its group's transposing read.
@@ -196,7 +202,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     for (uint32_t g = 0; g < kGroups; ++g) {
 #pragma unroll
       for (uint32_t ks = 0; ks < G::kKs; ++ks) {
-        fa_base[g][ks] = lds0 + g * 65536u + (wm * 128u + (lane & 31u)) * (2u * BK) +
+        fa_base[g][ks] = lds0 + g * 65536u + (wm * G::kBMW + (lane & 31u)) * (2u * BK) +
                          16u * ((2u * ks + (lane >> 5)) ^ a_swz<BK>(lane & 15u));
         asm volatile("" : "+v"(fa_base[g][ks]));
       }
@@ -210,11 +216,11 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   }
 
   struct Frags {
-    u32x4 a[4], b[NJ];
+    u32x4 a[MI], b[NJ];
   };
   // Read r (0 .. kReads-1) of the fragments of k-step ks in a stage, in the
-  // order the MFMAs consume them: A0, B0 .. B(NJ-1) (two halves each), A1,
-  // A2, A3.
+  // order the MFMAs consume them: A0, B0 .. B(NJ-1) (two halves each), A1 ..
+  // A(MI-1).
   auto read = [&](uint32_t stage, uint32_t ks, Frags &f, uint32_t r) {
     const uint32_t g = stage * G::kStage / 65536u, in_group = stage * G::kStage % 65536u;
     if (r == 0 || r > 2u * NJ) {
@@ -235,9 +241,9 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     }
   };
 
-  f32x16 acc[4][NJ];
+  f32x16 acc[MI][NJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
@@ -252,7 +258,19 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 
   const uint32_t nk = (K + BK - 1) / BK;
   static_assert(D >= 1 && D <= G::kKs, "a slice's DMA is issued within the k-steps before the next barrier");
-  static_assert(P <= G::kMf && G::kReads <= G::kMf, "k-step schedule");
+  static_assert(P < G::kMf, "k-step schedule: MFMAs after the barrier carry the next slice's first reads");
+  // fragment reads of the next k-step issued after MFMA q of an ordinary
+  // k-step: one after each of the first kReads MFMAs, or spread evenly when
+  // there are more reads than MFMAs
+  auto reads_after = [](uint32_t q, uint32_t &lo, uint32_t &hi) {
+    if constexpr (G::kReads <= G::kMf) {
+      lo = q;
+      hi = q < G::kReads ? q + 1 : q;
+    } else {
+      lo = q * G::kReads / G::kMf;
+      hi = (q + 1) * G::kReads / G::kMf;
+    }
+  };
   // DMA ops of one slice issued during the e-th k-step after its barrier
   auto dma_part = [&](const Slice &d, uint32_t e, uint32_t x, uint32_t nx) {
     const uint32_t lo = e * G::kDma / D, hi = (e + 1) * G::kDma / D;
@@ -296,7 +314,10 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 #pragma unroll
           for (uint32_t q = 0; q < G::kMf; ++q) {
             mfma_q(frag[cur], q);
-            if (q < G::kReads) read(st, ks + 1, frag[cur ^ 1], q);
+            uint32_t lo, hi;
+            reads_after(q, lo, hi);
+#pragma unroll
+            for (uint32_t r = lo; r < hi; ++r) read(st, ks + 1, frag[cur ^ 1], r);
             if (e < D) dma_part(pend, e, q, G::kMf);
             __builtin_amdgcn_sched_barrier(0);
           }
@@ -330,7 +351,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   wait_vmcnt<0>();
   __syncthreads();
 
-  // Epilogue through LDS, one 64-row band per round: each wave writes its
+  // Epilogue through LDS, one 64-row band per round (MI / 2 rounds): each wave writes its
   // 64 x kBNW FP32 band (D layout of v_mfma_f32_32x32x16 with C^T tiles: lane
   // l holds row l % 32, columns 8 g + 4 (l / 32) + 0..3 in accumulators
   // 4 g..4 g + 3) as 16-byte rows into its own region (pitch kBNW + 4
@@ -343,7 +364,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   const uint32_t m_lane = lane & 31u, n_lane = (lane >> 5) * 4u;
   const uint32_t r_lane = lane / kLpr, c_lane = (lane % kLpr) * 8u;
 #pragma unroll
-  for (int band = 0; band < 2; ++band) {
+  for (int band = 0; band < MI / 2; ++band) {
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
@@ -362,7 +383,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
       const uint32_t r = rr * kRpr + r_lane;
       const f32x4 lo = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane);
       const f32x4 hi = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane + 4u);
-      const uint32_t m = m0 + wm * 128u + band * 64u + r, n = n0 + wn * G::kBNW + c_lane;
+      const uint32_t m = m0 + wm * G::kBMW + band * 64u + r, n = n0 + wn * G::kBNW + c_lane;
       if (m >= M || n >= n_out) continue;
       const u32x4 packed{cvt_pack<DT>(lo.x, lo.y), cvt_pack<DT>(lo.z, lo.w), cvt_pack<DT>(hi.x, hi.y),
                          cvt_pack<DT>(hi.z, hi.w)};
@@ -399,20 +420,32 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 }  // namespace dma
 }  // namespace xpu
 
-#define XPU_GEMM_DMA_VARIANT(NAME, DT, NJ, BK, S, P, D, MINB, C16)                            \
+#define XPU_GEMM_DMA_VARIANT(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16)                        \
   extern "C" __global__ __launch_bounds__(256, MINB) void NAME(                               \
       const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C, \
       uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {         \
     XPU_STAMP(xpu::kStampGemm);                                                                 \
-    xpu::dma::body<DT, NJ, BK, S, P, D, C16>(A, B, C, M, N, K, kb, ldc, n_out);                \
+    xpu::dma::body<DT, MI, NJ, BK, S, P, D, C16>(A, B, C, M, N, K, kb, ldc, n_out);            \
   }
 
-// BK = 64, two stages, barrier after 4 MFMAs of a slice's last k-step, each
-// slice's DMA spread over two k-steps
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dma, xpu::kBf16, 4, 64, 2, 4, 2, 1, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dma, xpu::kFp16, 4, 64, 2, 4, 2, 1, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dmau, xpu::kBf16, 4, 64, 2, 4, 2, 1, false)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dmau, xpu::kFp16, 4, 64, 2, 4, 2, 1, false)
+// 256 x 256: BK = 64, two stages, barrier after 4 MFMAs of a slice's last
+// k-step, each slice's DMA spread over two k-steps
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dma, xpu::kBf16, 4, 4, 64, 2, 4, 2, 1, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dma, xpu::kFp16, 4, 4, 64, 2, 4, 2, 1, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dmau, xpu::kBf16, 4, 4, 64, 2, 4, 2, 1, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dmau, xpu::kFp16, 4, 4, 64, 2, 4, 2, 1, false)
+// 128 x 256 (one block per compute unit: 96 KiB of stages, 132 KiB of
+// epilogue staging)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_m128_dma, xpu::kBf16, 2, 4, 64, 2, 4, 2, 1, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_m128_dma, xpu::kFp16, 2, 4, 64, 2, 4, 2, 1, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_m128_dmau, xpu::kBf16, 2, 4, 64, 2, 4, 2, 1, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_m128_dmau, xpu::kFp16, 2, 4, 64, 2, 4, 2, 1, false)
+// 128 x 128 (two blocks per compute unit: 64 KiB of stages, 68 KiB of
+// epilogue staging); the barrier after 2 of the k-step's 4 MFMAs
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_t128_dma, xpu::kBf16, 2, 2, 64, 2, 2, 2, 2, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_t128_dma, xpu::kFp16, 2, 2, 64, 2, 2, 2, 2, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_t128_dmau, xpu::kBf16, 2, 2, 64, 2, 2, 2, 2, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_t128_dmau, xpu::kFp16, 2, 2, 64, 2, 2, 2, 2, false)
 
 // dst[r][c] = src[r * src_ld + c] for c < cols, 0 for cols <= c < dst_cols
 // (dst_cols % 8 == 0, dst 16-byte aligned): the zero padding of the
