@@ -38,7 +38,7 @@
 // B 16-byte aligned; the host pads other shapes into a workspace first
 // (xpu_pad_rows below, the device counterpart of the reference's host
 // padding, gemm.cpp:75-85). Stores are masked to M x n_out; the _dmau
-// variants store C element by element (C rows not 16-byte aligned).
+// variants take C rows that are only 2-byte aligned.
 #include "device_common.hpp"
 
 namespace xpu {
@@ -384,31 +384,26 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
       const f32x4 lo = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane);
       const f32x4 hi = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane + 4u);
       const uint32_t m = m0 + wm * G::kBMW + band * 64u + r, n = n0 + wn * G::kBNW + c_lane;
-      if (m >= M || n >= n_out) continue;
+      if (m >= M || n + 8u > n_out) continue;  // whole 16-byte chunks; the edge chunk below
       const u32x4 packed{cvt_pack<DT>(lo.x, lo.y), cvt_pack<DT>(lo.z, lo.w), cvt_pack<DT>(hi.x, hi.y),
                          cvt_pack<DT>(hi.z, hi.w)};
       uint16_t *dst = C + static_cast<uint64_t>(m) * ldc + n;
-      if constexpr (C16) {
-        *reinterpret_cast<u32x4 *>(dst) = packed;  // n_out % 8 == 0: n + 7 < n_out
-      } else {
-        const uint32_t w[4] = {packed.x, packed.y, packed.z, packed.w};
-        if (n + 8u <= n_out && (reinterpret_cast<uintptr_t>(dst) & 3u) == 0) {
-          // 4-byte aligned: four dword stores
-          uint32_t *d32 = reinterpret_cast<uint32_t *>(dst);
+      if constexpr (C16)
+        *reinterpret_cast<u32x4 *>(dst) = packed;
+      else  // C rows 2-byte aligned: global memory runs in unaligned access mode on gfx950
+        __builtin_memcpy(dst, &packed, 16);
+    }
+    if constexpr (!C16) {
+      // The partial chunk at C's right edge (n_out % 8 columns), once per
+      // band by the wave whose columns hold it: lane = row of the band.
+      const uint32_t nb = n0 + wn * G::kBNW, edge = n_out & ~7u, cnt = n_out & 7u;
+      const uint32_t m = m0 + wm * G::kBMW + band * 64u + lane;
+      if (cnt != 0 && edge >= nb && edge < nb + G::kBNW && m < M) {
+        const float *src = ep + lane * kEpPitch + (edge - nb);
+        uint16_t *dst = C + static_cast<uint64_t>(m) * ldc + edge;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) d32[i] = w[i];
-        } else if (n + 8u <= n_out) {
-          // 2 bytes past a 4-byte boundary: element 0, three dwords, element 7
-          dst[0] = static_cast<uint16_t>(w[0]);
-          uint32_t *d32 = reinterpret_cast<uint32_t *>(dst + 1);
-#pragma unroll
-          for (int i = 0; i < 3; ++i) d32[i] = (w[i] >> 16) | (w[i + 1] << 16);
-          dst[7] = static_cast<uint16_t>(w[3] >> 16);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (n + e < n_out) dst[e] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
-        }
+        for (uint32_t e = 0; e < 7; ++e)
+          if (e < cnt) dst[e] = static_cast<uint16_t>(cvt_pack<DT>(src[e], 0.0f));
       }
     }
     __builtin_amdgcn_wave_barrier();
