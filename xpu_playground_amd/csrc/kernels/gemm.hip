@@ -446,20 +446,17 @@ XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_t128_dmau, xpu::kFp16, 2, 2, 64, 2, 2, 2, 2, 
 // (dst_cols % 8 == 0, dst 16-byte aligned): the zero padding of the
 // reference's host GEMM setup (gemm.cpp:75-85) done on the device, so rows
 // of the copy are 16-byte aligned. One thread per 8 destination elements.
-// src only needs 2-byte alignment: a chunk that starts on a 4-byte boundary
-// is one 16-byte load; one that starts 2 bytes past it is the 16-byte load
-// one element earlier plus the chunk's last element, shifted into place.
-// The chunk holding the row's end is read element by element, so no load
-// reaches past the last element of a row.
+// src only needs 2-byte alignment: a whole chunk is one 16-byte load at a
+// 2-byte aligned address (global memory runs in unaligned access mode on
+// gfx950). The chunk holding the row's end is read element by element, so
+// no load reaches past the last element of a row.
 namespace xpu {
 // One 16-byte destination chunk (8 elements from column c0 of src row p).
 XPU_DEVICE xpu::u32x4 pad_chunk(const uint16_t *__restrict__ p, uint32_t c0, uint32_t cols) {
   if (c0 + 8u <= cols) {
-    if ((reinterpret_cast<uintptr_t>(p) & 3u) == 0) return *reinterpret_cast<const xpu::u32x4 *>(p);
-    const xpu::u32x4 d = *reinterpret_cast<const xpu::u32x4 *>(p - 1);  // elements -1..6
-    const uint32_t last = p[7];
-    return xpu::u32x4{__builtin_amdgcn_alignbit(d.y, d.x, 16), __builtin_amdgcn_alignbit(d.z, d.y, 16),
-                      __builtin_amdgcn_alignbit(d.w, d.z, 16), __builtin_amdgcn_alignbit(last, d.w, 16)};
+    xpu::u32x4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
   }
   uint32_t w[4];
 #pragma unroll
