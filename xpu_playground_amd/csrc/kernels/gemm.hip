@@ -95,13 +95,16 @@ XPU_DEVICE TileCoord tile_of_block(uint32_t b, uint32_t tiles_m, uint32_t tiles_
   return {first_m + in_group % rows, in_group / rows};
 }
 
+// Two FP32 values to two RNE-rounded 16-bit codes in one register (lo in
+// bits 0-15): one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 template <int DT> XPU_DEVICE uint32_t cvt_pack(float lo, float hi) {
   if constexpr (DT == kFp16)
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
   else
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(lo))) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 // MI, NJ: 32 x 32 MFMA tiles per wavefront along M and N (wavefront tile
@@ -378,20 +381,35 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // Rows of the band in batches of kBatch read-back rows: every LDS read of
+    // a batch is issued before the first conversion. Bands inside M x n_out
+    // skip the per-row bounds checks.
+    constexpr uint32_t kIter = 64u / kRpr, kBatch = 4;
+    const uint32_t mb = m0 + wm * G::kBMW + band * 64u, nb0 = n0 + wn * G::kBNW;
+    const bool inside = mb + 64u <= M && nb0 + G::kBNW <= n_out;
 #pragma unroll
-    for (uint32_t rr = 0; rr < 64u / kRpr; ++rr) {
-      const uint32_t r = rr * kRpr + r_lane;
-      const f32x4 lo = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane);
-      const f32x4 hi = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane + 4u);
-      const uint32_t m = m0 + wm * G::kBMW + band * 64u + r, n = n0 + wn * G::kBNW + c_lane;
-      if (m >= M || n + 8u > n_out) continue;  // whole 16-byte chunks; the edge chunk below
-      const u32x4 packed{cvt_pack<DT>(lo.x, lo.y), cvt_pack<DT>(lo.z, lo.w), cvt_pack<DT>(hi.x, hi.y),
-                         cvt_pack<DT>(hi.z, hi.w)};
-      uint16_t *dst = C + static_cast<uint64_t>(m) * ldc + n;
-      if constexpr (C16)
-        *reinterpret_cast<u32x4 *>(dst) = packed;
-      else  // C rows 2-byte aligned: global memory runs in unaligned access mode on gfx950
-        __builtin_memcpy(dst, &packed, 16);
+    for (uint32_t rr0 = 0; rr0 < kIter; rr0 += kBatch) {
+      f32x4 lo[kBatch], hi[kBatch];
+#pragma unroll
+      for (uint32_t b = 0; b < kBatch; ++b) {
+        const uint32_t r = (rr0 + b) * kRpr + r_lane;
+        lo[b] = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane);
+        hi[b] = *reinterpret_cast<const f32x4 *>(ep + r * kEpPitch + c_lane + 4u);
+      }
+#pragma unroll
+      for (uint32_t b = 0; b < kBatch; ++b) {
+        const uint32_t r = (rr0 + b) * kRpr + r_lane;
+        const uint32_t m = mb + r, n = nb0 + c_lane;
+        // whole 16-byte chunks; the edge chunk below
+        if (!inside && (m >= M || n + 8u > n_out)) continue;
+        const u32x4 packed{cvt_pack<DT>(lo[b].x, lo[b].y), cvt_pack<DT>(lo[b].z, lo[b].w),
+                           cvt_pack<DT>(hi[b].x, hi[b].y), cvt_pack<DT>(hi[b].z, hi[b].w)};
+        uint16_t *dst = C + static_cast<uint64_t>(m) * ldc + n;
+        if constexpr (C16)
+          *reinterpret_cast<u32x4 *>(dst) = packed;
+        else  // C rows 2-byte aligned: global memory runs in unaligned access mode on gfx950
+          __builtin_memcpy(dst, &packed, 16);
+      }
     }
     if constexpr (!C16) {
       // The partial chunk at C's right edge (n_out % 8 columns), once per
