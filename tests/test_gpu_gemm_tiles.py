@@ -1,8 +1,8 @@
-"""The GEMM's three block tiles (256x256; 128x256, the reference's small tile
-of gemm_kernel.hpp:26-27; 128x128) launched by name on the same shapes, each
-against the FP64 oracle at the GEMM bar, with 16-byte and 2-byte-offset C;
-and the tile xpu_gemm picks (gemm.cpp:145's choice, made here by compute-unit
-fill)."""
+"""The GEMM's block tiles (256x256, also in its odd-slice-count form;
+128x256, the reference's small tile of gemm_kernel.hpp:26-27; 128x128)
+launched by name on the same shapes, each against the FP64 oracle at the GEMM
+bar, with 16-byte and 2-byte-offset C; and the tile xpu_gemm picks
+(gemm.cpp:145's choice, made here by compute-unit fill)."""
 import numpy as np
 import pytest
 
@@ -13,7 +13,14 @@ from xpu_playground_amd import Args
 
 pytestmark = pytest.mark.gpu
 
-TILES = {"": (256, 256), "_m128": (128, 256), "_t128": (128, 128)}
+# "_odd": the 256x256 kernel for an odd number (3 or more) of 64-deep
+# K-slices (the last slice on its own after the pairs, only its k-steps below
+# K); launched only on such K, as xpu_gemm does
+TILES = {"": (256, 256), "_odd": (256, 256), "_m128": (128, 256), "_t128": (128, 128)}
+
+
+def slices(k):
+    return (k + 63) // 64
 GUARD = 0x7E7E
 
 
@@ -46,8 +53,10 @@ def launch_tile(rt, tag, dtype, a, b, m, n, k, c_offset):
 @pytest.mark.parametrize("dtype", [xpu.BF16, xpu.FP16])
 @pytest.mark.parametrize("c_offset", [0, 2])
 @pytest.mark.parametrize("m,n,k", [(128, 128, 64), (255, 264, 72), (37, 56, 8), (300, 8, 16), (513, 392, 1032),
-                                   (1000, 600, 520)])
+                                   (1000, 600, 520), (255, 264, 136), (300, 8, 184), (64, 520, 1056)])
 def test_tile_variant(rt, tag, dtype, c_offset, m, n, k):
+    if tag == "_odd" and (slices(k) % 2 == 0 or slices(k) < 3):
+        pytest.skip("the odd form takes an odd slice count of 3 or more")
     a = orc.uniform(m * k, 50 + m, dtype)
     b = orc.uniform(k * n, 60 + n, dtype)
     check(launch_tile(rt, tag, dtype, a, b, m, n, k, c_offset), a, b, m, n, k, dtype)
@@ -56,11 +65,11 @@ def test_tile_variant(rt, tag, dtype, c_offset, m, n, k):
 def test_tiles_same_bits(rt):
     # every tile runs the same k-order in each MFMA chain, so all three give
     # the same output bits
-    m, n, k = 700, 520, 1000
+    m, n, k = 700, 520, 1064  # 17 slices, 3 live k-steps in the last
     a = orc.uniform(m * k, 71, xpu.BF16)
     b = orc.uniform(k * n, 72, xpu.BF16)
     outs = [launch_tile(rt, tag, xpu.BF16, a, b, m, n, k, 0) for tag in TILES]
-    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
 
 
 def test_tile_choice(rt):

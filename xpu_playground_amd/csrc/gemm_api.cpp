@@ -136,8 +136,13 @@ int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, 
   const uint32_t n_run = static_cast<uint32_t>(b_direct ? N : np);  // columns of the B operand
   const bool c16 = reinterpret_cast<uintptr_t>(C) % 16 == 0 && N % 8 == 0;
   const GemmTile &tile = choose_tile(rt->compute_units, M, n_run);
-  const std::string name =
-      std::string("xpu_gemm_") + (dtype ? "fp16" : "bf16") + tile.tag + (c16 ? "_dma" : "_dmau");
+  // the 256 x 256 kernels come in a form for an odd number (3 or more) of
+  // 64-deep K-slices, which skips the slice of zeros that closes the last
+  // pair and the last slice's k-steps past K
+  const uint32_t slices = (k_run + 63) / 64;
+  const bool odd = tile.tag[0] == '\0' && slices % 2 == 1 && slices >= 3;
+  const std::string name = std::string("xpu_gemm_") + (dtype ? "fp16" : "bf16") + tile.tag + (odd ? "_odd" : "") +
+                           (c16 ? "_dma" : "_dmau");
   const xpu::KernelInfo *k = rt->find_exact(name);
   if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: " + name);
   const uint64_t tiles = ((static_cast<uint64_t>(M) + tile.rows - 1) / tile.rows) *

@@ -41,6 +41,8 @@
 // variants take C rows that are only 2-byte aligned.
 #include "device_common.hpp"
 
+#include <type_traits>
+
 namespace xpu {
 namespace dma {
 
@@ -136,7 +138,12 @@ template <int MI, int NJ, int BK, int S> struct Cfg {
   static_assert(kDmaA >= 1, "every wave issues A DMA");
 };
 
-template <int DT, int MI, int NJ, int BK, int S, int P, int D, bool C16>
+// ODD: the slice count nk is odd and at least 3 (the host's choice; other
+// counts would sum a slice twice); the last slice runs on its own after the
+// pairs, and only its k-steps that start below K (otherwise the last pair's
+// second slice would add a slice of zeros, and a slice that ends past K its
+// dead k-steps).
+template <int DT, int MI, int NJ, int BK, int S, int P, int D, bool C16, bool ODD>
 XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
                      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {
   using G = Cfg<MI, NJ, BK, S>;
@@ -281,18 +288,18 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     for (uint32_t op = lo + x * (hi - lo) / nx; op < lo + (x + 1) * (hi - lo) / nx; ++op) dma(d, op);
   };
   Frags frag[2];
-  // Prologue: slices 0 .. S-2 whole, and the first part of slice S-1 as if
-  // its barrier had just passed; the rest of slice S-1 follows during slice
-  // 0 like any slice's DMA.
-#pragma unroll
-  for (uint32_t p = 0; p + 1 < S; ++p) {
-    const Slice d = slice_of(p, p);
+  static_assert(S == 2, "pairs of slices");
+  // Slice s lives in LDS stage s % 2. Prologue: slice 0 whole, and the first
+  // part of slice 1 as if its barrier had just passed; the rest of slice 1
+  // follows during slice 0 like any slice's DMA.
+  {
+    const Slice d = slice_of(0, 0);
 #pragma unroll
     for (uint32_t op = 0; op < G::kDma; ++op) dma(d, op);
   }
-  Slice pend = slice_of(S - 1, S - 1);
+  Slice pend = slice_of(1, 1);
   dma_part(pend, 0, 0, 1);
-  wait_vmcnt<(S - 2) * G::kDma + G::kDma / D>();
+  wait_vmcnt<G::kDma / D>();
   __syncthreads();
 #pragma unroll
   for (uint32_t r = 0; r < G::kReads; ++r) read(0, 0, frag[0], r);
@@ -304,11 +311,9 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   // barrier, then the remaining MFMAs with the next slice's first fragment
   // reads and the first share of the new slice's DMA (the DMA of a slice is
   // spread over the D k-steps from its barrier on).
-  // Whole groups of S slices (one exit keeps the accumulators in place);
-  // slices past nk read zeros and add nothing.
-  for (uint32_t s0 = 0; s0 < nk; s0 += S) {
-#pragma unroll
-    for (uint32_t st = 0; st < S; ++st) {
+  // One slice: s0 + st, in stage st (st a compile-time constant).
+  auto slice_step = [&](auto stc, uint32_t s0) {
+    constexpr uint32_t st = decltype(stc)::value;
 #pragma unroll
       for (uint32_t ks = 0; ks < G::kKs; ++ks) {
         const int cur = (st * G::kKs + ks) & 1;
@@ -345,6 +350,41 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
               read((st + 1) % S, 0, frag[cur ^ 1], r);
             __builtin_amdgcn_sched_barrier(0);
           }
+        }
+      }
+  };
+  // Whole pairs of slices (one exit keeps the accumulators in place); a
+  // pair's second slice past nk reads zeros and adds nothing. With ODD the
+  // pairs stop before the last slice, which follows on its own (stage 0, its
+  // DMA and barrier already done by the last pair): the MFMAs of its k-steps
+  // that start below K, with the next k-step's fragment reads.
+  using St0 = std::integral_constant<uint32_t, 0>;
+  using St1 = std::integral_constant<uint32_t, 1>;
+  // (at least one pair: ODD kernels take nk >= 3)
+  uint32_t s0 = 0;
+  do {
+    slice_step(St0{}, s0);
+    slice_step(St1{}, s0);
+    s0 += S;
+  } while (s0 < (ODD ? nk - 1 : nk));
+  if constexpr (ODD) {
+    const uint32_t live = (K - (nk - 1) * BK + 15) / 16;  // 1 .. kKs
+    // k-steps past the live ones are skipped by a uniform branch; the reads
+    // of k-step ks + 1 only where it is live
+#pragma unroll
+    for (uint32_t ks = 0; ks < G::kKs; ++ks) {
+      if (ks == 0 || ks < live) {
+        const int cur = ks & 1;
+#pragma unroll
+        for (uint32_t q = 0; q < G::kMf; ++q) {
+          mfma_q(frag[cur], q);
+          uint32_t lo, hi;
+          reads_after(q, lo, hi);
+          if (ks + 1 < G::kKs && ks + 1 < live) {
+#pragma unroll
+            for (uint32_t r = lo; r < hi; ++r) read(0, ks + 1, frag[cur ^ 1], r);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
@@ -433,32 +473,37 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 }  // namespace dma
 }  // namespace xpu
 
-#define XPU_GEMM_DMA_VARIANT(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16)                        \
+#define XPU_GEMM_DMA_VARIANT(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD)                   \
   extern "C" __global__ __launch_bounds__(256, MINB) void NAME(                               \
       const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C, \
       uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {         \
     XPU_STAMP(xpu::kStampGemm);                                                                 \
-    xpu::dma::body<DT, MI, NJ, BK, S, P, D, C16>(A, B, C, M, N, K, kb, ldc, n_out);            \
+    xpu::dma::body<DT, MI, NJ, BK, S, P, D, C16, ODD>(A, B, C, M, N, K, kb, ldc, n_out);       \
   }
 
 // 256 x 256: BK = 64, two stages, barrier after 4 MFMAs of a slice's last
-// k-step, each slice's DMA spread over two k-steps
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dma, xpu::kBf16, 4, 4, 64, 2, 4, 2, 1, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dma, xpu::kFp16, 4, 4, 64, 2, 4, 2, 1, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dmau, xpu::kBf16, 4, 4, 64, 2, 4, 2, 1, false)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dmau, xpu::kFp16, 4, 4, 64, 2, 4, 2, 1, false)
+// k-step, each slice's DMA spread over two k-steps; _odd for an odd number
+// of 64-deep slices
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dma, xpu::kBf16, 4, 4, 64, 2, 4, 2, 1, true, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dma, xpu::kFp16, 4, 4, 64, 2, 4, 2, 1, true, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_dmau, xpu::kBf16, 4, 4, 64, 2, 4, 2, 1, false, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_dmau, xpu::kFp16, 4, 4, 64, 2, 4, 2, 1, false, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_odd_dma, xpu::kBf16, 4, 4, 64, 2, 4, 2, 1, true, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_odd_dma, xpu::kFp16, 4, 4, 64, 2, 4, 2, 1, true, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_odd_dmau, xpu::kBf16, 4, 4, 64, 2, 4, 2, 1, false, true)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_odd_dmau, xpu::kFp16, 4, 4, 64, 2, 4, 2, 1, false, true)
 // 128 x 256 (one block per compute unit: 96 KiB of stages, 132 KiB of
 // epilogue staging)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_m128_dma, xpu::kBf16, 2, 4, 64, 2, 4, 2, 1, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_m128_dma, xpu::kFp16, 2, 4, 64, 2, 4, 2, 1, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_m128_dmau, xpu::kBf16, 2, 4, 64, 2, 4, 2, 1, false)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_m128_dmau, xpu::kFp16, 2, 4, 64, 2, 4, 2, 1, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_m128_dma, xpu::kBf16, 2, 4, 64, 2, 4, 2, 1, true, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_m128_dma, xpu::kFp16, 2, 4, 64, 2, 4, 2, 1, true, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_m128_dmau, xpu::kBf16, 2, 4, 64, 2, 4, 2, 1, false, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_m128_dmau, xpu::kFp16, 2, 4, 64, 2, 4, 2, 1, false, false)
 // 128 x 128 (two blocks per compute unit: 64 KiB of stages, 68 KiB of
 // epilogue staging); the barrier after 2 of the k-step's 4 MFMAs
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_t128_dma, xpu::kBf16, 2, 2, 64, 2, 2, 2, 2, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_t128_dma, xpu::kFp16, 2, 2, 64, 2, 2, 2, 2, true)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_t128_dmau, xpu::kBf16, 2, 2, 64, 2, 2, 2, 2, false)
-XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_t128_dmau, xpu::kFp16, 2, 2, 64, 2, 2, 2, 2, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_t128_dma, xpu::kBf16, 2, 2, 64, 2, 2, 2, 2, true, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_t128_dma, xpu::kFp16, 2, 2, 64, 2, 2, 2, 2, true, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_t128_dmau, xpu::kBf16, 2, 2, 64, 2, 2, 2, 2, false, false)
+XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_t128_dmau, xpu::kFp16, 2, 2, 64, 2, 2, 2, 2, false, false)
 
 // dst[r][c] = src[r * src_ld + c] for c < cols, 0 for cols <= c < dst_cols
 // (dst_cols % 8 == 0, dst 16-byte aligned): the zero padding of the
