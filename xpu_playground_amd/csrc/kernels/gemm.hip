@@ -3,7 +3,7 @@
 // gemm_kernel.hpp:25-143, argument order (a, b, c, m, n, k) of
 // level_zero/gem_spv_entry.cpp:28-60).
 //
-// Block tile (64 MI) x (64 NJ), K-slice BK (64 or 32), S LDS stages, 256
+// Block tile (64 MI) x (64 NJ), K-slice BK (64 or 32), two LDS stages, 256
 // threads: four wavefronts in a 2 x 2 arrangement, each owning 32 MI x 32 NJ
 // of C as MI x NJ tiles of v_mfma_f32_32x32x16_{bf16,f16}. The large tile is
 // 256 x 256 (MI = NJ = 4, 256 FP32 accumulators per lane). The small tiles,
@@ -23,14 +23,15 @@
 // lanes (j >> 2) + 4 e, e = 0..3), which hand each lane 8 consecutive k of
 // one column n - the MFMA operand layout - out of the [k][n] tile.
 //
-// Pipeline (slice s in stage s % S): the DMA of slice s + S is issued right
+// Pipeline (slice s in stage s % 2): the DMA of slice s + 2 is issued right
 // after the barrier that publishes slice s + 1, into the stage slice s just
 // vacated; that barrier sits in slice s's last k-step after the first P of
-// its 16 MFMAs and is preceded by a vmcnt wait that leaves the DMA of slices
-// s + 2 .. s + S - 1 in flight. A slice's DMA is spread over the D k-steps
-// from its barrier on (D = 2 leaves the last of it more than two k-steps to
-// land). Fragments of the next k-step are read while the current one's MFMAs
-// run.
+// its MFMAs and is preceded by a wait for the DMA of slice s + 1. A slice's
+// DMA is spread over the D k-steps from its barrier on (D = 2 leaves the last
+// of it more than two k-steps to land). Fragments of the next k-step are read
+// while the current one's MFMAs run. Slices go in pairs; the _odd kernels
+// (an odd slice count of 3 or more) run the last slice on its own, only its
+// k-steps below K.
 //
 // Edges: loads past row M of A and past row K of B read zero through the
 // buffer range check; 16-byte chunks past column K of A or N of B are sent
