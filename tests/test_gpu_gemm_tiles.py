@@ -95,3 +95,27 @@ def test_small_tile_shapes_through_xpu_gemm(rt, m, n, k):
     a = orc.uniform(m * k, 80 + m, xpu.BF16)
     b = orc.uniform(k * n, 90 + n, xpu.BF16)
     check(gpu_gemm(rt, a, b, m, n, k, xpu.BF16), a, b, m, n, k, xpu.BF16)
+
+
+def random_shapes(count, seed):
+    """Seeded shapes across every launch form: small outputs (128x128 and
+    128x256 tiles), outputs that fill the chip with 256x256 tiles (short K,
+    so the FP64 oracle stays within a few seconds), ragged M, N and K
+    (padding, unaligned C), and odd and even slice counts."""
+    rng = np.random.default_rng(seed)
+    regimes = [((1, 1200), (1, 1200), (1, 1400)), ((1400, 2700), (1400, 4200), (8, 700)),
+               ((2800, 4200), (2800, 4200), (8, 400))]
+    shapes = []
+    for i in range(count):
+        (m0, m1), (n0, n1), (k0, k1) = regimes[i % 3]
+        shapes.append((int(rng.integers(m0, m1)), int(rng.integers(n0, n1)), int(rng.integers(k0, k1))))
+    return shapes
+
+
+@pytest.mark.parametrize("m,n,k", random_shapes(24, 2026))
+def test_gemm_random_shapes(rt, m, n, k):
+    print(f"xpu_gemm {m}x{n}x{k} tile {rt.gemm_tile(m, n)}", flush=True)
+    dtype = xpu.FP16 if (m + n + k) % 2 else xpu.BF16
+    a = orc.uniform(m * k, 7 * m + 1, dtype)
+    b = orc.uniform(k * n, 11 * n + 2, dtype)
+    check(gpu_gemm(rt, a, b, m, n, k, dtype), a, b, m, n, k, dtype)
