@@ -43,6 +43,9 @@ def check_against_fp64(y, a, x, m, k, lda, dtype):
 SHAPES = [
     (1, 1, 1), (3, 5, 5), (64, 512, 512), (37, 1000, 1000), (1000, 1032, 1040), (33, 4097, 4097),
     (4096, 1024, 1024), (1024, 3072, 3072), (151936, 1024, 1024), (8191, 2050, 2050),
+    # two rows per wavefront (K <= 8192, aligned) with an odd row count: the
+    # last wavefront's second row is past M
+    (4095, 2048, 2048), (7, 8192, 8200), (1025, 8200, 8200),
 ]
 
 

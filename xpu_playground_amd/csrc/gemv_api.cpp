@@ -30,11 +30,16 @@ int plan_gemv(const xpu_runtime &rt, int dtype, const void *A, const void *x, ui
     return set_error(XPU_ERR_INVALID, "GEMV K=" + std::to_string(K) +
                                           " exceeds the LDS and needs 16-byte aligned A, x and K, lda "
                                           "multiples of 8");
-  // one row per wavefront; 512-column chunks per pipelined load batch: 4
-  // with the vector in LDS (82-84% of 8 TB/s at 16384^2 fp16, against 63-77%
-  // for 2 or 4 rows per wavefront), 8 when the vector is read from global
-  // memory, 2 for the 16-bit-load path of unaligned operands
-  const uint32_t rows = 1, unroll = !vec ? 2 : global_x ? 8 : 4;
+  // rows per wavefront and 512-column chunks per pipelined load batch. With
+  // the vector in LDS: rows longer than 8192 columns one per wavefront, 4
+  // chunks per batch (6.7 TB/s at 16384^2 fp16, against 5.8-6.2 for 2 rows);
+  // shorter rows two per wavefront, 2 chunks per batch, so the bubble at each
+  // row's end is shared by two rows (6.6 TB/s at 65536 x 4096 and
+  // 32768 x 8192, against 5.2 and 6.3 for one row). 8 chunks when the vector
+  // is read from global memory, 2 for the 16-bit-load path of unaligned
+  // operands.
+  const bool short_rows = vec && !global_x && K <= 8192;
+  const uint32_t rows = short_rows ? 2 : 1, unroll = !vec ? 2 : global_x ? 8 : short_rows ? 2 : 4;
   plan.shared = global_x ? 0 : static_cast<uint32_t>(kpad * 2);
   // one block per compute unit, grid-stride over 4-row tiles: each block
   // stages the vector once

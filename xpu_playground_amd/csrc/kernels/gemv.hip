@@ -59,6 +59,7 @@ XPU_DEVICE void gemv_entry(const uint16_t *__restrict__ A, const uint16_t *__res
   XPU_GEMV_VARIANT(xpu_gemv_fp16_r##R##u##U##_vec, xpu::kFp16, R, U, true, false)
 
 XPU_GEMV_TYPES(1, 4)
+XPU_GEMV_TYPES(2, 2)
 XPU_GEMV_VARIANT(xpu_gemv_bf16_r1u2_any, xpu::kBf16, 1, 2, false, false)
 XPU_GEMV_VARIANT(xpu_gemv_fp16_r1u2_any, xpu::kFp16, 1, 2, false, false)
 XPU_GEMV_VARIANT(xpu_gemv_bf16_r1u8_vecg, xpu::kBf16, 1, 8, true, true)
