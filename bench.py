@@ -175,9 +175,10 @@ def xpu_check(code):
     xpu.check(code)
 
 
-def qwen3_decode(xpu, n_prompt=128, max_seq=256):
+def qwen3_decode(xpu, n_prompt=128, max_seq=256, prefill=None):
     """Qwen3-0.6B shape, random N(0, 0.02^2) bf16 weights, n_prompt seeded
-    prompt ids, 128 greedy steps; returns decode and prompt tok/s."""
+    prompt ids, 128 greedy steps; returns decode and prompt tok/s. prefill:
+    the engine's prompt mode (None: its default, 1 batched; 2 gemm)."""
     import numpy as np
 
     lib = xpu.library()
@@ -191,6 +192,8 @@ def qwen3_decode(xpu, n_prompt=128, max_seq=256):
     eng = ctypes.c_void_p()
     xpu.check(lib.xpu_qwen3_create(rt.handle, ctypes.byref(cfg), max_seq, 0, 0.0, ctypes.byref(eng)))
     try:
+        if prefill is not None:
+            xpu.check(lib.xpu_qwen3_set_prefill(eng, prefill))
         prompt = np.empty(n_prompt, np.uint32)
         # the same seeded ids as the oracle's orc_fill_tokens(seed 1)
         from xpu_playground_amd import qwen3 as q3
@@ -450,6 +453,12 @@ def main() -> int:
                 "prompt_tok_s": round(q["prompt_tok_s"], 1),
                 "attention": "split over compute units from 257 positions"}
             log(f"Qwen3 decode after 2048 prompt ids {q['decode_tok_s']:.1f} tok/s")
+            g = qwen3_decode(xpu, 2048, 2304, prefill=2)
+            if g:
+                secondary["qwen3_0.6b_decode_after_2048_prompt"]["prompt_tok_s_gemm_prefill"] = \
+                    round(g["prompt_tok_s"], 1)
+                log(f"Qwen3 2048-id prompt on the MFMA GEMM {g['prompt_tok_s']:.1f} tok/s "
+                    f"(batched GEMV {q['prompt_tok_s']:.1f})")
 
     # CPU baselines, after every GPU measurement (none overlaps a timed GPU region)
     cpu = None

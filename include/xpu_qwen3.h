@@ -115,14 +115,19 @@ int xpu_qwen3_get_config(const xpu_qwen3 *eng, xpu_qwen3_config *out);
  * and graph/eager mode, start again at position 0 (generate always does). */
 int xpu_qwen3_set_mode(xpu_qwen3 *eng, int mode);
 
-/* Prompt processing in xpu_qwen3_generate (graph and eager modes): batched
- * (default when the module has kernels for the shape) runs the prompt
- * positions before the last as one batch per layer with the same arithmetic
- * as the decode step, so the KV caches, tokens and logits are bit-identical
- * to the stepwise path, which feeds the prompt through decode one position
- * at a time as the reference does (main.cpp:343-344). XPU_ERR_INVALID when
- * batched is requested for an unsupported shape. */
-int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int batched);
+/* Prompt processing in xpu_qwen3_generate (graph and eager modes), mode:
+ *   0 stepwise: the prompt goes through decode one position at a time, as
+ *     the reference does (main.cpp:343-344);
+ *   1 batched (default when the module has kernels for the shape): the
+ *     prompt positions before the last run as one batch per layer with the
+ *     same arithmetic as the decode step, so the KV caches, tokens and
+ *     logits are bit-identical to stepwise;
+ *   2 gemm: as batched, with the four projections on the MFMA GEMM (FP32
+ *     accumulation in the GEMM's k-order, so the caches differ from
+ *     stepwise by rounding: within the GEMM's error bound, not bitwise).
+ * XPU_ERR_INVALID for another mode or a mode without kernels for the
+ * shape. The reference has no batched prompt path. */
+int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int mode);
 
 /* Attention of the graph and eager modes for contexts of at least
  * min_context positions (position + 1 >= min_context) runs split over
@@ -155,7 +160,7 @@ int xpu_qwen3_generate(xpu_qwen3 *eng, const uint32_t *prompt, uint32_t n_prompt
 /* Command line with the reference's flags (main.cpp:17-72):
  *   --model-dir DIR | --synthetic PRESET [--seed N] [--gain-std X]
  *   --input-ids FILE|- --max-new-tokens N [--max-seq-len N]
- *   [--mode graph|eager|reference] [--prefill batched|stepwise] [--no-eos-stop]
+ *   [--mode graph|eager|reference] [--prefill batched|gemm|stepwise] [--no-eos-stop]
  * prints {"generated_ids":[...]} on stdout, diagnostics on stderr. */
 int run_qwen3(int argc, char **argv);
 

@@ -324,3 +324,50 @@ def test_mode_switch_mid_sequence_is_rejected(rt):
     out += [eng.decode(seq[2], 2), eng.decode(seq[3], 3)]
     assert out == ref
     eng.close()
+
+
+@pytest.mark.parametrize("n_prompt,max_seq", [(40, 96), (300, 320), (2, 16)])
+def test_gemm_prefill_within_rounding(rt, n_prompt, max_seq):
+    # the projections of the prompt positions on the MFMA GEMM: each
+    # projection output is within the GEMM's bar of the canonical one, so
+    # the caches differ from the oracle's by bf16 rounding and the logits and
+    # hidden state of the first new token by a small multiple of it; a
+    # dropped residual, a swapped gate/up half or a transposed weight moves
+    # them by O(1)
+    cfg = orc.config("small")
+    prompt = orc.tokens(n_prompt, 12, cfg.vocab)
+    m = orc.Model(cfg, seed=4, gain_std=0.1, max_seq=max_seq)
+    ref, ref_logits = m.generate(prompt, 1, logit_steps=1)
+    want = orc.decode(ref_logits[0], xpu.BF16).astype(np.float64)
+    want_h = orc.decode(m.hidden(), xpu.BF16).astype(np.float64)
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=max_seq, seed=4, gain_std=0.1, runtime=rt)
+    eng.set_prefill("gemm")
+    for mode in (qwen3.GRAPH, qwen3.EAGER):
+        print(f"gemm prefill n_prompt={n_prompt} mode={mode}", flush=True)
+        eng.set_mode(mode)
+        out, _, _ = eng.generate(prompt, 1, stop_on_eos=False)
+        got = orc.decode(eng.logits(), xpu.BF16).astype(np.float64)
+        got_h = orc.decode(eng.hidden(), xpu.BF16).astype(np.float64)
+        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+        rel_h = np.linalg.norm(got_h - want_h) / np.linalg.norm(want_h)
+        dmax = float(np.abs(got - want).max())
+        print(f"logits rel-L2 {rel:.3e} max|d| {dmax:.3e} (max|logit| {np.abs(want).max():.3e}), "
+              f"hidden rel-L2 {rel_h:.3e}", flush=True)
+        assert rel <= 2e-2 and rel_h <= 2e-2, (rel, rel_h)
+        top2 = np.sort(want)[-2:]
+        if top2[1] - top2[0] > 2 * dmax:
+            assert out.tolist() == ref.tolist()
+    eng.set_prefill("batched")
+    eng.generate(prompt, 1, stop_on_eos=False)
+    assert np.array_equal(eng.logits(), ref_logits[0])
+    eng.close()
+
+
+def test_gemm_prefill_mode_checks(rt):
+    cfg = orc.config("tiny")
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=32, seed=1, gain_std=0.1, runtime=rt)
+    with pytest.raises(xpu.XpuError, match="prefill"):
+        eng.set_prefill("gemm")
+    with pytest.raises(xpu.XpuError, match="prefill mode"):
+        xpu.check(eng.lib.xpu_qwen3_set_prefill(eng.handle, 3))
+    eng.close()

@@ -154,6 +154,33 @@ int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, 
   return rt->launch(*k, static_cast<uint32_t>(tiles), 1, 256, 0, args, 9);
 }
 
+// C[M x N] = A[M x K] W^T for W given [N][K] (bf16, K and N multiples of 8,
+// every pointer 16-byte aligned, row strides K, K and N), the projections of
+// the batched prompt (qwen3_engine.cpp); residual: C = bf16(C + bf16(A W^T)).
+// The block tile and the odd-slice form are chosen as for xpu_gemm.
+int gemm_nt(xpu_runtime *rt, const void *A, const void *W, void *C, uint32_t M, uint32_t N, uint32_t K,
+            bool residual) {
+  if (!rt || !A || !W || !C) return set_error(XPU_ERR_INVALID, "gemm_nt: null argument");
+  if (M == 0 || N == 0 || K == 0 || K % 8 || N % 8 || (reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(W) |
+                                                       reinterpret_cast<uintptr_t>(C)) % 16)
+    return set_error(XPU_ERR_INVALID, "gemm_nt: needs positive M, N, K with K, N multiples of 8 and 16-byte aligned "
+                                      "operands");
+  if (static_cast<uint64_t>(K) * 256 * 2 >= (1ull << 31) || static_cast<uint64_t>(N) >= (1u << 24))
+    return set_error(XPU_ERR_INVALID, "gemm_nt: K must be below 4M and N below 16M");
+  const GemmTile &tile = choose_tile(rt->compute_units, M, N);
+  const uint32_t slices = (K + 63) / 64;
+  const bool odd = tile.tag[0] == '\0' && slices % 2 == 1 && slices >= 3;
+  const std::string name = std::string("xpu_gemm_bf16") + tile.tag + (odd ? "_odd" : "") + "_nt" +
+                           (residual ? "_res" : "") + "_dma";
+  const xpu::KernelInfo *k = rt->find_exact(name);
+  if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: " + name);
+  const uint64_t tiles = ((static_cast<uint64_t>(M) + tile.rows - 1) / tile.rows) *
+                         ((static_cast<uint64_t>(N) + tile.cols - 1) / tile.cols);
+  uint32_t kb = K, ldc = N, n_out = N;
+  const xpu_kernel_arg args[] = {{8, &A}, {8, &W}, {8, &C}, {4, &M}, {4, &N}, {4, &K}, {4, &kb}, {4, &ldc}, {4, &n_out}};
+  return rt->launch(*k, static_cast<uint32_t>(tiles), 1, 256, 0, args, 9);
+}
+
 }  // namespace xpu
 
 extern "C" int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,

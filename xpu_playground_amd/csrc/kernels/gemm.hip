@@ -112,7 +112,7 @@ template <int DT> XPU_DEVICE uint32_t cvt_pack(float lo, float hi) {
 
 // MI, NJ: 32 x 32 MFMA tiles per wavefront along M and N (wavefront tile
 // 32 MI x 32 NJ, block tile 64 MI x 64 NJ); BK: K-slice; S: LDS stages.
-template <int MI, int NJ, int BK, int S> struct Cfg {
+template <int MI, int NJ, int BK, int S, bool BT = false> struct Cfg {
   static constexpr uint32_t kBMW = 32u * MI;                 // rows per wavefront
   static constexpr uint32_t kBM = 2u * kBMW;                 // block tile rows
   static constexpr uint32_t kBNW = 32u * NJ;                 // columns per wavefront
@@ -126,10 +126,12 @@ template <int MI, int NJ, int BK, int S> struct Cfg {
   static constexpr uint32_t kBCpr = kBN / 8;                 // 16-byte chunks per B row
   static constexpr uint32_t kBRpi = 64 / kBCpr;              // B rows per DMA instruction
   static constexpr uint32_t kDmaA = kBM / kRpi / 4;          // A DMA instructions per wave per slice
-  static constexpr uint32_t kDmaB = BK / kBRpi / 4;          // B DMA instructions per wave per slice
+  // B DMA instructions per wave per slice ([n][k] tiles: as A, kBN rows)
+  static constexpr uint32_t kDmaB = BT ? kBN / kRpi / 4 : BK / kBRpi / 4;
   static constexpr uint32_t kDma = kDmaA + kDmaB;
   static constexpr uint32_t kMf = MI * NJ;                   // MFMAs per k-step
-  static constexpr uint32_t kReads = MI + 2u * NJ;           // fragment reads per k-step
+  // fragment reads per k-step ([n][k] B fragments are one read each)
+  static constexpr uint32_t kReads = BT ? MI + NJ : MI + 2u * NJ;
   static constexpr uint32_t kEpPitch = kBNW + 4;             // epilogue staging pitch (floats)
   static constexpr uint32_t kEpBytes = 4u * 64u * kEpPitch * 4u;
   static constexpr uint32_t kLds = S * kStage > kEpBytes ? S * kStage : kEpBytes;
@@ -144,10 +146,15 @@ template <int MI, int NJ, int BK, int S> struct Cfg {
 // pairs, and only its k-steps that start below K (otherwise the last pair's
 // second slice would add a slice of zeros, and a slice that ends past K its
 // dead k-steps).
-template <int DT, int MI, int NJ, int BK, int S, int P, int D, bool C16, bool ODD>
+// BT: B is given as its transpose, [N][K] row-major (the rows of a weight
+// matrix W for C = X W^T); its tile is staged and read like A's. RES: C is
+// updated in place, C = bf16(C + bf16(A B)) (a residual add), C16 only.
+template <int DT, int MI, int NJ, int BK, int S, int P, int D, bool C16, bool ODD, bool BT = false,
+          bool RES = false>
 XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
                      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {
-  using G = Cfg<MI, NJ, BK, S>;
+  using G = Cfg<MI, NJ, BK, S, BT>;
+  static_assert(!RES || C16, "the residual epilogue stores 16-byte chunks");
   __shared__ __align__(1024) uint8_t lds[G::kLds];
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -164,26 +171,34 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   const uint32_t a_chunk = (lane % G::kCpr) ^ a_swz<BK>(a_row & 15u);
   const uint32_t a_voff = (a_row * K + a_chunk * 8u) * 2u;
   const uint32_t a_istride = 4u * G::kRpi * K * 2u;
-  const uint32_t b_row = G::kBRpi * wave + lane / G::kBCpr;
-  const uint32_t b_chunk = (lane % G::kBCpr) ^ b_swz(b_row & 3u);
-  const uint32_t b_voff = n0 + b_chunk * 8u < N ? (b_row * N + b_chunk * 8u) * 2u : kOob;
-  const uint32_t b_istride = 4u * G::kBRpi * N * 2u;
+  // B as [k][n]: instruction i fills rows kBRpi (wave + 4 i) .. + kBRpi - 1;
+  // B as [n][k] (BT): the A map over its kBN rows
+  const uint32_t b_row = BT ? a_row : G::kBRpi * wave + lane / G::kBCpr;
+  const uint32_t b_chunk = BT ? a_chunk : (lane % G::kBCpr) ^ b_swz(b_row & 3u);
+  const uint32_t b_voff = BT ? (b_row * K + b_chunk * 8u) * 2u
+                             : (n0 + b_chunk * 8u < N ? (b_row * N + b_chunk * 8u) * 2u : kOob);
+  const uint32_t b_istride = BT ? a_istride : 4u * G::kBRpi * N * 2u;
 
   // DMA instruction d (0 .. kDma-1) of slice s into stage st: A rows first,
   // then B rows. Per slice the descriptors are rebased to the slice's first
   // column (A) and row (B).
   struct Slice {
     i32x4 r_a, r_b;
-    uint32_t a_base, st_base;
+    uint32_t a_base, b_base, st_base;
   };
   auto slice_of = [&](uint32_t s, uint32_t stage) {
     const uint64_t k0 = static_cast<uint64_t>(s) * BK;
     Slice d;
     d.r_a = rsrc(A + static_cast<uint64_t>(m0) * K + k0,
                  (static_cast<int64_t>(M - m0) * K - static_cast<int64_t>(k0)) * 2);
-    d.r_b = rsrc(B + k0 * N + n0,
-                 (static_cast<int64_t>(kb) - static_cast<int64_t>(k0)) * N * 2 - static_cast<int64_t>(n0) * 2);
+    if constexpr (BT)
+      d.r_b = rsrc(B + static_cast<uint64_t>(n0) * K + k0,
+                   (static_cast<int64_t>(N - n0) * K - static_cast<int64_t>(k0)) * 2);
+    else
+      d.r_b = rsrc(B + k0 * N + n0,
+                   (static_cast<int64_t>(kb) - static_cast<int64_t>(k0)) * N * 2 - static_cast<int64_t>(n0) * 2);
     d.a_base = k0 + a_chunk * 8u < K ? a_voff : kOob;
+    d.b_base = !BT || k0 + b_chunk * 8u < K ? b_voff : kOob;
     d.st_base = lds0 + stage * G::kStage;
     return d;
   };
@@ -192,7 +207,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
       dma16(d.st_base + (wave + 4u * op) * 1024u, d.r_a, d.a_base + op * a_istride);
     else
       dma16(d.st_base + G::kABytes + (wave + 4u * (op - G::kDmaA)) * 1024u, d.r_b,
-            b_voff + (op - G::kDmaA) * b_istride);
+            d.b_base + (op - G::kDmaA) * b_istride);
   };
 
   // Fragment addresses (bytes within a stage). A: row wm*kBMW + 32 i + l%32,
@@ -205,7 +220,8 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   // that it keeps them in registers instead of materialising one register per
   // (stage, k-step, tile) combination.
   constexpr uint32_t kGroups = (S * G::kStage + 65535u) / 65536u;
-  uint32_t fa_base[kGroups][G::kKs], fb_base[kGroups][NJ];
+  constexpr uint32_t kFb = BT ? G::kKs : NJ;  // B bases: per k-step ([n][k]) or per column tile ([k][n])
+  uint32_t fa_base[kGroups][G::kKs], fb_base[kGroups][kFb];
   {
     const uint32_t krow = 8u * (lane >> 5) + ((lane & 15u) >> 2);
     const uint32_t x = 2u * ((lane >> 4) & 1u) + ((lane & 3u) >> 1);
@@ -218,9 +234,13 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
         asm volatile("" : "+v"(fa_base[g][ks]));
       }
 #pragma unroll
-      for (uint32_t j = 0; j < NJ; ++j) {
-        fb_base[g][j] = lds0 + g * 65536u + G::kABytes + krow * G::kBRow +
-                        16u * ((wn * (G::kBNW / 8u) + 4u * j + x) ^ b_swz(krow & 3u)) + 8u * (lane & 1u);
+      for (uint32_t j = 0; j < kFb; ++j) {
+        if constexpr (BT)  // row wn*kBNW + 32 jj + l%32, logical chunk 2 ks + l/32 (ks = j here)
+          fb_base[g][j] = lds0 + g * 65536u + G::kABytes + (wn * G::kBNW + (lane & 31u)) * (2u * BK) +
+                          16u * ((2u * j + (lane >> 5)) ^ a_swz<BK>(lane & 15u));
+        else
+          fb_base[g][j] = lds0 + g * 65536u + G::kABytes + krow * G::kBRow +
+                          16u * ((wn * (G::kBNW / 8u) + 4u * j + x) ^ b_swz(krow & 3u)) + 8u * (lane & 1u);
         asm volatile("" : "+v"(fb_base[g][j]));
       }
     }
@@ -234,6 +254,18 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   // A(MI-1).
   auto read = [&](uint32_t stage, uint32_t ks, Frags &f, uint32_t r) {
     const uint32_t g = stage * G::kStage / 65536u, in_group = stage * G::kStage % 65536u;
+    if constexpr (BT) {
+      // A0, B0 .. B(NJ-1), A1 .. A(MI-1), one ds_read_b128 each
+      if (r == 0 || r > NJ) {
+        const uint32_t i = r == 0 ? 0 : r - NJ;
+        f.a[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
+            fa_base[g][ks] + in_group + i * 32u * 2u * BK);
+      } else {
+        f.b[r - 1] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
+            fb_base[g][ks] + in_group + (r - 1) * 32u * 2u * BK);
+      }
+      return;
+    }
     if (r == 0 || r > 2u * NJ) {
       const uint32_t i = r == 0 ? 0 : r - 2u * NJ;
       const uint32_t addr = fa_base[g][ks] + in_group + i * 32u * 2u * BK;
@@ -446,7 +478,18 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
         const u32x4 packed{cvt_pack<DT>(lo[b].x, lo[b].y), cvt_pack<DT>(lo[b].z, lo[b].w),
                            cvt_pack<DT>(hi[b].x, hi[b].y), cvt_pack<DT>(hi[b].z, hi[b].w)};
         uint16_t *dst = C + static_cast<uint64_t>(m) * ldc + n;
-        if constexpr (C16)
+        if constexpr (RES) {
+          // C = bf16(C + bf16(product)), element by element
+          const u32x4 old = *reinterpret_cast<const u32x4 *>(dst);
+          const float pr[8] = {lo[b].x, lo[b].y, lo[b].z, lo[b].w, hi[b].x, hi[b].y, hi[b].z, hi[b].w};
+          const uint32_t ow[4] = {old.x, old.y, old.z, old.w};
+          uint32_t nw[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            nw[q] = f32_to_bf16(bf16_to_f32(ow[q] & 0xffffu) + round_bf16(pr[2 * q])) |
+                    (f32_to_bf16(bf16_to_f32(ow[q] >> 16) + round_bf16(pr[2 * q + 1])) << 16);
+          *reinterpret_cast<u32x4 *>(dst) = u32x4{nw[0], nw[1], nw[2], nw[3]};
+        } else if constexpr (C16)
           *reinterpret_cast<u32x4 *>(dst) = packed;
         else  // C rows 2-byte aligned: global memory runs in unaligned access mode on gfx950
           __builtin_memcpy(dst, &packed, 16);
@@ -481,6 +524,24 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     XPU_STAMP(xpu::kStampGemm);                                                                 \
     xpu::dma::body<DT, MI, NJ, BK, S, P, D, C16, ODD>(A, B, C, M, N, K, kb, ldc, n_out);       \
   }
+
+// C = A W^T with W given [N][K] (BT) for the batched prompt projections, bf16,
+// 16-byte aligned C; _res adds into C (residual)
+#define XPU_GEMM_NT_VARIANT(NAME, MI, NJ, P, MINB, ODD, RES)                                      \
+  extern "C" __global__ __launch_bounds__(256, MINB) void NAME(                               \
+      const uint16_t *__restrict__ A, const uint16_t *__restrict__ W, uint16_t *__restrict__ C, \
+      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {         \
+    XPU_STAMP(xpu::kStampGemm);                                                                 \
+    xpu::dma::body<xpu::kBf16, MI, NJ, 64, 2, P, 2, true, ODD, true, RES>(A, W, C, M, N, K, kb, ldc, n_out); \
+  }
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_nt_dma, 4, 4, 4, 1, false, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_nt_res_dma, 4, 4, 4, 1, false, true)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_odd_nt_dma, 4, 4, 4, 1, true, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_odd_nt_res_dma, 4, 4, 4, 1, true, true)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_dma, 2, 4, 4, 1, false, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_res_dma, 2, 4, 4, 1, false, true)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_dma, 2, 2, 2, 2, false, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_res_dma, 2, 2, 2, 2, false, true)
 
 // 256 x 256: BK = 64, two stages, barrier after 4 MFMAs of a slice's last
 // k-step, each slice's DMA spread over two k-steps; _odd for an odd number

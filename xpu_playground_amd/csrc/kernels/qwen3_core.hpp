@@ -275,12 +275,7 @@ XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const 
                                const uint16_t *vcur, float scale, uint16_t *out, float *sbuf,
                                uint16_t *vtile, float *red) {
   const uint32_t tid = threadIdx.x;
-  const uint32_t nchunks = (n + kAttnChunk - 1) / kAttnChunk;
   const bool single_tile = n <= kAttnTile;
-  auto score_of = [&](uint32_t t) -> float {
-    if (HAS_CURRENT && t + 1 == n) return attention_score(qs, kcur, scale);
-    return attention_score(qs, kbase + static_cast<uint64_t>(t) * lay.kstride, scale, lay.kchunk);
-  };
   // V row t: chunk j at vrow_of(t) + j * vchunk_of(t) (the new token's row,
   // kept contiguous in vcur, when HAS_CURRENT and t is the last position)
   auto vrow_of = [&](uint32_t t) -> const uint16_t * {

@@ -1125,6 +1125,31 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_rmsnorm(const uint16
     *reinterpret_cast<u32x4 *>(Xn + row + i) = *reinterpret_cast<const u32x4 *>(xs + i);
 }
 
+// Hb[t][i] = bf16(bf16(silu(g)) u) for g = GU[t][i], u = GU[t][I + i]: the
+// SiLU-multiply after the MFMA form of the prompt's [gate; up] projection
+// (GU [T][2I], its gate and up halves side by side), the same rounding
+// points as the fused kernels (silu_mul_code). One thread per 8 outputs
+// (I % 8 == 0).
+extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_silu_mul(const uint16_t *__restrict__ GU,
+                                                                     uint16_t *__restrict__ Hb, uint32_t I,
+                                                                     uint32_t T) {
+  const uint32_t per_row = I / 8u;
+  const uint64_t total = static_cast<uint64_t>(T) * per_row;
+  for (uint64_t c = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < total;
+       c += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+    const uint64_t t = c / per_row, i = (c % per_row) * 8u;
+    const u32x4 g = *reinterpret_cast<const u32x4 *>(GU + t * 2u * I + i);
+    const u32x4 u = *reinterpret_cast<const u32x4 *>(GU + t * 2u * I + I + i);
+    const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+    uint32_t hw[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      hw[q] = silu_mul_code(xpu::bf16_to_f32(gw[q] & 0xffffu), xpu::bf16_to_f32(uw[q] & 0xffffu)) |
+              (silu_mul_code(xpu::bf16_to_f32(gw[q] >> 16), xpu::bf16_to_f32(uw[q] >> 16)) << 16);
+    *reinterpret_cast<u32x4 *>(Hb + t * I + i) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+  }
+}
+
 namespace {
 
 // Batched canonical GEMV: Out[t][row] for rows of W (M x K, K = 512 NC) and

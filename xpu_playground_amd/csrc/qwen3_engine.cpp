@@ -157,12 +157,15 @@ struct xpu_qwen3 {
     uint32_t grid = 0, shared = 0;
   } qkv_l, attn_l, scores_l, pv_l, o_l, gu_l, down_l, logits_l, finish_l;
   // batched prefill (kernels/qwen3_ops.hip part 3): chunk buffers of
-  // pf_chunk tokens; pf_ok when the shape has kernels for every projection
-  bool pf_ok = false, batched_prefill = false;
+  // pf_chunk tokens; pf_ok when the shape has kernels for every projection;
+  // gemm_prefill: the projections on the MFMA GEMM (pf_gemm_ok when the
+  // module has its kernels)
+  bool pf_ok = false, batched_prefill = false, pf_gemm_ok = false, gemm_prefill = false;
   uint32_t pf_chunk = 0;
   void *pf_block = nullptr;
   uint16_t *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_a = nullptr,
-           *pf_h = nullptr;
+           *pf_h = nullptr, *pf_gu = nullptr;
+  const xpu::KernelInfo *pf_silu_k = nullptr;
   const xpu::KernelInfo *pf_attn_short_k = nullptr;  // chunks whose contexts stay within 256 positions
   const xpu::KernelInfo *pf_embed_k = nullptr, *pf_norm_k = nullptr, *pf_rope_k = nullptr, *pf_attn_k = nullptr,
                         *pf_qkv_k = nullptr, *pf_o_k = nullptr, *pf_gu_k = nullptr, *pf_down_k = nullptr;
@@ -372,18 +375,24 @@ int setup_prefill(xpu_qwen3 &e) {
   if (!e.pf_ok) return XPU_OK;
   e.pf_chunk = std::min<uint32_t>(e.max_seq, 256);
   const uint64_t T = e.pf_chunk, qkv_rows = uint64_t{c.heads + 2 * c.kv_heads} * c.head_dim;
-  const uint64_t sizes[6] = {T * c.hidden, T * c.hidden, T * qkv_rows, T * qd, T * qd, T * c.intermediate};
+  const uint64_t sizes[7] = {T * c.hidden, T * c.hidden, T * qkv_rows, T * qd, T * qd, T * c.intermediate,
+                             T * 2 * c.intermediate};
   uint64_t total = 0;
   for (uint64_t n : sizes) total += (n * 2 + 255) & ~uint64_t{255};
   int rc = xpu_rt_alloc(e.rt, total, 4096, &e.pf_block);
   if (rc) return rc;
-  uint16_t **dst[6] = {&e.pf_x, &e.pf_xn, &e.pf_qkv, &e.pf_q, &e.pf_a, &e.pf_h};
+  uint16_t **dst[7] = {&e.pf_x, &e.pf_xn, &e.pf_qkv, &e.pf_q, &e.pf_a, &e.pf_h, &e.pf_gu};
   uint8_t *p = static_cast<uint8_t *>(e.pf_block);
-  for (int i = 0; i < 6; ++i) {
+  for (int i = 0; i < 7; ++i) {
     *dst[i] = reinterpret_cast<uint16_t *>(p);
     p += (sizes[i] * 2 + 255) & ~uint64_t{255};
   }
   e.batched_prefill = true;
+  // the MFMA form: every projection's K and N multiples of 8 (the NT GEMM
+  // kernels read the weight rows in place)
+  e.pf_silu_k = e.rt->find_exact("xpu_q3_pf_silu_mul");
+  e.pf_gemm_ok = e.pf_silu_k && e.rt->find_exact("xpu_gemm_bf16_nt_dma") && c.intermediate % 8 == 0 &&
+                 qd % 8 == 0 && qkv_rows % 8 == 0;
   return XPU_OK;
 }
 
@@ -477,9 +486,12 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
       if ((rc = go(e.pf_norm_k, T, 1, 256, kpad_bytes(H),
                    {{8, &e.pf_x}, {8, &L.in_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}})))
         return rc;
-      if ((rc = go(e.pf_qkv_k, (qkv_rows + 7) / 8, 1, 256, pf_lds(H),
-                   {{8, &L.qkv}, {8, &e.pf_xn}, {8, &e.pf_qkv}, {4, &qkv_rows}, {4, &T}})))
+      if (e.gemm_prefill) {
+        if ((rc = xpu::gemm_nt(rt, e.pf_xn, L.qkv, e.pf_qkv, T, qkv_rows, H, false))) return rc;
+      } else if ((rc = go(e.pf_qkv_k, (qkv_rows + 7) / 8, 1, 256, pf_lds(H),
+                          {{8, &L.qkv}, {8, &e.pf_xn}, {8, &e.pf_qkv}, {4, &qkv_rows}, {4, &T}}))) {
         return rc;
+      }
       if ((rc = go(e.pf_rope_k, heads + kv, T, 64, 0,
                    {{8, &e.pf_qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &kc},
                     {8, &vc}, {8, &e.pf_q}, {4, &p0}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps}})))
@@ -490,11 +502,22 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
                     {4, &max_seq}, {4, &scale}})))
         return rc;
       if (l + 1 == c.layers) break;
-      if ((rc = go(e.pf_o_k, (H + 3) / 4, 1, 256, pf_lds(qd), {{8, &L.o}, {8, &e.pf_a}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
+      if (e.gemm_prefill) {
+        if ((rc = xpu::gemm_nt(rt, e.pf_a, L.o, e.pf_x, T, H, qd, true))) return rc;
+      } else if ((rc = go(e.pf_o_k, (H + 3) / 4, 1, 256, pf_lds(qd),
+                          {{8, &L.o}, {8, &e.pf_a}, {8, &e.pf_x}, {4, &H}, {4, &T}}))) {
         return rc;
+      }
       if ((rc = go(e.pf_norm_k, T, 1, 256, kpad_bytes(H),
                    {{8, &e.pf_x}, {8, &L.post_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}})))
         return rc;
+      if (e.gemm_prefill) {
+        const uint32_t two_i = 2 * I, silu_grid = std::min<uint32_t>((T * (I / 8) + 255) / 256, 4096);
+        if ((rc = xpu::gemm_nt(rt, e.pf_xn, L.gu, e.pf_gu, T, two_i, H, false))) return rc;
+        if ((rc = go(e.pf_silu_k, silu_grid, 1, 256, 0, {{8, &e.pf_gu}, {8, &e.pf_h}, {4, &I}, {4, &T}}))) return rc;
+        if ((rc = xpu::gemm_nt(rt, e.pf_h, L.down, e.pf_x, T, H, I, true))) return rc;
+        continue;
+      }
       if ((rc = go(e.pf_gu_k, (I + 3) / 4, 1, 256, pf_lds(H), {{8, &L.gu}, {8, &e.pf_xn}, {8, &e.pf_h}, {4, &I}, {4, &T}})))
         return rc;
       if ((rc = go(e.pf_down_k, (H + 3) / 4, 1, 256, pf_lds(I), {{8, &L.down}, {8, &e.pf_h}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
@@ -982,11 +1005,15 @@ extern "C" int xpu_qwen3_set_mode(xpu_qwen3 *eng, int mode) {
   return XPU_OK;
 }
 
-extern "C" int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int batched) {
+extern "C" int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int mode) {
   if (!eng) return set_error(XPU_ERR_INVALID, "null engine");
-  if (batched && !eng->pf_ok)
+  if (mode < 0 || mode > 2) return set_error(XPU_ERR_INVALID, "prefill mode must be 0 (stepwise), 1 (batched) or 2 (gemm)");
+  if (mode && !eng->pf_ok)
     return set_error(XPU_ERR_INVALID, "batched prefill has no kernels for this model shape");
-  eng->batched_prefill = batched != 0;
+  if (mode == 2 && !eng->pf_gemm_ok)
+    return set_error(XPU_ERR_INVALID, "gemm prefill has no kernels for this model shape");
+  eng->batched_prefill = mode != 0;
+  eng->gemm_prefill = mode == 2;
   return XPU_OK;
 }
 
@@ -1169,7 +1196,7 @@ QwenOptions parse_qwen(int argc, char **argv) {
       std::cout << "Usage: " << argv[0]
                 << " --model-dir DIR | --synthetic qwen3-0.6b|qwen3-8b|tiny|small [--seed N] [--gain-std X]\n"
                    "       --input-ids FILE|- --max-new-tokens N [--max-seq-len N]\n"
-                   "       [--mode graph|eager|reference] [--prefill batched|stepwise] [--no-eos-stop]\n";
+                   "       [--mode graph|eager|reference] [--prefill batched|gemm|stepwise] [--no-eos-stop]\n";
       std::exit(0);
     }
     if (opt == "--no-eos-stop") { o.stop_on_eos = false; continue; }
@@ -1190,7 +1217,8 @@ QwenOptions parse_qwen(int argc, char **argv) {
     } else if (opt == "--prefill") {
       if (v == "batched") o.prefill = 1;
       else if (v == "stepwise") o.prefill = 0;
-      else qwen_usage_error("--prefill must be batched or stepwise");
+      else if (v == "gemm") o.prefill = 2;
+      else qwen_usage_error("--prefill must be batched, gemm or stepwise");
     } else {
       qwen_usage_error("unknown option: " + opt);
     }

@@ -52,6 +52,11 @@ template <typename T> T arg_value(const xpu_kernel_arg *args, uint32_t index) {
 int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, uint32_t M, uint32_t N, uint32_t K,
              void *fixed_workspace, uint64_t fixed_capacity);
 
+// C = A W^T for W given [N][K], bf16, aligned operands (gemm_api.cpp);
+// residual adds into C
+int gemm_nt(xpu_runtime *rt, const void *A, const void *W, void *C, uint32_t M, uint32_t N, uint32_t K,
+            bool residual);
+
 // Device address of the no-allocation scratch array on `device` (the
 // current device), looked up once per device; called by xpu_rt_create.
 int noalloc_scratch_setup(int device);

@@ -110,9 +110,14 @@ class Engine:
     def set_mode(self, mode: int) -> None:
         check(self.lib.xpu_qwen3_set_mode(self.handle, mode))
 
-    def set_prefill(self, batched: bool) -> None:
-        """Batched (default) or stepwise prompt processing in generate."""
-        check(self.lib.xpu_qwen3_set_prefill(self.handle, 1 if batched else 0))
+    PREFILL_MODES = {"stepwise": 0, "batched": 1, "gemm": 2}
+
+    def set_prefill(self, mode) -> None:
+        """Prompt processing in generate: "batched" (default; True),
+        "stepwise" (False) or "gemm" (the projections on the MFMA GEMM)."""
+        if isinstance(mode, bool):
+            mode = "batched" if mode else "stepwise"
+        check(self.lib.xpu_qwen3_set_prefill(self.handle, self.PREFILL_MODES[mode]))
 
     def set_attention_split(self, min_context: int) -> None:
         """Split the attention over compute units for contexts of at least
