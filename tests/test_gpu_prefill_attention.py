@@ -1,0 +1,91 @@
+"""The prompt chunk's attention on MFMA (xpu_q3_pf_attention_mfma_g<G>,
+the engine's GEMM prompt mode) against the oracle's attention
+(orc_attention_head, qwen3/kernels.hpp:157-192) for every query row and
+head, with the per-token kernel of the batched prompt mode
+(xpu_q3_pf_attention) as the bit-exact control on the same caches.
+
+The MFMA kernel rounds where the oracle rounds (bf16 scores, bf16(s *
+scale), exact row max, canonical exp, bf16 p, FP32 P.V, bf16 out); its FP32
+sums run in the MFMA's order, so a score can round to the neighbouring bf16
+code and move its p by a bf16 step. The bar: rel-L2 <= 1e-2 over the chunk
+and every element within 2 bf16 ulps of the row's largest |out| plus
+1/64 of it. Cache positions past the chunk hold NaN codes, which a read of
+a key beyond the block's last query would spread into the output."""
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+import xpu_playground_amd as xpu
+from xpu_playground_amd import Args
+
+pytestmark = pytest.mark.gpu
+
+NAN = 0x7FC0
+
+
+def run_case(rt, p0, T, heads, kv, max_seq, q_gain, seed):
+    g = heads // kv
+    q = orc.uniform(T * heads * 128, seed, xpu.BF16)
+    if q_gain != 1.0:
+        q = orc.encode(orc.decode(q, xpu.BF16) * q_gain, xpu.BF16)
+    n = p0 + T
+    kpos = np.full((kv, max_seq, 128), NAN, np.uint16)
+    vpos = np.full((kv, max_seq, 128), NAN, np.uint16)
+    kpos[:, :n] = orc.uniform(kv * n * 128, seed + 1, xpu.BF16).reshape(kv, n, 128)
+    vpos[:, :n] = orc.uniform(kv * n * 128, seed + 2, xpu.BF16).reshape(kv, n, 128)
+    # chunk-major [kv][16][max_seq][8]
+    kcm = np.ascontiguousarray(kpos.reshape(kv, max_seq, 16, 8).transpose(0, 2, 1, 3))
+    vcm = np.ascontiguousarray(vpos.reshape(kv, max_seq, 16, 8).transpose(0, 2, 1, 3))
+    scale = float(np.float32(1.0 / np.sqrt(128.0)))
+    dq, dk, dv = rt.upload(q), rt.upload(kcm), rt.upload(vcm)
+    outs = {}
+    try:
+        for name in (f"xpu_q3_pf_attention_mfma_g{g}", "xpu_q3_pf_attention"):
+            da = rt.alloc(T * heads * 128 * 2)
+            try:
+                rt.memset(da, 0xFF, T * heads * 128 * 2)
+                if name.startswith("xpu_q3_pf_attention_mfma"):
+                    blocks = (T + 128 // g - 1) // (128 // g) * kv
+                    args = Args().ptr(dq).ptr(dk).ptr(dv).ptr(da).u32(p0).u32(T).u32(heads).u32(kv).u32(max_seq)
+                    print(f"{name} p0={p0} T={T} heads={heads} kv={kv} blocks={blocks}", flush=True)
+                    rt.launch_grid(name, blocks, 256, 0, args.f32(scale))
+                else:
+                    args = Args().ptr(dq).ptr(dk).ptr(dv).ptr(da).u32(p0).u32(heads).u32(kv).u32(max_seq)
+                    print(f"{name} p0={p0} T={T}", flush=True)
+                    rt.launch_grid(name, heads, 256, 0, args.f32(scale), grid_y=T)
+                rt.synchronize()
+                outs[name] = rt.download(da, T * heads * 128, np.uint16).reshape(T, heads, 128)
+            finally:
+                rt.free(da)
+    finally:
+        for p in (dq, dk, dv):
+            rt.free(p)
+    qr = q.reshape(T, heads, 128)
+    ref = np.empty((T, heads, 128), np.uint16)
+    for t in range(T):
+        for h in range(heads):
+            ref[t, h] = orc.attention_head(qr[t, h], kpos[h // g], vpos[h // g], 128, p0 + t + 1)
+    return outs[f"xpu_q3_pf_attention_mfma_g{g}"], outs["xpu_q3_pf_attention"], ref
+
+
+CASES = [(0, 300, 16, 8, 1.0), (0, 300, 16, 8, 8.0), (37, 129, 16, 8, 4.0), (0, 1, 16, 8, 1.0), (5, 2, 16, 8, 1.0),
+         (200, 64, 32, 8, 4.0), (0, 100, 8, 8, 4.0), (513, 200, 16, 8, 2.0), (64, 191, 16, 4, 4.0)]
+
+
+@pytest.mark.parametrize("p0,T,heads,kv,q_gain", CASES)
+def test_mfma_prefill_attention(rt, p0, T, heads, kv, q_gain):
+    got, control, ref = run_case(rt, p0, T, heads, kv, p0 + T + 40, q_gain, 900 + p0 + T)
+    assert np.array_equal(control, ref), "per-token kernel differs from the oracle"
+    g = orc.decode(got.reshape(-1), xpu.BF16).astype(np.float64).reshape(T, heads, 128)
+    r = orc.decode(ref.reshape(-1), xpu.BF16).astype(np.float64).reshape(T, heads, 128)
+    assert np.all(np.isfinite(g))
+    rel = np.linalg.norm(g - r) / np.linalg.norm(r)
+    rowmax = np.abs(r).max(axis=2, keepdims=True)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(rowmax, 1e-30))) - 7)
+    err = np.abs(g - r)
+    same = float(np.mean(got == ref))
+    print(f"rel-L2 {rel:.3e}, max err / row max {float((err / rowmax).max()):.3e}, identical codes {same:.4f}",
+          flush=True)
+    assert rel <= 1e-2, rel
+    bad = err > 2 * ulp + rowmax / 64
+    assert not bad.any(), (int(bad.sum()), np.argwhere(bad)[:5])

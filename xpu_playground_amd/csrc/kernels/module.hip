@@ -11,4 +11,5 @@ __device__ xpu::StampRecord xpu_stamp_ring[xpu::kStampSlots * xpu::kStampRing];
 #include "synth.hip"
 #include "qwen3_ops.hip"
 #include "gemm.hip"
+#include "prefill_attention.hip"
 #include "peak.hip"

@@ -1,0 +1,238 @@
+// Causal attention of a prompt chunk on MFMA (the GEMM prompt mode of the
+// Qwen3 engine): queries p0 .. p0 + T - 1 of every query head against cache
+// positions 0 .. own position, K and V read from the chunk-major caches
+// [kv_head][16][max_seq][8] that xpu_q3_pf_rope_cache filled.
+//
+// The rounding points are the decode attention's (qwen3/kernels.hpp:157-192
+// as restated by the oracle): s = bf16(bf16(q . k) * scale), the row max M
+// over the bf16 scores, e = exp(s - M) by canonical_exp, the FP32 sum of
+// the e, p = bf16(e * (1 / sum)), out = bf16(sum_t p_t v_t) in FP32. Only
+// the FP32 summation orders differ (the MFMA's), so results agree with the
+// decode path to rounding, not bitwise. Three sweeps over the key tiles: the
+// row max, the sum with that max, then p and P.V (the exact max and sum of
+// the decode path need the scores three times; QK^T is recomputed rather
+// than stored).
+//
+// Block: one kv head, G of its query heads, 128 query rows = 4 wavefronts of
+// 32 (wave w: head w % G, queries 32 (w / G) ..), QT = 128 / G queries. Key
+// tiles of 64 positions staged by LDS-DMA, two stages of K [16 chunks][64
+// keys][8] and V [64 keys][16 chunks, XOR-swizzled][8]. Per wave and tile:
+// S^T = K Q^T as two 32 x 32 MFMA tiles (A: K rows from LDS, B: the wave's Q
+// rows held in registers), so each lane holds 32 scores of one query; O^T
+// += V^T P^T with the lane's own bf16 p as the B operand and V^T fragments
+// from two ds_read_b64_tr_b16 whose row blocks follow the accumulator's key
+// order (4 keys of each half-wave, then 4 more 8 keys on). Keys past the
+// block's last query read as zero (out-of-range DMA offsets); keys past a
+// query's own position are masked before the max, the sum and p.
+#include "device_common.hpp"
+
+namespace xpu {
+namespace pfa {
+
+using dma::bf16x8;
+using dma::f32x16;
+using dma::lds_s16x4;
+
+constexpr uint32_t kKeys = 64;          // keys per tile
+constexpr uint32_t kStage = 32768;      // K (16 KiB) then V (16 KiB)
+constexpr uint32_t kOob = dma::kOob;
+
+XPU_DEVICE f32x16 mfma_bf16(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+template <int G>
+XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ kcache,
+                                  const uint16_t *__restrict__ vcache, uint16_t *__restrict__ out, uint32_t p0,
+                                  uint32_t T, uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float scale) {
+  static_assert(G == 1 || G == 2 || G == 4, "128 query rows per block: 1, 2 or 4 query heads per kv head");
+  constexpr uint32_t QT = 128u / G;
+  __shared__ __align__(1024) uint8_t lds[2 * kStage];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, hh = lane >> 5;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // heaviest query tiles first: block b takes tile n_qt - 1 - b / kv_heads
+  const uint32_t n_qt = (T + QT - 1) / QT;
+  const uint32_t qt = n_qt - 1u - blockIdx.x / kv_heads, kvh = blockIdx.x % kv_heads;
+  const uint32_t head = kvh * G + wave % G;
+  const uint32_t t0 = qt * QT + 32u * (wave / G);  // the wave's first query
+  const uint32_t t = t0 + (lane & 31u);
+  const uint32_t qpos = p0 + t;
+  const uint32_t n_valid = p0 + min(qt * QT + QT, T);  // keys of the block: 0 .. n_valid - 1
+  const uint32_t n_tiles = (n_valid + kKeys - 1) / kKeys;
+  const uint32_t wave_tiles = t0 < T ? (p0 + min(t0 + 31u, T - 1u)) / kKeys + 1u : 0u;
+
+  // the lane's Q row (B operand of S^T): dims 16 ks + 8 hh .. + 7
+  u32x4 qf[8];
+  {
+    const uint16_t *qrow = Q + (static_cast<uint64_t>(min(t, T - 1u)) * heads + head) * kHeadDim;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const u32x4 *>(qrow + (2u * ks + hh) * 8u);
+  }
+
+  const uint64_t head_base = static_cast<uint64_t>(kvh) * max_seq * kHeadDim;
+  const i32x4 rk = rsrc(kcache + head_base, static_cast<int64_t>(max_seq) * kHeadDim * 2);
+  const i32x4 rv = rsrc(vcache + head_base, static_cast<int64_t>(max_seq) * kHeadDim * 2);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+
+  // DMA of key tile `tile` into stage `stage`: K chunk c (wave 4 j) = 64
+  // keys x 16 bytes; V rows 4 i .. 4 i + 3, lane -> (key 4 i + lane / 16,
+  // physical chunk lane % 16 = logical chunk ^ b_swz(key))
+  auto issue = [&](uint32_t tile, uint32_t stage, bool with_v) {
+    const uint32_t k0 = tile * kKeys, sb = lds0 + stage * kStage;
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      const uint32_t c = wave * 4u + j, key = k0 + lane;
+      dma16(sb + c * 1024u, rk, key < n_valid ? (c * max_seq + key) * 16u : kOob);
+    }
+    if (with_v) {
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t i = wave * 4u + j, key = k0 + 4u * i + (lane >> 4);
+        const uint32_t c = (lane & 15u) ^ dma::b_swz(lane >> 4);
+        dma16(sb + 16384u + i * 1024u, rv, key < n_valid ? (c * max_seq + key) * 16u : kOob);
+      }
+    }
+  };
+
+  // S^T of a tile: s[kt] holds keys 32 kt + 8 (r / 4) + 4 hh + r % 4 of the
+  // lane's query (r = register), scaled and rounded as the decode path does
+  auto scores = [&](uint32_t stage, f32x16 (&s)[2]) {
+    const uint32_t kb = lds0 + stage * kStage;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
+#pragma unroll
+    for (uint32_t ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (uint32_t kt = 0; kt < 2; ++kt) {
+        const u32x4 kf = *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(
+            kb + ((2u * ks + hh) * kKeys + 32u * kt + (lane & 31u)) * 16u);
+        s[kt] = mfma_bf16(kf, qf[ks], s[kt]);
+      }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kt][r] = round_bf16(round_bf16(s[kt][r]) * scale);
+  };
+  auto key_of = [&](uint32_t tile, int kt, int r) {
+    return tile * kKeys + 32u * kt + 8u * (r / 4) + 4u * hh + (r % 4);
+  };
+
+  auto sweep = [&](bool with_v, auto &&body) {
+    issue(0, 0, with_v);
+    for (uint32_t i = 0; i < n_tiles; ++i) {
+      wait_vmcnt<0>();
+      __syncthreads();
+      if (i + 1 < n_tiles) issue(i + 1, (i + 1) & 1u, with_v);
+      if (i < wave_tiles) body(i, i & 1u);
+    }
+    __syncthreads();  // the next sweep's first DMA reuses stage 0
+  };
+
+  // 1: row max over the lane's keys, then across the two half-waves
+  float mx = -__builtin_inff();
+  sweep(false, [&](uint32_t tile, uint32_t stage) {
+    f32x16 s[2];
+    scores(stage, s);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (key_of(tile, kt, r) <= qpos) mx = fmaxf(mx, s[kt][r]);
+  });
+  mx = fmaxf(mx, xor32_f(mx));
+
+  // 2: sum of exp(s - M)
+  float sum = 0.0f;
+  sweep(false, [&](uint32_t tile, uint32_t stage) {
+    f32x16 s[2];
+    scores(stage, s);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (key_of(tile, kt, r) <= qpos) sum = sum + canonical_exp(s[kt][r] - mx);
+  });
+  sum = sum + xor32_f(sum);
+  const float inv = 1.0f / sum;
+
+  // 3: p and O^T += V^T P^T; O^T tile dt: dims 32 dt + 8 (r / 4) + 4 hh + r % 4
+  f32x16 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[dt][r] = 0.0f;
+  // tr-read address pieces: lane i of a 16-lane group gives row (i & 15) / 4
+  // of the group's 4-row block, dims 16 ((lane / 16) % 2) + 4 (lane % 4)
+  const uint32_t tr_row = (lane & 15u) >> 2;
+  const uint32_t tr_chunk = 2u * ((lane >> 4) & 1u) + ((lane & 3u) >> 1);
+  const uint32_t tr_half = 8u * (lane & 1u);
+  sweep(true, [&](uint32_t tile, uint32_t stage) {
+    f32x16 s[2];
+    scores(stage, s);
+    uint32_t pk[2][8];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float e0 = key_of(tile, kt, r) <= qpos ? round_bf16(canonical_exp(s[kt][r] - mx) * inv) : 0.0f;
+        const float e1 =
+            key_of(tile, kt, r + 1) <= qpos ? round_bf16(canonical_exp(s[kt][r + 1] - mx) * inv) : 0.0f;
+        pk[kt][r / 2] = dma::cvt_pack<kBf16>(e0, e1);
+      }
+    const uint32_t vb = lds0 + stage * kStage + 16384u;
+#pragma unroll
+    for (uint32_t ks = 0; ks < 4; ++ks) {
+      const uint32_t kt = ks / 2, rb = 4u * (ks % 2);
+      const u32x4 pf = {pk[kt][rb], pk[kt][rb + 1], pk[kt][rb + 2], pk[kt][rb + 3]};
+#pragma unroll
+      for (uint32_t dt = 0; dt < 4; ++dt) {
+        u32x4 vf;
+#pragma unroll
+        for (uint32_t h2 = 0; h2 < 2; ++h2) {
+          const uint32_t row = 16u * ks + 4u * hh + 8u * h2 + tr_row;
+          const uint32_t addr = vb + row * 256u + 16u * ((4u * dt + tr_chunk) ^ dma::b_swz(tr_row)) + tr_half;
+          const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(addr)));
+          if (h2 == 0) {
+            vf.x = v.x;
+            vf.y = v.y;
+          } else {
+            vf.z = v.x;
+            vf.w = v.y;
+          }
+        }
+        o[dt] = mfma_bf16(vf, pf, o[dt]);
+      }
+    }
+  });
+
+  if (t < T && t0 < T) {
+    uint16_t *orow = out + (static_cast<uint64_t>(t) * heads + head) * kHeadDim;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x2 w = {dma::cvt_pack<kBf16>(o[dt][4 * q], o[dt][4 * q + 1]),
+                         dma::cvt_pack<kBf16>(o[dt][4 * q + 2], o[dt][4 * q + 3])};
+        *reinterpret_cast<u32x2 *>(orow + 32u * dt + 8u * q + 4u * hh) = w;
+      }
+  }
+}
+
+}  // namespace pfa
+}  // namespace xpu
+
+// grid: ceil(T / (128 / G)) * kv_heads blocks of 256 threads; heads = G
+// kv_heads; A: [T][heads][128]
+#define XPU_PF_ATTN_MFMA(G)                                                                                   \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_attention_mfma_g##G(                           \
+      const uint16_t *__restrict__ Q, const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, \
+      uint16_t *__restrict__ A, uint32_t p0, uint32_t T, uint32_t heads, uint32_t kv_heads, uint32_t max_seq,  \
+      float scale) {                                                                                          \
+    xpu::pfa::prefill_attention<G>(Q, kcache, vcache, A, p0, T, heads, kv_heads, max_seq, scale);            \
+  }
+XPU_PF_ATTN_MFMA(1)
+XPU_PF_ATTN_MFMA(2)
+XPU_PF_ATTN_MFMA(4)

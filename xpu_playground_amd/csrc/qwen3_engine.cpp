@@ -161,11 +161,11 @@ struct xpu_qwen3 {
   // gemm_prefill: the projections on the MFMA GEMM (pf_gemm_ok when the
   // module has its kernels)
   bool pf_ok = false, batched_prefill = false, pf_gemm_ok = false, gemm_prefill = false;
-  uint32_t pf_chunk = 0;
+  uint32_t pf_chunk = 0, pf_chunk_gemm = 0;
   void *pf_block = nullptr;
   uint16_t *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_a = nullptr,
            *pf_h = nullptr, *pf_gu = nullptr;
-  const xpu::KernelInfo *pf_silu_k = nullptr;
+  const xpu::KernelInfo *pf_silu_k = nullptr, *pf_attn_mfma_k = nullptr;
   const xpu::KernelInfo *pf_attn_short_k = nullptr;  // chunks whose contexts stay within 256 positions
   const xpu::KernelInfo *pf_embed_k = nullptr, *pf_norm_k = nullptr, *pf_rope_k = nullptr, *pf_attn_k = nullptr,
                         *pf_qkv_k = nullptr, *pf_o_k = nullptr, *pf_gu_k = nullptr, *pf_down_k = nullptr;
@@ -373,8 +373,21 @@ int setup_prefill(xpu_qwen3 &e) {
             e.pf_attn_k && c.hidden % 8 == 0 && kpad_bytes(c.hidden) <= e.rt->max_shared &&
             32u * std::max({c.hidden, qd, c.intermediate}) <= e.rt->max_shared;
   if (!e.pf_ok) return XPU_OK;
+  const uint64_t qkv_rows = uint64_t{c.heads + 2 * c.kv_heads} * c.head_dim;
+  // the MFMA form: every projection's K and N multiples of 8 (the NT GEMM
+  // kernels read the weight rows in place) and 1, 2 or 4 query heads per kv
+  // head (the MFMA attention's 128 query rows per block)
+  const uint32_t group = c.heads / c.kv_heads;
+  e.pf_silu_k = e.rt->find_exact("xpu_q3_pf_silu_mul");
+  if (group == 1 || group == 2 || group == 4)
+    e.pf_attn_mfma_k = e.rt->find_exact("xpu_q3_pf_attention_mfma_g" + std::to_string(group));
+  e.pf_gemm_ok = e.pf_silu_k && e.pf_attn_mfma_k && e.rt->find_exact("xpu_gemm_bf16_nt_dma") &&
+                 c.intermediate % 8 == 0 && qd % 8 == 0 && qkv_rows % 8 == 0;
+  // chunks of 256 positions for the batched GEMV form; up to 4096 for the
+  // GEMM form, whose GEMMs and attention fill the chip only with long chunks
   e.pf_chunk = std::min<uint32_t>(e.max_seq, 256);
-  const uint64_t T = e.pf_chunk, qkv_rows = uint64_t{c.heads + 2 * c.kv_heads} * c.head_dim;
+  e.pf_chunk_gemm = e.pf_gemm_ok ? std::min<uint32_t>(e.max_seq, 4096) : 0;
+  const uint64_t T = std::max(e.pf_chunk, e.pf_chunk_gemm);
   const uint64_t sizes[7] = {T * c.hidden, T * c.hidden, T * qkv_rows, T * qd, T * qd, T * c.intermediate,
                              T * 2 * c.intermediate};
   uint64_t total = 0;
@@ -388,11 +401,6 @@ int setup_prefill(xpu_qwen3 &e) {
     p += (sizes[i] * 2 + 255) & ~uint64_t{255};
   }
   e.batched_prefill = true;
-  // the MFMA form: every projection's K and N multiples of 8 (the NT GEMM
-  // kernels read the weight rows in place)
-  e.pf_silu_k = e.rt->find_exact("xpu_q3_pf_silu_mul");
-  e.pf_gemm_ok = e.pf_silu_k && e.rt->find_exact("xpu_gemm_bf16_nt_dma") && c.intermediate % 8 == 0 &&
-                 qd % 8 == 0 && qkv_rows % 8 == 0;
   return XPU_OK;
 }
 
@@ -459,8 +467,9 @@ int enqueue_fused_step(xpu_qwen3 &e, bool split) {
 }
 
 // K/V cache entries of prompt positions [0, P) (prompt ids already in
-// e.prompt), in chunks of pf_chunk positions. The last layer's o_proj and
-// MLP are skipped: only the caches are wanted.
+// e.prompt), in chunks of pf_chunk positions (pf_chunk_gemm in the GEMM
+// form). The last layer's o_proj and MLP are skipped: only the caches are
+// wanted.
 int run_prefill(xpu_qwen3 &e, uint32_t P) {
   const xpu_qwen3_config &c = e.c;
   uint32_t H = c.hidden, I = c.intermediate, V = c.vocab, heads = c.heads, kv = c.kv_heads, max_seq = e.max_seq;
@@ -476,8 +485,9 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
     return rt->launch(*k, gx, gy, block, shared, args.begin(), static_cast<uint32_t>(args.size()));
   };
   int rc;
-  for (uint32_t p0 = 0; p0 < P; p0 += e.pf_chunk) {
-    uint32_t T = std::min(e.pf_chunk, P - p0);
+  const uint32_t chunk = e.gemm_prefill ? e.pf_chunk_gemm : e.pf_chunk;
+  for (uint32_t p0 = 0; p0 < P; p0 += chunk) {
+    uint32_t T = std::min(chunk, P - p0);
     if ((rc = go(e.pf_embed_k, T, 1, 256, 0, {{8, &e.embed}, {8, &e.prompt}, {4, &p0}, {8, &e.pf_x}, {4, &H}, {4, &V}})))
       return rc;
     for (uint32_t l = 0; l < c.layers; ++l) {
@@ -496,11 +506,19 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
                    {{8, &e.pf_qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &kc},
                     {8, &vc}, {8, &e.pf_q}, {4, &p0}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps}})))
         return rc;
-      const bool short_ctx = e.pf_attn_short_k && p0 + T <= 256;  // every token's context within 256 positions
-      if ((rc = go(short_ctx ? e.pf_attn_short_k : e.pf_attn_k, heads, T, 256, 0,
-                   {{8, &e.pf_q}, {8, &kc}, {8, &vc}, {8, &e.pf_a}, {4, &p0}, {4, &heads}, {4, &kv},
-                    {4, &max_seq}, {4, &scale}})))
-        return rc;
+      if (e.gemm_prefill) {
+        const uint32_t qrows = 128 / (heads / kv), blocks = (T + qrows - 1) / qrows * kv;
+        if ((rc = go(e.pf_attn_mfma_k, blocks, 1, 256, 0,
+                     {{8, &e.pf_q}, {8, &kc}, {8, &vc}, {8, &e.pf_a}, {4, &p0}, {4, &T}, {4, &heads}, {4, &kv},
+                      {4, &max_seq}, {4, &scale}})))
+          return rc;
+      } else {
+        const bool short_ctx = e.pf_attn_short_k && p0 + T <= 256;  // every token's context within 256 positions
+        if ((rc = go(short_ctx ? e.pf_attn_short_k : e.pf_attn_k, heads, T, 256, 0,
+                     {{8, &e.pf_q}, {8, &kc}, {8, &vc}, {8, &e.pf_a}, {4, &p0}, {4, &heads}, {4, &kv},
+                      {4, &max_seq}, {4, &scale}})))
+          return rc;
+      }
       if (l + 1 == c.layers) break;
       if (e.gemm_prefill) {
         if ((rc = xpu::gemm_nt(rt, e.pf_a, L.o, e.pf_x, T, H, qd, true))) return rc;
