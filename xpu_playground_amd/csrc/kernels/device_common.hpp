@@ -136,10 +136,14 @@ XPU_DEVICE float wave_butterfly(float s) {
 // operation sequence as orc_exp in the oracle.
 XPU_DEVICE float pow2i(int e) { return __uint_as_float(static_cast<uint32_t>(e + 127) << 23); }
 
+// Written without branches: every case is computed and the result picked by
+// selects in the oracle's order of tests (NaN, overflow, underflow, the
+// subnormal scaling, then the ordinary result), so a wavefront with mixed
+// cases (or masked lanes) runs one straight sequence; the results are the
+// oracle's bit for bit. n is clamped before the integer conversion so that
+// out-of-range inputs convert to a defined value (their results are
+// replaced by the selects).
 XPU_DEVICE float canonical_exp(float x) {
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return __builtin_inff();
-  if (x < -103.972084045410156f) return 0.0f;
   const float n = __builtin_rintf(x * 1.44269502162933349609f);
   float r = __builtin_fmaf(-n, 0.693145751953125f, x);
   r = __builtin_fmaf(-n, 1.42860676533018704504e-06f, r);
@@ -151,10 +155,16 @@ XPU_DEVICE float canonical_exp(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  int e = static_cast<int>(n);
-  if (e > 127) { p = p * 2.0f; e -= 1; }
-  if (e < -126) return (p * pow2i(e + 64)) * 0x1p-64f;
-  return p * pow2i(e);
+  int e = static_cast<int>(__builtin_fminf(__builtin_fmaxf(n, -200.0f), 200.0f));
+  const bool top = e > 127;
+  p = top ? p * 2.0f : p;
+  e = top ? e - 1 : e;
+  const float normal = p * pow2i(e < -126 ? 0 : e);
+  const float sub = (p * pow2i(e < -126 ? e + 64 : 0)) * 0x1p-64f;
+  float res = e < -126 ? sub : normal;
+  res = x < -103.972084045410156f ? 0.0f : res;
+  res = x > 88.72283935546875f ? __builtin_inff() : res;
+  return x != x ? x : res;
 }
 
 XPU_DEVICE u32x4 load_nt16(const void *p) {

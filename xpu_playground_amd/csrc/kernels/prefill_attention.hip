@@ -8,10 +8,9 @@
 // over the bf16 scores, e = exp(s - M) by canonical_exp, the FP32 sum of
 // the e, p = bf16(e * (1 / sum)), out = bf16(sum_t p_t v_t) in FP32. Only
 // the FP32 summation orders differ (the MFMA's), so results agree with the
-// decode path to rounding, not bitwise. Three sweeps over the key tiles: the
-// row max, the sum with that max, then p and P.V (the exact max and sum of
-// the decode path need the scores three times; QK^T is recomputed rather
-// than stored).
+// decode path to rounding, not bitwise. Two sweeps over the key tiles: the
+// row max with the sum of exp(s - max) (rescaled as the max grows), then p
+// and P.V; QK^T is recomputed in the second sweep rather than stored.
 //
 // Block: one kv head, G of its query heads, 128 query rows = 4 wavefronts of
 // 32 (wave w: head w % G, queries 32 (w / G) ..), QT = 128 / G queries. Key
@@ -131,34 +130,46 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     __syncthreads();  // the next sweep's first DMA reuses stage 0
   };
 
-  // 1: row max over the lane's keys, then across the two half-waves
-  float mx = -__builtin_inff();
+  // 1: the row max M and the sum of exp(s - M) in one sweep: per lane a
+  // running max m and sum, the sum rescaled by exp(m_old - m_new) when the
+  // max grows; then the two half-waves' (m, sum) pairs are merged. The max is
+  // exact; the sum is the decode path's up to FP32 rounding of the rescaled
+  // terms.
+  const float ninf = -__builtin_inff();
+  float mx = ninf, sum = 0.0f;
   sweep(false, [&](uint32_t tile, uint32_t stage) {
     f32x16 s[2];
     scores(stage, s);
+    float tmax = ninf;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (key_of(tile, kt, r) <= qpos) mx = fmaxf(mx, s[kt][r]);
-  });
-  mx = fmaxf(mx, xor32_f(mx));
-
-  // 2: sum of exp(s - M)
-  float sum = 0.0f;
-  sweep(false, [&](uint32_t tile, uint32_t stage) {
-    f32x16 s[2];
-    scores(stage, s);
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, key_of(tile, kt, r) <= qpos ? s[kt][r] : ninf);
+    const float m_new = fmaxf(mx, tmax);
+    float part = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (key_of(tile, kt, r) <= qpos) sum = sum + canonical_exp(s[kt][r] - mx);
+      for (int r = 0; r < 16; ++r) {
+        const float ex = canonical_exp(s[kt][r] - m_new);
+        part = part + (key_of(tile, kt, r) <= qpos ? ex : 0.0f);
+      }
+    // no valid key yet (m_new = -inf): part is 0 and the sum stays 0
+    const float rescale = canonical_exp(mx - m_new);
+    sum = mx == ninf ? part : sum * rescale + part;
+    mx = m_new;
   });
-  sum = sum + xor32_f(sum);
+  {
+    const float m_other = xor32_f(mx), s_other = xor32_f(sum);
+    const float m_row = fmaxf(mx, m_other);
+    const float own = mx == ninf ? 0.0f : sum * canonical_exp(mx - m_row);
+    const float other = m_other == ninf ? 0.0f : s_other * canonical_exp(m_other - m_row);
+    sum = own + other;  // the same two terms, in either order, in both half-waves
+    mx = m_row;
+  }
   const float inv = 1.0f / sum;
 
-  // 3: p and O^T += V^T P^T; O^T tile dt: dims 32 dt + 8 (r / 4) + 4 hh + r % 4
+  // 2: p and O^T += V^T P^T; O^T tile dt: dims 32 dt + 8 (r / 4) + 4 hh + r % 4
   f32x16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -177,10 +188,10 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const float e0 = key_of(tile, kt, r) <= qpos ? round_bf16(canonical_exp(s[kt][r] - mx) * inv) : 0.0f;
-        const float e1 =
-            key_of(tile, kt, r + 1) <= qpos ? round_bf16(canonical_exp(s[kt][r + 1] - mx) * inv) : 0.0f;
-        pk[kt][r / 2] = dma::cvt_pack<kBf16>(e0, e1);
+        const float e0 = round_bf16(canonical_exp(s[kt][r] - mx) * inv);
+        const float e1 = round_bf16(canonical_exp(s[kt][r + 1] - mx) * inv);
+        pk[kt][r / 2] = dma::cvt_pack<kBf16>(key_of(tile, kt, r) <= qpos ? e0 : 0.0f,
+                                             key_of(tile, kt, r + 1) <= qpos ? e1 : 0.0f);
       }
     const uint32_t vb = lds0 + stage * kStage + 16384u;
 #pragma unroll
