@@ -167,6 +167,31 @@ XPU_DEVICE float canonical_exp(float x) {
   return x != x ? x : res;
 }
 
+// canonical_exp for x <= 0 (a softmax's s - max), the same bits with fewer
+// operations: NaN, overflow and the e > 127 adjustment cannot occur, and
+// the result is always formed as (p * 2^(e + 64)) * 2^-64, which is the
+// subnormal path itself and, for a normal result, equal to p * 2^e (both
+// products are exact power-of-two scalings). Inputs above 0 give
+// unspecified finite-or-infinite values.
+XPU_DEVICE float canonical_exp_nonpos(float x) {
+  const float n = __builtin_rintf(x * 1.44269502162933349609f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.42860676533018704504e-06f, r);
+  float p = 1.98412698412698412526e-04f;
+  p = __builtin_fmaf(p, r, 1.38888888888888894189e-03f);
+  p = __builtin_fmaf(p, r, 8.33333333333333321769e-03f);
+  p = __builtin_fmaf(p, r, 4.16666666666666643537e-02f);
+  p = __builtin_fmaf(p, r, 1.66666666666666657415e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  // -151 <= n <= 0 wherever the result is used; the clamp keeps the
+  // conversion and the exponent arithmetic defined for the rest
+  const int e = static_cast<int>(__builtin_fminf(__builtin_fmaxf(n, -160.0f), 60.0f));
+  const float res = (p * pow2i(e + 64)) * 0x1p-64f;
+  return x < -103.972084045410156f ? 0.0f : res;
+}
+
 XPU_DEVICE u32x4 load_nt16(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 }

@@ -25,6 +25,8 @@
 // query's own position are masked before the max, the sum and p.
 #include "device_common.hpp"
 
+#include <type_traits>
+
 namespace xpu {
 namespace pfa {
 
@@ -110,14 +112,27 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
             kb + ((2u * ks + hh) * kKeys + 32u * kt + (lane & 31u)) * 16u);
         s[kt] = mfma_bf16(kf, qf[ks], s[kt]);
       }
+    // bf16(bf16(q . k) * scale), the roundings by v_cvt_pk_bf16_f32 (RNE,
+    // the bits of f32_to_bf16 for finite values)
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[kt][r] = round_bf16(round_bf16(s[kt][r]) * scale);
+      for (int r = 0; r < 16; r += 2) {
+        const uint32_t w = dma::cvt_pack<kBf16>(s[kt][r], s[kt][r + 1]);
+        const uint32_t w2 = dma::cvt_pack<kBf16>(lo16<kBf16>(w) * scale, hi16<kBf16>(w) * scale);
+        s[kt][r] = lo16<kBf16>(w2);
+        s[kt][r + 1] = hi16<kBf16>(w2);
+      }
   };
-  auto key_of = [&](uint32_t tile, int kt, int r) {
-    return tile * kKeys + 32u * kt + 8u * (r / 4) + 4u * hh + (r % 4);
+  // Masks: key 32 kt + 8 (r / 4) + 4 hh + r % 4 of the tile is valid for the
+  // lane's query when that offset <= lim = qpos - (first key + 4 hh). Only
+  // the tiles that reach past the wave's first query position need them
+  // (the diagonal ones); the others run the unmasked body.
+  auto lim_of = [&](uint32_t tile) {
+    return static_cast<int32_t>(qpos) - static_cast<int32_t>(tile * kKeys + 4u * hh);
   };
+  auto valid = [](int32_t lim, int kt, int r) { return 32 * kt + 8 * (r / 4) + (r % 4) <= lim; };
+  auto diagonal = [&](uint32_t tile) { return tile * kKeys + kKeys - 1u > p0 + t0; };
 
   auto sweep = [&](bool with_v, auto &&body) {
     issue(0, 0, with_v);
@@ -125,7 +140,10 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
       wait_vmcnt<0>();
       __syncthreads();
       if (i + 1 < n_tiles) issue(i + 1, (i + 1) & 1u, with_v);
-      if (i < wave_tiles) body(i, i & 1u);
+      if (i < wave_tiles) {
+        if (diagonal(i)) body(i, i & 1u, std::true_type{});
+        else body(i, i & 1u, std::false_type{});
+      }
     }
     __syncthreads();  // the next sweep's first DMA reuses stage 0
   };
@@ -137,33 +155,34 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
   // terms.
   const float ninf = -__builtin_inff();
   float mx = ninf, sum = 0.0f;
-  sweep(false, [&](uint32_t tile, uint32_t stage) {
+  sweep(false, [&](uint32_t tile, uint32_t stage, auto diag) {
     f32x16 s[2];
     scores(stage, s);
+    const int32_t lim = lim_of(tile);
     float tmax = ninf;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, key_of(tile, kt, r) <= qpos ? s[kt][r] : ninf);
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, !diag || valid(lim, kt, r) ? s[kt][r] : ninf);
     const float m_new = fmaxf(mx, tmax);
     float part = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float ex = canonical_exp(s[kt][r] - m_new);
-        part = part + (key_of(tile, kt, r) <= qpos ? ex : 0.0f);
+        const float ex = canonical_exp_nonpos(s[kt][r] - m_new);
+        part = part + (!diag || valid(lim, kt, r) ? ex : 0.0f);
       }
     // no valid key yet (m_new = -inf): part is 0 and the sum stays 0
-    const float rescale = canonical_exp(mx - m_new);
+    const float rescale = canonical_exp_nonpos(mx - m_new);
     sum = mx == ninf ? part : sum * rescale + part;
     mx = m_new;
   });
   {
     const float m_other = xor32_f(mx), s_other = xor32_f(sum);
     const float m_row = fmaxf(mx, m_other);
-    const float own = mx == ninf ? 0.0f : sum * canonical_exp(mx - m_row);
-    const float other = m_other == ninf ? 0.0f : s_other * canonical_exp(m_other - m_row);
+    const float own = mx == ninf ? 0.0f : sum * canonical_exp_nonpos(mx - m_row);
+    const float other = m_other == ninf ? 0.0f : s_other * canonical_exp_nonpos(m_other - m_row);
     sum = own + other;  // the same two terms, in either order, in both half-waves
     mx = m_row;
   }
@@ -180,18 +199,20 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
   const uint32_t tr_row = (lane & 15u) >> 2;
   const uint32_t tr_chunk = 2u * ((lane >> 4) & 1u) + ((lane & 3u) >> 1);
   const uint32_t tr_half = 8u * (lane & 1u);
-  sweep(true, [&](uint32_t tile, uint32_t stage) {
+  sweep(true, [&](uint32_t tile, uint32_t stage, auto diag) {
     f32x16 s[2];
     scores(stage, s);
+    const int32_t lim = lim_of(tile);
+    // p = bf16(exp(s - M) * inv): the packing conversion is the rounding
     uint32_t pk[2][8];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const float e0 = round_bf16(canonical_exp(s[kt][r] - mx) * inv);
-        const float e1 = round_bf16(canonical_exp(s[kt][r + 1] - mx) * inv);
-        pk[kt][r / 2] = dma::cvt_pack<kBf16>(key_of(tile, kt, r) <= qpos ? e0 : 0.0f,
-                                             key_of(tile, kt, r + 1) <= qpos ? e1 : 0.0f);
+        const float e0 = canonical_exp_nonpos(s[kt][r] - mx) * inv;
+        const float e1 = canonical_exp_nonpos(s[kt][r + 1] - mx) * inv;
+        pk[kt][r / 2] = dma::cvt_pack<kBf16>(!diag || valid(lim, kt, r) ? e0 : 0.0f,
+                                             !diag || valid(lim, kt, r + 1) ? e1 : 0.0f);
       }
     const uint32_t vb = lds0 + stage * kStage + 16384u;
 #pragma unroll
