@@ -45,7 +45,8 @@ def run_case(rt, p0, T, heads, kv, max_seq, q_gain, seed):
             try:
                 rt.memset(da, 0xFF, T * heads * 128 * 2)
                 if name.startswith("xpu_q3_pf_attention_mfma"):
-                    blocks = (T + 128 // g - 1) // (128 // g) * kv
+                    qt = 64 if g == 1 else 32  # queries per block
+                    blocks = (T + qt - 1) // qt * kv
                     args = Args().ptr(dq).ptr(dk).ptr(dv).ptr(da).u32(p0).u32(T).u32(heads).u32(kv).u32(max_seq)
                     print(f"{name} p0={p0} T={T} heads={heads} kv={kv} blocks={blocks}", flush=True)
                     rt.launch_grid(name, blocks, 256, 0, args.f32(scale))

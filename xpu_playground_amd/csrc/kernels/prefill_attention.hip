@@ -12,10 +12,14 @@
 // row max with the sum of exp(s - max) (rescaled as the max grows), then p
 // and P.V; QK^T is recomputed in the second sweep rather than stored.
 //
-// Block: one kv head, G of its query heads, 128 query rows = 4 wavefronts of
-// 32 (wave w: head w % G, queries 32 (w / G) ..), QT = 128 / G queries. Key
-// tiles of 64 positions staged by LDS-DMA, two stages of K [16 chunks][64
-// keys][8] and V [64 keys][16 chunks, XOR-swizzled][8]. Per wave and tile:
+// Block: one kv head, 4 wavefronts of 32 query rows each: G query heads x
+// U query sub-tiles x H key halves (G U H = 4; QT = 32 U queries). Key
+// tiles of 64 positions: half h takes tiles h, h + H, ..., so the causal
+// work of a block is spread over its waves, and the halves merge their
+// (max, sum) after the first sweep and their FP32 partial outputs after the
+// second through LDS, in half order. Tiles are staged by LDS-DMA, two stages
+// of H tile slots of K [16 chunks][64 keys][8] and V [64 keys][16 chunks,
+// XOR-swizzled][8]. Per wave and tile:
 // S^T = K Q^T as two 32 x 32 MFMA tiles (A: K rows from LDS, B: the wave's Q
 // rows held in registers), so each lane holds 32 scores of one query; O^T
 // += V^T P^T with the lane's own bf16 p as the B operand and V^T fragments
@@ -43,20 +47,23 @@ XPU_DEVICE f32x16 mfma_bf16(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
                                                  0, 0, 0);
 }
 
-template <int G>
+template <int G, int H>
 XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ kcache,
                                   const uint16_t *__restrict__ vcache, uint16_t *__restrict__ out, uint32_t p0,
                                   uint32_t T, uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float scale) {
-  static_assert(G == 1 || G == 2 || G == 4, "128 query rows per block: 1, 2 or 4 query heads per kv head");
-  constexpr uint32_t QT = 128u / G;
-  __shared__ __align__(1024) uint8_t lds[2 * kStage];
+  static_assert((G == 1 || G == 2 || G == 4) && (H == 1 || H == 2) && 4 % (G * H) == 0,
+                "4 wavefronts: G query heads x U query sub-tiles x H key halves");
+  constexpr uint32_t U = 4u / (G * H), QT = 32u * U, kSlots = G * U;  // waves per half
+  __shared__ __align__(1024) uint8_t lds[2 * H * kStage];
+  __shared__ float merge[H][kSlots][2][64];  // (max, sum) of each half's waves
   const uint32_t tid = threadIdx.x, lane = tid & 63u, hh = lane >> 5;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t half = wave / kSlots, slot = wave % kSlots;
   // heaviest query tiles first: block b takes tile n_qt - 1 - b / kv_heads
   const uint32_t n_qt = (T + QT - 1) / QT;
   const uint32_t qt = n_qt - 1u - blockIdx.x / kv_heads, kvh = blockIdx.x % kv_heads;
-  const uint32_t head = kvh * G + wave % G;
-  const uint32_t t0 = qt * QT + 32u * (wave / G);  // the wave's first query
+  const uint32_t head = kvh * G + slot % G;
+  const uint32_t t0 = qt * QT + 32u * (slot / G);  // the wave's first query
   const uint32_t t = t0 + (lane & 31u);
   const uint32_t qpos = p0 + t;
   const uint32_t n_valid = p0 + min(qt * QT + QT, T);  // keys of the block: 0 .. n_valid - 1
@@ -76,11 +83,11 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
   const i32x4 rv = rsrc(vcache + head_base, static_cast<int64_t>(max_seq) * kHeadDim * 2);
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
 
-  // DMA of key tile `tile` into stage `stage`: K chunk c (wave 4 j) = 64
-  // keys x 16 bytes; V rows 4 i .. 4 i + 3, lane -> (key 4 i + lane / 16,
-  // physical chunk lane % 16 = logical chunk ^ b_swz(key))
-  auto issue = [&](uint32_t tile, uint32_t stage, bool with_v) {
-    const uint32_t k0 = tile * kKeys, sb = lds0 + stage * kStage;
+  // DMA of key tile `tile` into slot `slot_of` of a stage: K chunk c (wave
+  // 4 j) = 64 keys x 16 bytes; V rows 4 i .. 4 i + 3, lane -> (key 4 i +
+  // lane / 16, physical chunk lane % 16 = logical chunk ^ b_swz(key))
+  auto issue_tile = [&](uint32_t tile, uint32_t sb, bool with_v) {
+    const uint32_t k0 = tile * kKeys;
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) {
       const uint32_t c = wave * 4u + j, key = k0 + lane;
@@ -95,11 +102,17 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
       }
     }
   };
+  // step i of a sweep: tiles H i .. H i + H - 1 into stage i % 2
+  const uint32_t n_steps = (n_tiles + H - 1) / H;
+  auto issue = [&](uint32_t step, bool with_v) {
+#pragma unroll
+    for (uint32_t h = 0; h < H; ++h)
+      if (H * step + h < n_tiles) issue_tile(H * step + h, lds0 + ((step & 1u) * H + h) * kStage, with_v);
+  };
 
   // S^T of a tile: s[kt] holds keys 32 kt + 8 (r / 4) + 4 hh + r % 4 of the
   // lane's query (r = register), scaled and rounded as the decode path does
-  auto scores = [&](uint32_t stage, f32x16 (&s)[2]) {
-    const uint32_t kb = lds0 + stage * kStage;
+  auto scores = [&](uint32_t kb, f32x16 (&s)[2]) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -134,15 +147,18 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
   auto valid = [](int32_t lim, int kt, int r) { return 32 * kt + 8 * (r / 4) + (r % 4) <= lim; };
   auto diagonal = [&](uint32_t tile) { return tile * kKeys + kKeys - 1u > p0 + t0; };
 
+  // body(tile, stage byte address of the tile, diagonal?) for the wave's
+  // tiles: H step + half
   auto sweep = [&](bool with_v, auto &&body) {
-    issue(0, 0, with_v);
-    for (uint32_t i = 0; i < n_tiles; ++i) {
+    issue(0, with_v);
+    for (uint32_t i = 0; i < n_steps; ++i) {
       wait_vmcnt<0>();
       __syncthreads();
-      if (i + 1 < n_tiles) issue(i + 1, (i + 1) & 1u, with_v);
-      if (i < wave_tiles) {
-        if (diagonal(i)) body(i, i & 1u, std::true_type{});
-        else body(i, i & 1u, std::false_type{});
+      if (i + 1 < n_steps) issue(i + 1, with_v);
+      const uint32_t tile = H * i + half, sb = lds0 + ((i & 1u) * H + half) * kStage;
+      if (tile < wave_tiles) {
+        if (diagonal(tile)) body(tile, sb, std::true_type{});
+        else body(tile, sb, std::false_type{});
       }
     }
     __syncthreads();  // the next sweep's first DMA reuses stage 0
@@ -155,9 +171,9 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
   // terms.
   const float ninf = -__builtin_inff();
   float mx = ninf, sum = 0.0f;
-  sweep(false, [&](uint32_t tile, uint32_t stage, auto diag) {
+  sweep(false, [&](uint32_t tile, uint32_t sb, auto diag) {
     f32x16 s[2];
-    scores(stage, s);
+    scores(sb, s);
     const int32_t lim = lim_of(tile);
     float tmax = ninf;
 #pragma unroll
@@ -178,13 +194,24 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     sum = mx == ninf ? part : sum * rescale + part;
     mx = m_new;
   });
-  {
-    const float m_other = xor32_f(mx), s_other = xor32_f(sum);
-    const float m_row = fmaxf(mx, m_other);
-    const float own = mx == ninf ? 0.0f : sum * canonical_exp_nonpos(mx - m_row);
-    const float other = m_other == ninf ? 0.0f : s_other * canonical_exp_nonpos(m_other - m_row);
-    sum = own + other;  // the same two terms, in either order, in both half-waves
-    mx = m_row;
+  // merge two (max, sum) pairs: the same two terms in either order
+  auto merge2 = [&](float &m, float &sm, float m2, float s2) {
+    const float m_row = fmaxf(m, m2);
+    const float a = m == ninf ? 0.0f : sm * canonical_exp_nonpos(m - m_row);
+    const float b = m2 == ninf ? 0.0f : s2 * canonical_exp_nonpos(m2 - m_row);
+    sm = a + b;
+    m = m_row;
+  };
+  merge2(mx, sum, xor32_f(mx), xor32_f(sum));  // the two half-waves
+  if constexpr (H > 1) {
+    // the key halves, merged in half order by every wave alike
+    merge[half][slot][0][lane] = mx;
+    merge[half][slot][1][lane] = sum;
+    __syncthreads();
+    mx = merge[0][slot][0][lane];
+    sum = merge[0][slot][1][lane];
+#pragma unroll
+    for (uint32_t h = 1; h < H; ++h) merge2(mx, sum, merge[h][slot][0][lane], merge[h][slot][1][lane]);
   }
   const float inv = 1.0f / sum;
 
@@ -199,9 +226,9 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
   const uint32_t tr_row = (lane & 15u) >> 2;
   const uint32_t tr_chunk = 2u * ((lane >> 4) & 1u) + ((lane & 3u) >> 1);
   const uint32_t tr_half = 8u * (lane & 1u);
-  sweep(true, [&](uint32_t tile, uint32_t stage, auto diag) {
+  sweep(true, [&](uint32_t tile, uint32_t sb, auto diag) {
     f32x16 s[2];
-    scores(stage, s);
+    scores(sb, s);
     const int32_t lim = lim_of(tile);
     // p = bf16(exp(s - M) * inv): the packing conversion is the rounding
     uint32_t pk[2][8];
@@ -214,7 +241,7 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
         pk[kt][r / 2] = dma::cvt_pack<kBf16>(!diag || valid(lim, kt, r) ? e0 : 0.0f,
                                              !diag || valid(lim, kt, r + 1) ? e1 : 0.0f);
       }
-    const uint32_t vb = lds0 + stage * kStage + 16384u;
+    const uint32_t vb = sb + 16384u;
 #pragma unroll
     for (uint32_t ks = 0; ks < 4; ++ks) {
       const uint32_t kt = ks / 2, rb = 4u * (ks % 2);
@@ -240,6 +267,25 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     }
   });
 
+  if constexpr (H > 1) {
+    // half h > 0 leaves its partial O^T in the (now idle) stage memory; half
+    // 0 adds them in half order
+    float *po = reinterpret_cast<float *>(lds);
+    if (half > 0) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) po[(((half - 1) * kSlots + slot) * 64 + dt * 16 + r) * 64 + lane] = o[dt][r];
+    }
+    __syncthreads();
+    if (half > 0) return;
+#pragma unroll
+    for (uint32_t h = 1; h < H; ++h)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] + po[(((h - 1) * kSlots + slot) * 64 + dt * 16 + r) * 64 + lane];
+  }
   if (t < T && t0 < T) {
     uint16_t *orow = out + (static_cast<uint64_t>(t) * heads + head) * kHeadDim;
 #pragma unroll
@@ -256,15 +302,15 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
 }  // namespace pfa
 }  // namespace xpu
 
-// grid: ceil(T / (128 / G)) * kv_heads blocks of 256 threads; heads = G
-// kv_heads; A: [T][heads][128]
-#define XPU_PF_ATTN_MFMA(G)                                                                                   \
+// grid: ceil(T / QT) * kv_heads blocks of 256 threads (QT = 64 for G = 1,
+// 32 for G = 2 and 4); heads = G kv_heads; A: [T][heads][128]
+#define XPU_PF_ATTN_MFMA(G, H)                                                                                \
   extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_attention_mfma_g##G(                           \
       const uint16_t *__restrict__ Q, const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, \
       uint16_t *__restrict__ A, uint32_t p0, uint32_t T, uint32_t heads, uint32_t kv_heads, uint32_t max_seq,  \
       float scale) {                                                                                          \
-    xpu::pfa::prefill_attention<G>(Q, kcache, vcache, A, p0, T, heads, kv_heads, max_seq, scale);            \
+    xpu::pfa::prefill_attention<G, H>(Q, kcache, vcache, A, p0, T, heads, kv_heads, max_seq, scale);         \
   }
-XPU_PF_ATTN_MFMA(1)
-XPU_PF_ATTN_MFMA(2)
-XPU_PF_ATTN_MFMA(4)
+XPU_PF_ATTN_MFMA(1, 2)
+XPU_PF_ATTN_MFMA(2, 2)
+XPU_PF_ATTN_MFMA(4, 1)

@@ -507,7 +507,9 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
                     {8, &vc}, {8, &e.pf_q}, {4, &p0}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps}})))
         return rc;
       if (e.gemm_prefill) {
-        const uint32_t qrows = 128 / (heads / kv), blocks = (T + qrows - 1) / qrows * kv;
+        // queries per block: 32 U, U = 4 / (G H) with H = 2 key halves for
+        // G = 1 and 2, 1 for G = 4
+        const uint32_t qrows = heads / kv == 1 ? 64 : 32, blocks = (T + qrows - 1) / qrows * kv;
         if ((rc = go(e.pf_attn_mfma_k, blocks, 1, 256, 0,
                      {{8, &e.pf_q}, {8, &kc}, {8, &vc}, {8, &e.pf_a}, {4, &p0}, {4, &T}, {4, &heads}, {4, &kv},
                       {4, &max_seq}, {4, &scale}})))
