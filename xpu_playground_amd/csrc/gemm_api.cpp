@@ -170,12 +170,19 @@ int gemm_nt(xpu_runtime *rt, const void *A, const void *W, void *C, uint32_t M, 
   const GemmTile &tile = choose_tile(rt->compute_units, M, N);
   const uint32_t slices = (K + 63) / 64;
   const bool odd = tile.tag[0] == '\0' && slices % 2 == 1 && slices >= 3;
-  const std::string name = std::string("xpu_gemm_bf16") + tile.tag + (odd ? "_odd" : "") + "_nt" +
-                           (residual ? "_res" : "") + "_dma";
+  auto count = [&](uint32_t rows, uint32_t cols) {
+    return ((static_cast<uint64_t>(M) + rows - 1) / rows) * ((static_cast<uint64_t>(N) + cols - 1) / cols);
+  };
+  uint64_t tiles = count(tile.rows, tile.cols);
+  std::string tag = tile.tag;
+  // 128 x 64 tiles where even 128 x 128 ones leave compute units idle
+  if (tag == "_t128" && tiles < rt->compute_units) {
+    tag = "_n64";
+    tiles = count(128, 64);
+  }
+  const std::string name = "xpu_gemm_bf16" + tag + (odd ? "_odd" : "") + "_nt" + (residual ? "_res" : "") + "_dma";
   const xpu::KernelInfo *k = rt->find_exact(name);
   if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: " + name);
-  const uint64_t tiles = ((static_cast<uint64_t>(M) + tile.rows - 1) / tile.rows) *
-                         ((static_cast<uint64_t>(N) + tile.cols - 1) / tile.cols);
   uint32_t kb = K, ldc = N, n_out = N;
   const xpu_kernel_arg args[] = {{8, &A}, {8, &W}, {8, &C}, {4, &M}, {4, &N}, {4, &K}, {4, &kb}, {4, &ldc}, {4, &n_out}};
   return rt->launch(*k, static_cast<uint32_t>(tiles), 1, 256, 0, args, 9);

@@ -136,7 +136,7 @@ template <int MI, int NJ, int BK, int S, bool BT = false> struct Cfg {
   static constexpr uint32_t kEpBytes = 4u * 64u * kEpPitch * 4u;
   static constexpr uint32_t kLds = S * kStage > kEpBytes ? S * kStage : kEpBytes;
   static_assert(kLds <= 160u * 1024u, "LDS");
-  static_assert(kBCpr == 16 || kBCpr == 32, "B rows of 16 or 32 chunks (the swizzle permutes 16)");
+  static_assert(BT || kBCpr == 16 || kBCpr == 32, "[k][n] B rows of 16 or 32 chunks (the swizzle permutes 16)");
   static_assert(MI == 2 || MI == 4, "64-row epilogue bands");
   static_assert(kDmaA >= 1, "every wave issues A DMA");
 };
@@ -542,6 +542,10 @@ XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_dma, 2, 4, 4, 1, false, false)
 XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_res_dma, 2, 4, 4, 1, false, true)
 XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_dma, 2, 2, 2, 2, false, false)
 XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_res_dma, 2, 2, 2, 2, false, true)
+// 128 x 64 ([n][k] weights only): outputs that leave compute units idle even
+// with 128 x 128 tiles (a 1024-wide projection of a few thousand tokens)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_dma, 2, 1, 1, 2, false, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_res_dma, 2, 1, 1, 2, false, true)
 
 // 256 x 256: BK = 64, two stages, barrier after 4 MFMAs of a slice's last
 // k-step, each slice's DMA spread over two k-steps; _odd for an odd number
