@@ -198,6 +198,48 @@ XPU_DEVICE void head_norm_rope_vec(const u32x4 &xv, const u32x4 &wv, const u32x4
   }
 }
 
+// head_norm_rope_vec for four head rows per wavefront, one per 16-lane row
+// (local lane l = lane % 16 holds elements 8 l..8 l + 7; every lane
+// active). The sum of squares folds each lane's 8 slots and then runs the
+// butterfly's l ^ 8, 4, 2, 1 steps within the row: the single-row form's
+// l ^ 32 and l ^ 16 steps only add the idle lanes' zeros to a sum of
+// squares (x + 0 = x), so the result is the same bits.
+XPU_DEVICE void head_norm_rope_rows16(const u32x4 &xv, const u32x4 &wv, const u32x4 &cv, const u32x4 &sv,
+                                      float eps, uint16_t *roped_out, uint64_t out_chunk = 8) {
+  const uint32_t l16 = lane_id() & 15u;
+  float x[8], wf[8];
+  unpack8<kBf16>(xv, x);
+  unpack8<kBf16>(wv, wf);
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(x[e], x[e], 0.0f);
+  float ss = fold8(acc);
+  ss = ss + xor8_f(ss);
+  ss = ss + dpp_f<0x124>(ss);  // row_ror:4 (the values depend on l % 8 only)
+  ss = ss + dpp_f<0x4E>(ss);   // quad_perm [2,3,0,1]
+  ss = ss + dpp_f<0xB1>(ss);   // quad_perm [1,0,3,2]
+  const float scale = 1.0f / __builtin_sqrtf(ss / static_cast<float>(kHeadDim) + eps);
+  float n[8], p[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) n[e] = round_bf16(wf[e] * round_bf16(x[e] * scale));
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = xor8_f(n[e]);
+  float cf[8], sf[8];
+  unpack8<kBf16>(cv, cf);
+  unpack8<kBf16>(sv, sf);
+  uint32_t codes[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float rot = l16 < 8 ? -p[e] : p[e];
+    const float a = round_bf16(n[e] * cf[e]);
+    const float b = round_bf16(rot * sf[e]);
+    codes[e] = f32_to_bf16(a + b);
+  }
+  *reinterpret_cast<u32x4 *>(roped_out + l16 * out_chunk) =
+      u32x4{codes[0] | (codes[1] << 16), codes[2] | (codes[3] << 16), codes[4] | (codes[5] << 16),
+            codes[6] | (codes[7] << 16)};
+}
+
 XPU_DEVICE float block_max(float v, float *red) {
   v = wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
   const uint32_t wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;

@@ -1331,35 +1331,37 @@ XPU_Q3_PF_GEMV(2, 2, 2)
 XPU_Q3_PF_GEMV(2, 2, 4)
 XPU_Q3_PF_GEMV(2, 2, 8)
 
-// QK-norm + RoPE of every token of the chunk: block (h, t), one wavefront.
-// h < heads: roped q of head h into Q[t]; else kv head h - heads: roped k
-// and the v row into the engine caches at position p0 + t.
-extern "C" __global__ __launch_bounds__(64) void xpu_q3_pf_rope_cache(
+// QK-norm + RoPE of every token of the chunk: 16 head rows per 256-thread
+// block, one per 16 lanes; row r = t (heads + kv_heads) + h of the T
+// (heads + kv_heads) rows. h < heads: roped q of head h into Q[t]; else kv
+// head h - heads: roped k and the v row into the engine caches at position
+// p0 + t.
+extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_rope_cache(
     const uint16_t *__restrict__ QKV, const uint16_t *__restrict__ qnorm_w, const uint16_t *__restrict__ knorm_w,
     const uint16_t *__restrict__ rope_cos, const uint16_t *__restrict__ rope_sin, uint16_t *__restrict__ kcache,
-    uint16_t *__restrict__ vcache, uint16_t *__restrict__ Q, uint32_t p0, uint32_t heads, uint32_t kv_heads,
-    uint32_t max_seq, float eps) {
-  const uint32_t h = blockIdx.x, t = blockIdx.y, pos = p0 + t, lane = xpu::lane_id();
+    uint16_t *__restrict__ vcache, uint16_t *__restrict__ Q, uint32_t p0, uint32_t T, uint32_t heads,
+    uint32_t kv_heads, uint32_t max_seq, float eps) {
+  const uint32_t nh = heads + kv_heads, l16 = threadIdx.x & 15u;
+  // rows past the last are clamped onto it (recomputed, stored identically)
+  const uint32_t r = min(blockIdx.x * 16u + (threadIdx.x >> 4), T * nh - 1u);
+  const uint32_t t = r / nh, h = r % nh, pos = p0 + t;
   const uint32_t row_len = (heads + 2 * kv_heads) * xpu::kHeadDim;
   const uint16_t *row = QKV + static_cast<uint64_t>(t) * row_len;
   const bool is_q = h < heads;
   const uint32_t kvh = is_q ? 0 : h - heads;
-  const uint16_t *src = is_q ? row + h * xpu::kHeadDim : row + (heads + kvh) * xpu::kHeadDim;
-  u32x4 hx = {0, 0, 0, 0}, hw = {0, 0, 0, 0}, hc = {0, 0, 0, 0}, hs = {0, 0, 0, 0};
-  if (lane < 16) {
-    hx = *reinterpret_cast<const u32x4 *>(src + lane * 8u);
-    hw = *reinterpret_cast<const u32x4 *>((is_q ? qnorm_w : knorm_w) + lane * 8u);
-    hc = *reinterpret_cast<const u32x4 *>(rope_cos + static_cast<uint64_t>(pos) * xpu::kHeadDim + lane * 8u);
-    hs = *reinterpret_cast<const u32x4 *>(rope_sin + static_cast<uint64_t>(pos) * xpu::kHeadDim + lane * 8u);
-  }
+  const uint16_t *src = row + h * xpu::kHeadDim;  // q heads, then k heads
+  const u32x4 hx = *reinterpret_cast<const u32x4 *>(src + l16 * 8u);
+  const u32x4 hw = *reinterpret_cast<const u32x4 *>((is_q ? qnorm_w : knorm_w) + l16 * 8u);
+  const u32x4 hc = *reinterpret_cast<const u32x4 *>(rope_cos + static_cast<uint64_t>(pos) * xpu::kHeadDim + l16 * 8u);
+  const u32x4 hs = *reinterpret_cast<const u32x4 *>(rope_sin + static_cast<uint64_t>(pos) * xpu::kHeadDim + l16 * 8u);
   // K and V: chunk-major [kv_head][16][max_seq][8]
   const uint64_t kslot = static_cast<uint64_t>(kvh) * max_seq * xpu::kHeadDim + static_cast<uint64_t>(pos) * 8u;
   uint16_t *dst = is_q ? Q + static_cast<uint64_t>(t) * heads * xpu::kHeadDim + h * xpu::kHeadDim : kcache + kslot;
-  xpu::head_norm_rope_vec(hx, hw, hc, hs, eps, dst, is_q ? 8u : static_cast<uint64_t>(max_seq) * 8u);
-  if (!is_q && lane < 16) {
+  xpu::head_norm_rope_rows16(hx, hw, hc, hs, eps, dst, is_q ? 8u : static_cast<uint64_t>(max_seq) * 8u);
+  if (!is_q) {
     const uint16_t *vsrc = row + (heads + kv_heads + kvh) * xpu::kHeadDim;
-    *reinterpret_cast<u32x4 *>(vcache + kslot + lane * static_cast<uint64_t>(max_seq) * 8u) =
-        *reinterpret_cast<const u32x4 *>(vsrc + lane * 8u);
+    *reinterpret_cast<u32x4 *>(vcache + kslot + l16 * static_cast<uint64_t>(max_seq) * 8u) =
+        *reinterpret_cast<const u32x4 *>(vsrc + l16 * 8u);
   }
 }
 

@@ -502,9 +502,9 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
                           {{8, &L.qkv}, {8, &e.pf_xn}, {8, &e.pf_qkv}, {4, &qkv_rows}, {4, &T}}))) {
         return rc;
       }
-      if ((rc = go(e.pf_rope_k, heads + kv, T, 64, 0,
+      if ((rc = go(e.pf_rope_k, (T * (heads + kv) + 15) / 16, 1, 256, 0,
                    {{8, &e.pf_qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &kc},
-                    {8, &vc}, {8, &e.pf_q}, {4, &p0}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps}})))
+                    {8, &vc}, {8, &e.pf_q}, {4, &p0}, {4, &T}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps}})))
         return rc;
       if (e.gemm_prefill) {
         // queries per block: 32 U, U = 4 / (G H) with H = 2 key halves for
