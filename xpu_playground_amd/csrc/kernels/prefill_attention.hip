@@ -6,9 +6,11 @@
 // The rounding points are the decode attention's (qwen3/kernels.hpp:157-192
 // as restated by the oracle): s = bf16(bf16(q . k) * scale), the row max M
 // over the bf16 scores, e = exp(s - M) by canonical_exp, the FP32 sum of
-// the e, p = bf16(e * (1 / sum)), out = bf16(sum_t p_t v_t) in FP32. Only
-// the FP32 summation orders differ (the MFMA's), so results agree with the
-// decode path to rounding, not bitwise. Two sweeps over the key tiles: the
+// the e, p = bf16(e * (1 / sum)), out = bf16(sum_t p_t v_t) in FP32. The
+// FP32 summation orders differ (the MFMA's), and the denominator's terms
+// are the hardware's exp2 (v_exp_f32 of (s - m) log2 e, a few FP32 ulps from
+// canonical_exp), so results agree with the decode path to rounding, not
+// bitwise; the max and each p's exponential are the decode path's. Two sweeps over the key tiles: the
 // row max with the sum of exp(s - max) (rescaled as the max grows), then p
 // and P.V; QK^T is recomputed in the second sweep rather than stored.
 //
@@ -138,17 +140,23 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
       }
   };
   // Masks: key 32 kt + 8 (r / 4) + 4 hh + r % 4 of the tile is valid for the
-  // lane's query when that offset <= lim = qpos - (first key + 4 hh). Only
-  // the tiles that reach past the wave's first query position need them
-  // (the diagonal ones); the others run the unmasked body.
-  auto lim_of = [&](uint32_t tile) {
-    return static_cast<int32_t>(qpos) - static_cast<int32_t>(tile * kKeys + 4u * hh);
+  // lane's query when that offset <= qpos - (first key + 4 hh). Only the
+  // tiles that reach past the wave's first query position (the diagonal
+  // ones) have invalid keys; there the invalid scores become -inf, which
+  // leaves the max alone and whose exponentials are 0.
+  const float ninf = -__builtin_inff();
+  auto mask_scores = [&](uint32_t tile, f32x16 (&s)[2]) {
+    if (__builtin_expect(tile * kKeys + kKeys - 1u <= p0 + t0, 1)) return;  // wave-uniform
+    const int32_t lim = static_cast<int32_t>(qpos) - static_cast<int32_t>(tile * kKeys + 4u * hh);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (32 * kt + 8 * (r / 4) + (r % 4) > lim) s[kt][r] = ninf;
   };
-  auto valid = [](int32_t lim, int kt, int r) { return 32 * kt + 8 * (r / 4) + (r % 4) <= lim; };
-  auto diagonal = [&](uint32_t tile) { return tile * kKeys + kKeys - 1u > p0 + t0; };
 
-  // body(tile, stage byte address of the tile, diagonal?) for the wave's
-  // tiles: H step + half
+  // body(tile, stage byte address of the tile) for the wave's tiles:
+  // H step + half
   auto sweep = [&](bool with_v, auto &&body) {
     issue(0, with_v);
     for (uint32_t i = 0; i < n_steps; ++i) {
@@ -156,10 +164,7 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
       __syncthreads();
       if (i + 1 < n_steps) issue(i + 1, with_v);
       const uint32_t tile = H * i + half, sb = lds0 + ((i & 1u) * H + half) * kStage;
-      if (tile < wave_tiles) {
-        if (diagonal(tile)) body(tile, sb, std::true_type{});
-        else body(tile, sb, std::false_type{});
-      }
+      if (tile < wave_tiles) body(tile, sb);
     }
     __syncthreads();  // the next sweep's first DMA reuses stage 0
   };
@@ -167,38 +172,35 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
   // 1: the row max M and the sum of exp(s - M) in one sweep: per lane a
   // running max m and sum, the sum rescaled by exp(m_old - m_new) when the
   // max grows; then the two half-waves' (m, sum) pairs are merged. The max is
-  // exact; the sum is the decode path's up to FP32 rounding of the rescaled
-  // terms.
-  const float ninf = -__builtin_inff();
+  // exact; the sum's terms and factors use the hardware exp2.
+  constexpr float kLog2e = 1.44269504088896340736f;
+  auto exp_hw = [&](float x) { return __builtin_amdgcn_exp2f(x * kLog2e); };
   float mx = ninf, sum = 0.0f;
-  sweep(false, [&](uint32_t tile, uint32_t sb, auto diag) {
+  sweep(false, [&](uint32_t tile, uint32_t sb) {
     f32x16 s[2];
     scores(sb, s);
-    const int32_t lim = lim_of(tile);
+    mask_scores(tile, s);
     float tmax = ninf;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, !diag || valid(lim, kt, r) ? s[kt][r] : ninf);
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kt][r]);
     const float m_new = fmaxf(mx, tmax);
     float part = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float ex = canonical_exp_nonpos(s[kt][r] - m_new);
-        part = part + (!diag || valid(lim, kt, r) ? ex : 0.0f);
-      }
-    // no valid key yet (m_new = -inf): part is 0 and the sum stays 0
-    const float rescale = canonical_exp_nonpos(mx - m_new);
-    sum = mx == ninf ? part : sum * rescale + part;
+      for (int r = 0; r < 16; ++r) part = part + exp_hw(s[kt][r] - m_new);
+    // no valid key yet (m_new = -inf, every s - m_new NaN): the sum stays 0
+    const float rescale = exp_hw(mx - m_new);
+    sum = m_new == ninf ? 0.0f : (mx == ninf ? part : sum * rescale + part);
     mx = m_new;
   });
   // merge two (max, sum) pairs: the same two terms in either order
   auto merge2 = [&](float &m, float &sm, float m2, float s2) {
     const float m_row = fmaxf(m, m2);
-    const float a = m == ninf ? 0.0f : sm * canonical_exp_nonpos(m - m_row);
-    const float b = m2 == ninf ? 0.0f : s2 * canonical_exp_nonpos(m2 - m_row);
+    const float a = m == ninf ? 0.0f : sm * exp_hw(m - m_row);
+    const float b = m2 == ninf ? 0.0f : s2 * exp_hw(m2 - m_row);
     sm = a + b;
     m = m_row;
   };
@@ -226,21 +228,20 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
   const uint32_t tr_row = (lane & 15u) >> 2;
   const uint32_t tr_chunk = 2u * ((lane >> 4) & 1u) + ((lane & 3u) >> 1);
   const uint32_t tr_half = 8u * (lane & 1u);
-  sweep(true, [&](uint32_t tile, uint32_t sb, auto diag) {
+  sweep(true, [&](uint32_t tile, uint32_t sb) {
     f32x16 s[2];
     scores(sb, s);
-    const int32_t lim = lim_of(tile);
+    mask_scores(tile, s);
     // p = bf16(exp(s - M) * inv): the packing conversion is the rounding
+    // (M is finite: position 0 is every query's key; masked s - M = -inf
+    // gives 0)
     uint32_t pk[2][8];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float e0 = canonical_exp_nonpos(s[kt][r] - mx) * inv;
-        const float e1 = canonical_exp_nonpos(s[kt][r + 1] - mx) * inv;
-        pk[kt][r / 2] = dma::cvt_pack<kBf16>(!diag || valid(lim, kt, r) ? e0 : 0.0f,
-                                             !diag || valid(lim, kt, r + 1) ? e1 : 0.0f);
-      }
+      for (int r = 0; r < 16; r += 2)
+        pk[kt][r / 2] = dma::cvt_pack<kBf16>(canonical_exp_nonpos(s[kt][r] - mx) * inv,
+                                             canonical_exp_nonpos(s[kt][r + 1] - mx) * inv);
     const uint32_t vb = sb + 16384u;
 #pragma unroll
     for (uint32_t ks = 0; ks < 4; ++ks) {
