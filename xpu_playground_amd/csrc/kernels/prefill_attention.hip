@@ -5,12 +5,14 @@
 //
 // The rounding points are the decode attention's (qwen3/kernels.hpp:157-192
 // as restated by the oracle): s = bf16(bf16(q . k) * scale), the row max M
-// over the bf16 scores, e = exp(s - M) by canonical_exp, the FP32 sum of
-// the e, p = bf16(e * (1 / sum)), out = bf16(sum_t p_t v_t) in FP32. The
-// FP32 summation orders differ (the MFMA's), and the denominator's terms
-// are the hardware's exp2 (v_exp_f32 of (s - m) log2 e, a few FP32 ulps from
-// canonical_exp), so results agree with the decode path to rounding, not
-// bitwise; the max and each p's exponential are the decode path's. Two sweeps over the key tiles: the
+// over the bf16 scores, e = exp(s - M), the FP32 sum of the e, p = bf16(e *
+// (1 / sum)), out = bf16(sum_t p_t v_t) in FP32. Two things differ from the
+// decode path, which is bit-exact against the CPU oracle: the FP32
+// summation orders (the MFMA's), and the exponential, here the hardware's
+// exp2 (v_exp_f32 of (s - M) log2 e, a few FP32 ulps from the oracle's
+// canonical_exp; the reference's own kernel uses the device exp too). So
+// results agree with the decode path to rounding, not bitwise; the max is
+// exact. Two sweeps over the key tiles: the
 // row max with the sum of exp(s - max) (rescaled as the max grows), then p
 // and P.V; QK^T is recomputed in the second sweep rather than stored.
 //
@@ -171,8 +173,7 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
 
   // 1: the row max M and the sum of exp(s - M) in one sweep: per lane a
   // running max m and sum, the sum rescaled by exp(m_old - m_new) when the
-  // max grows; then the two half-waves' (m, sum) pairs are merged. The max is
-  // exact; the sum's terms and factors use the hardware exp2.
+  // max grows; then the two half-waves' (m, sum) pairs are merged.
   constexpr float kLog2e = 1.44269504088896340736f;
   auto exp_hw = [&](float x) { return __builtin_amdgcn_exp2f(x * kLog2e); };
   float mx = ninf, sum = 0.0f;
@@ -240,8 +241,7 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; r += 2)
-        pk[kt][r / 2] = dma::cvt_pack<kBf16>(canonical_exp_nonpos(s[kt][r] - mx) * inv,
-                                             canonical_exp_nonpos(s[kt][r + 1] - mx) * inv);
+        pk[kt][r / 2] = dma::cvt_pack<kBf16>(exp_hw(s[kt][r] - mx) * inv, exp_hw(s[kt][r + 1] - mx) * inv);
     const uint32_t vb = sb + 16384u;
 #pragma unroll
     for (uint32_t ks = 0; ks < 4; ++ks) {
