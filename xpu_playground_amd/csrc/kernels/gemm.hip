@@ -321,18 +321,19 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     for (uint32_t op = lo + x * (hi - lo) / nx; op < lo + (x + 1) * (hi - lo) / nx; ++op) dma(d, op);
   };
   Frags frag[2];
-  static_assert(S == 2, "pairs of slices");
-  // Slice s lives in LDS stage s % 2. Prologue: slice 0 whole, and the first
-  // part of slice 1 as if its barrier had just passed; the rest of slice 1
-  // follows during slice 0 like any slice's DMA.
-  {
-    const Slice d = slice_of(0, 0);
+  static_assert(S == 2 || (S == 4 && !ODD), "groups of 2 or 4 slices; the odd tail follows a pair");
+  // Slice s lives in LDS stage s % S. Prologue: slices 0 .. S - 2 whole, and
+  // the first part of slice S - 1 as if its barrier had just passed; the
+  // rest of slice S - 1 follows during slice 0 like any slice's DMA.
+#pragma unroll
+  for (uint32_t s = 0; s + 1 < S; ++s) {
+    const Slice d = slice_of(s, s);
 #pragma unroll
     for (uint32_t op = 0; op < G::kDma; ++op) dma(d, op);
   }
-  Slice pend = slice_of(1, 1);
+  Slice pend = slice_of(S - 1, S - 1);
   dma_part(pend, 0, 0, 1);
-  wait_vmcnt<G::kDma / D>();
+  wait_vmcnt<(S - 2) * G::kDma + G::kDma / D>();  // slice 0 landed
   __syncthreads();
 #pragma unroll
   for (uint32_t r = 0; r < G::kReads; ++r) read(0, 0, frag[0], r);
@@ -386,18 +387,24 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
         }
       }
   };
-  // Whole pairs of slices (one exit keeps the accumulators in place); a
-  // pair's second slice past nk reads zeros and adds nothing. With ODD the
-  // pairs stop before the last slice, which follows on its own (stage 0, its
-  // DMA and barrier already done by the last pair): the MFMAs of its k-steps
+  // Whole groups of S slices (one exit keeps the accumulators in place); a
+  // group's slices past nk read zeros and add nothing. With ODD the pairs
+  // stop before the last slice, which follows on its own (stage 0, its DMA
+  // and barrier already done by the last pair): the MFMAs of its k-steps
   // that start below K, with the next k-step's fragment reads.
   using St0 = std::integral_constant<uint32_t, 0>;
   using St1 = std::integral_constant<uint32_t, 1>;
+  using St2 = std::integral_constant<uint32_t, 2>;
+  using St3 = std::integral_constant<uint32_t, 3>;
   // (at least one pair: ODD kernels take nk >= 3)
   uint32_t s0 = 0;
   do {
     slice_step(St0{}, s0);
     slice_step(St1{}, s0);
+    if constexpr (S == 4) {
+      slice_step(St2{}, s0);
+      slice_step(St3{}, s0);
+    }
     s0 += S;
   } while (s0 < (ODD ? nk - 1 : nk));
   if constexpr (ODD) {
@@ -527,25 +534,28 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 
 // C = A W^T with W given [N][K] (BT) for the batched prompt projections, bf16,
 // 16-byte aligned C; _res adds into C (residual)
-#define XPU_GEMM_NT_VARIANT(NAME, MI, NJ, P, MINB, ODD, RES)                                      \
+#define XPU_GEMM_NT_VARIANT(NAME, MI, NJ, S, P, MINB, ODD, RES)                                   \
   extern "C" __global__ __launch_bounds__(256, MINB) void NAME(                               \
       const uint16_t *__restrict__ A, const uint16_t *__restrict__ W, uint16_t *__restrict__ C, \
       uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {         \
     XPU_STAMP(xpu::kStampGemm);                                                                 \
-    xpu::dma::body<xpu::kBf16, MI, NJ, 64, 2, P, 2, true, ODD, true, RES>(A, W, C, M, N, K, kb, ldc, n_out); \
+    xpu::dma::body<xpu::kBf16, MI, NJ, 64, S, P, 2, true, ODD, true, RES>(A, W, C, M, N, K, kb, ldc, n_out); \
   }
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_nt_dma, 4, 4, 4, 1, false, false)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_nt_res_dma, 4, 4, 4, 1, false, true)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_odd_nt_dma, 4, 4, 4, 1, true, false)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_odd_nt_res_dma, 4, 4, 4, 1, true, true)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_dma, 2, 4, 4, 1, false, false)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_res_dma, 2, 4, 4, 1, false, true)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_dma, 2, 2, 2, 2, false, false)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_res_dma, 2, 2, 2, 2, false, true)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_nt_dma, 4, 4, 2, 4, 1, false, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_nt_res_dma, 4, 4, 2, 4, 1, false, true)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_odd_nt_dma, 4, 4, 2, 4, 1, true, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_odd_nt_res_dma, 4, 4, 2, 4, 1, true, true)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_dma, 2, 4, 2, 4, 1, false, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_res_dma, 2, 4, 2, 4, 1, false, true)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_dma, 2, 2, 2, 2, 2, false, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_res_dma, 2, 2, 2, 2, 2, false, true)
 // 128 x 64 ([n][k] weights only): outputs that leave compute units idle even
-// with 128 x 128 tiles (a 1024-wide projection of a few thousand tokens)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_dma, 2, 1, 1, 2, false, false)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_res_dma, 2, 1, 1, 2, false, true)
+// with 128 x 128 tiles (a 1024-wide projection of a few thousand tokens).
+// Its slices are short (8 MFMAs per wavefront), so four stages keep three
+// slices in flight to cover the memory latency; groups of 4 slices (K past
+// the last whole group reads zeros).
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_dma, 2, 1, 4, 1, 2, false, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_res_dma, 2, 1, 4, 1, 2, false, true)
 
 // 256 x 256: BK = 64, two stages, barrier after 4 MFMAs of a slice's last
 // k-step, each slice's DMA spread over two k-steps; _odd for an odd number
