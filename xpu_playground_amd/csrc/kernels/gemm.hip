@@ -321,7 +321,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     for (uint32_t op = lo + x * (hi - lo) / nx; op < lo + (x + 1) * (hi - lo) / nx; ++op) dma(d, op);
   };
   Frags frag[2];
-  static_assert(S == 2 || (S == 4 && !ODD), "groups of 2 or 4 slices; the odd tail follows a pair");
+  static_assert(S == 2 || ((S == 3 || S == 4) && !ODD), "groups of 2 to 4 slices; the odd tail follows a pair");
   // Slice s lives in LDS stage s % S. Prologue: slices 0 .. S - 2 whole, and
   // the first part of slice S - 1 as if its barrier had just passed; the
   // rest of slice S - 1 follows during slice 0 like any slice's DMA.
@@ -401,10 +401,8 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   do {
     slice_step(St0{}, s0);
     slice_step(St1{}, s0);
-    if constexpr (S == 4) {
-      slice_step(St2{}, s0);
-      slice_step(St3{}, s0);
-    }
+    if constexpr (S >= 3) slice_step(St2{}, s0);
+    if constexpr (S == 4) slice_step(St3{}, s0);
     s0 += S;
   } while (s0 < (ODD ? nk - 1 : nk));
   if constexpr (ODD) {
@@ -545,8 +543,9 @@ XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_nt_dma, 4, 4, 2, 4, 1, false, false)
 XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_nt_res_dma, 4, 4, 2, 4, 1, false, true)
 XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_odd_nt_dma, 4, 4, 2, 4, 1, true, false)
 XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_odd_nt_res_dma, 4, 4, 2, 4, 1, true, true)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_dma, 2, 4, 2, 4, 1, false, false)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_res_dma, 2, 4, 2, 4, 1, false, true)
+// 128 x 256 with three stages (two slices in flight)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_dma, 2, 4, 3, 4, 1, false, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_m128_nt_res_dma, 2, 4, 3, 4, 1, false, true)
 XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_dma, 2, 2, 2, 2, 2, false, false)
 XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_res_dma, 2, 2, 2, 2, 2, false, true)
 // 128 x 64 ([n][k] weights only): outputs that leave compute units idle even
