@@ -122,9 +122,10 @@ int xpu_qwen3_set_mode(xpu_qwen3 *eng, int mode);
  *     prompt positions before the last run as one batch per layer with the
  *     same arithmetic as the decode step, so the KV caches, tokens and
  *     logits are bit-identical to stepwise;
- *   2 gemm: as batched, with the four projections on the MFMA GEMM (FP32
- *     accumulation in the GEMM's k-order, so the caches differ from
- *     stepwise by rounding: within the GEMM's error bound, not bitwise).
+ *   2 gemm: as batched in chunks of up to 4096 positions, with the four
+ *     projections on the MFMA GEMM and the causal attention on MFMA (FP32
+ *     sums in the MFMA's order, the hardware exp), so the caches differ
+ *     from stepwise by rounding, not bitwise.
  * XPU_ERR_INVALID for another mode or a mode without kernels for the
  * shape. The reference has no batched prompt path. */
 int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int mode);
