@@ -1113,16 +1113,40 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_embed(const uint16_t
   for (uint32_t i = threadIdx.x; i < H; i += blockDim.x) X[static_cast<uint64_t>(t) * H + i] = src[i];
 }
 
-// Xn[t] = rmsnorm(X[t]) * w (the decode kernels' prologue, block_rmsnorm_vec)
+// Xn[t] = rmsnorm(X[t]) * w, one wavefront per token (4 per 256-thread
+// block, grid ceil(T / 4)); H a multiple of 8, X, w, Xn 16-byte aligned.
+// The operations of block_rmsnorm_vec in the same order: lane l accumulates
+// the squares of elements 512 c + 8 l + slot over chunks c in order (a
+// missing tail reads as zeros, as that kernel's zero padding), then fold8
+// and the 64-lane butterfly; out = bf16(w * bf16(x * scale)). The second
+// pass re-reads x and w (cache hits).
 extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_rmsnorm(const uint16_t *__restrict__ X,
                                                                     const uint16_t *__restrict__ w,
-                                                                    uint16_t *__restrict__ Xn, uint32_t H, float eps) {
-  extern __shared__ __align__(16) uint16_t xs[];
-  __shared__ float red[1];
-  const uint64_t row = static_cast<uint64_t>(blockIdx.x) * H;
-  xpu::block_rmsnorm_vec(xs, X + row, w, H, eps, red);
-  for (uint32_t i = threadIdx.x * 8u; i < H; i += blockDim.x * 8u)
-    *reinterpret_cast<u32x4 *>(Xn + row + i) = *reinterpret_cast<const u32x4 *>(xs + i);
+                                                                    uint16_t *__restrict__ Xn, uint32_t H, float eps,
+                                                                    uint32_t T) {
+  const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6), lane = xpu::lane_id();
+  if (t >= T) return;  // whole wavefronts
+  const uint16_t *x = X + static_cast<uint64_t>(t) * H;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (uint32_t j = lane * 8u; j < H; j += 512u) {
+    float f[8];
+    xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const u32x4 *>(x + j), f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(f[e], f[e], acc[e]);
+  }
+  const float ss = xpu::wave_butterfly(xpu::fold8(acc));
+  const float scale = 1.0f / __builtin_sqrtf(ss / static_cast<float>(H) + eps);
+  uint16_t *out = Xn + static_cast<uint64_t>(t) * H;
+  for (uint32_t j = lane * 8u; j < H; j += 512u) {
+    float xf[8], wf[8];
+    xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const u32x4 *>(x + j), xf);
+    xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const u32x4 *>(w + j), wf);
+    uint32_t c[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c[e] = xpu::f32_to_bf16(wf[e] * xpu::round_bf16(xf[e] * scale));
+    *reinterpret_cast<u32x4 *>(out + j) =
+        u32x4{c[0] | (c[1] << 16), c[2] | (c[3] << 16), c[4] | (c[5] << 16), c[6] | (c[7] << 16)};
+  }
 }
 
 // Hb[t][i] = bf16(bf16(silu(g)) u) for g = GU[t][i], u = GU[t][I + i]: the
@@ -1332,19 +1356,19 @@ XPU_Q3_PF_GEMV(2, 2, 4)
 XPU_Q3_PF_GEMV(2, 2, 8)
 
 // QK-norm + RoPE of every token of the chunk: 16 head rows per 256-thread
-// block, one per 16 lanes; row r = t (heads + kv_heads) + h of the T
-// (heads + kv_heads) rows. h < heads: roped q of head h into Q[t]; else kv
-// head h - heads: roped k and the v row into the engine caches at position
-// p0 + t.
+// block, one per 16 lanes: head h of tokens 16 b .. 16 b + 15 for block
+// (b, h) (grid ceil(T / 16) x (heads + kv_heads)), so a chunk's cache
+// writes of a wavefront are 64 contiguous bytes. h < heads: roped q of head
+// h into Q[t]; else kv head h - heads: roped k and the v row into the
+// engine caches at position p0 + t.
 extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_rope_cache(
     const uint16_t *__restrict__ QKV, const uint16_t *__restrict__ qnorm_w, const uint16_t *__restrict__ knorm_w,
     const uint16_t *__restrict__ rope_cos, const uint16_t *__restrict__ rope_sin, uint16_t *__restrict__ kcache,
     uint16_t *__restrict__ vcache, uint16_t *__restrict__ Q, uint32_t p0, uint32_t T, uint32_t heads,
     uint32_t kv_heads, uint32_t max_seq, float eps) {
-  const uint32_t nh = heads + kv_heads, l16 = threadIdx.x & 15u;
-  // rows past the last are clamped onto it (recomputed, stored identically)
-  const uint32_t r = min(blockIdx.x * 16u + (threadIdx.x >> 4), T * nh - 1u);
-  const uint32_t t = r / nh, h = r % nh, pos = p0 + t;
+  const uint32_t l16 = threadIdx.x & 15u, h = blockIdx.y;
+  // tokens past the last are clamped onto it (recomputed, stored identically)
+  const uint32_t t = min(blockIdx.x * 16u + (threadIdx.x >> 4), T - 1u), pos = p0 + t;
   const uint32_t row_len = (heads + 2 * kv_heads) * xpu::kHeadDim;
   const uint16_t *row = QKV + static_cast<uint64_t>(t) * row_len;
   const bool is_q = h < heads;

@@ -493,8 +493,8 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
     for (uint32_t l = 0; l < c.layers; ++l) {
       const Layer &L = e.layers[l];
       uint16_t *kc = e.kcache + l * cache_layer, *vc = e.vcache + l * cache_layer;
-      if ((rc = go(e.pf_norm_k, T, 1, 256, kpad_bytes(H),
-                   {{8, &e.pf_x}, {8, &L.in_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}})))
+      if ((rc = go(e.pf_norm_k, (T + 3) / 4, 1, 256, 0,
+                   {{8, &e.pf_x}, {8, &L.in_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}, {4, &T}})))
         return rc;
       if (e.gemm_prefill) {
         if ((rc = xpu::gemm_nt(rt, e.pf_xn, L.qkv, e.pf_qkv, T, qkv_rows, H, false))) return rc;
@@ -502,7 +502,7 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
                           {{8, &L.qkv}, {8, &e.pf_xn}, {8, &e.pf_qkv}, {4, &qkv_rows}, {4, &T}}))) {
         return rc;
       }
-      if ((rc = go(e.pf_rope_k, (T * (heads + kv) + 15) / 16, 1, 256, 0,
+      if ((rc = go(e.pf_rope_k, (T + 15) / 16, heads + kv, 256, 0,
                    {{8, &e.pf_qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &kc},
                     {8, &vc}, {8, &e.pf_q}, {4, &p0}, {4, &T}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps}})))
         return rc;
@@ -528,8 +528,8 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
                           {{8, &L.o}, {8, &e.pf_a}, {8, &e.pf_x}, {4, &H}, {4, &T}}))) {
         return rc;
       }
-      if ((rc = go(e.pf_norm_k, T, 1, 256, kpad_bytes(H),
-                   {{8, &e.pf_x}, {8, &L.post_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}})))
+      if ((rc = go(e.pf_norm_k, (T + 3) / 4, 1, 256, 0,
+                   {{8, &e.pf_x}, {8, &L.post_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}, {4, &T}})))
         return rc;
       if (e.gemm_prefill) {
         const uint32_t two_i = 2 * I, silu_grid = std::min<uint32_t>((T * (I / 8) + 255) / 256, 4096);
