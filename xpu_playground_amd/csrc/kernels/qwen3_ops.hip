@@ -1118,17 +1118,34 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_embed(const uint16_t
 // The operations of block_rmsnorm_vec in the same order: lane l accumulates
 // the squares of elements 512 c + 8 l + slot over chunks c in order (a
 // missing tail reads as zeros, as that kernel's zero padding), then fold8
-// and the 64-lane butterfly; out = bf16(w * bf16(x * scale)). The second
-// pass re-reads x and w (cache hits).
+// and the 64-lane butterfly; out = bf16(w * bf16(x * scale)). The first
+// kRegChunks chunks of x and w are loaded once, up front, and kept in
+// registers; wider rows re-read the rest.
 extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_rmsnorm(const uint16_t *__restrict__ X,
                                                                     const uint16_t *__restrict__ w,
                                                                     uint16_t *__restrict__ Xn, uint32_t H, float eps,
                                                                     uint32_t T) {
+  constexpr uint32_t kRegChunks = 8;
   const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6), lane = xpu::lane_id();
   if (t >= T) return;  // whole wavefronts
   const uint16_t *x = X + static_cast<uint64_t>(t) * H;
+  u32x4 xv[kRegChunks], wv[kRegChunks];
+#pragma unroll
+  for (uint32_t c = 0; c < kRegChunks; ++c) {
+    const uint32_t j = c * 512u + lane * 8u;
+    xv[c] = j < H ? *reinterpret_cast<const u32x4 *>(x + j) : u32x4{0, 0, 0, 0};
+    wv[c] = j < H ? *reinterpret_cast<const u32x4 *>(w + j) : u32x4{0, 0, 0, 0};
+  }
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (uint32_t j = lane * 8u; j < H; j += 512u) {
+#pragma unroll
+  for (uint32_t c = 0; c < kRegChunks; ++c) {
+    if (c * 512u >= H) break;  // uniform
+    float f[8];
+    xpu::unpack8<xpu::kBf16>(xv[c], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(f[e], f[e], acc[e]);
+  }
+  for (uint32_t j = kRegChunks * 512u + lane * 8u; j < H; j += 512u) {
     float f[8];
     xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const u32x4 *>(x + j), f);
 #pragma unroll
@@ -1137,16 +1154,23 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_rmsnorm(const uint16
   const float ss = xpu::wave_butterfly(xpu::fold8(acc));
   const float scale = 1.0f / __builtin_sqrtf(ss / static_cast<float>(H) + eps);
   uint16_t *out = Xn + static_cast<uint64_t>(t) * H;
-  for (uint32_t j = lane * 8u; j < H; j += 512u) {
+  auto emit = [&](const u32x4 &xq, const u32x4 &wq, uint32_t j) {
     float xf[8], wf[8];
-    xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const u32x4 *>(x + j), xf);
-    xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const u32x4 *>(w + j), wf);
+    xpu::unpack8<xpu::kBf16>(xq, xf);
+    xpu::unpack8<xpu::kBf16>(wq, wf);
     uint32_t c[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) c[e] = xpu::f32_to_bf16(wf[e] * xpu::round_bf16(xf[e] * scale));
     *reinterpret_cast<u32x4 *>(out + j) =
         u32x4{c[0] | (c[1] << 16), c[2] | (c[3] << 16), c[4] | (c[5] << 16), c[6] | (c[7] << 16)};
+  };
+#pragma unroll
+  for (uint32_t c = 0; c < kRegChunks; ++c) {
+    const uint32_t j = c * 512u + lane * 8u;
+    if (j < H) emit(xv[c], wv[c], j);
   }
+  for (uint32_t j = kRegChunks * 512u + lane * 8u; j < H; j += 512u)
+    emit(*reinterpret_cast<const u32x4 *>(x + j), *reinterpret_cast<const u32x4 *>(w + j), j);
 }
 
 // Hb[t][i] = bf16(bf16(silu(g)) u) for g = GU[t][i], u = GU[t][I + i]: the
