@@ -321,7 +321,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     for (uint32_t op = lo + x * (hi - lo) / nx; op < lo + (x + 1) * (hi - lo) / nx; ++op) dma(d, op);
   };
   Frags frag[2];
-  static_assert(S == 2 || ((S == 3 || S == 4) && !ODD), "groups of 2 to 4 slices; the odd tail follows a pair");
+  static_assert(S == 2 || (S >= 3 && S <= 6 && !ODD), "groups of 2 to 6 slices; the odd tail follows a pair");
   // Slice s lives in LDS stage s % S. Prologue: slices 0 .. S - 2 whole, and
   // the first part of slice S - 1 as if its barrier had just passed; the
   // rest of slice S - 1 follows during slice 0 like any slice's DMA.
@@ -392,17 +392,19 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   // stop before the last slice, which follows on its own (stage 0, its DMA
   // and barrier already done by the last pair): the MFMAs of its k-steps
   // that start below K, with the next k-step's fragment reads.
-  using St0 = std::integral_constant<uint32_t, 0>;
-  using St1 = std::integral_constant<uint32_t, 1>;
-  using St2 = std::integral_constant<uint32_t, 2>;
-  using St3 = std::integral_constant<uint32_t, 3>;
+  // stage constants 0 .. S - 1 (a stage index past S - 1 is never run)
+  auto step_if = [&](auto stc, uint32_t s) {
+    if constexpr (decltype(stc)::value < S) slice_step(stc, s);
+  };
   // (at least one pair: ODD kernels take nk >= 3)
   uint32_t s0 = 0;
   do {
-    slice_step(St0{}, s0);
-    slice_step(St1{}, s0);
-    if constexpr (S >= 3) slice_step(St2{}, s0);
-    if constexpr (S == 4) slice_step(St3{}, s0);
+    step_if(std::integral_constant<uint32_t, 0>{}, s0);
+    step_if(std::integral_constant<uint32_t, 1>{}, s0);
+    step_if(std::integral_constant<uint32_t, 2>{}, s0);
+    step_if(std::integral_constant<uint32_t, 3>{}, s0);
+    step_if(std::integral_constant<uint32_t, 4>{}, s0);
+    step_if(std::integral_constant<uint32_t, 5>{}, s0);
     s0 += S;
   } while (s0 < (ODD ? nk - 1 : nk));
   if constexpr (ODD) {
