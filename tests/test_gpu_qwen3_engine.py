@@ -326,15 +326,22 @@ def test_mode_switch_mid_sequence_is_rejected(rt):
     eng.close()
 
 
-@pytest.mark.parametrize("n_prompt,max_seq", [(40, 96), (300, 320), (2, 16)])
-def test_gemm_prefill_within_rounding(rt, n_prompt, max_seq):
+# "small" also has the batched GEMV form; "tiny" (hidden 256) and the
+# reference's own Qwen3-8B shape (qwen3/model.hpp:11-22; two layers, 4096
+# ids; intermediate 12288, 4 query heads per kv head) only the GEMM form
+GEMM_PROMPT_CASES = [("small", {}, 40, 96), ("small", {}, 300, 320), ("small", {}, 2, 16), ("tiny", {}, 30, 48),
+                     ("qwen3-8b", {"layers": 2, "vocab": 4096}, 24, 40)]
+
+
+@pytest.mark.parametrize("preset,over,n_prompt,max_seq", GEMM_PROMPT_CASES)
+def test_gemm_prefill_within_rounding(rt, preset, over, n_prompt, max_seq):
     # the projections of the prompt positions on the MFMA GEMM: each
     # projection output is within the GEMM's bar of the canonical one, so
     # the caches differ from the oracle's by bf16 rounding and the logits and
     # hidden state of the first new token by a small multiple of it; a
     # dropped residual, a swapped gate/up half or a transposed weight moves
     # them by O(1)
-    cfg = orc.config("small")
+    cfg = orc.config(preset, **over)
     prompt = orc.tokens(n_prompt, 12, cfg.vocab)
     m = orc.Model(cfg, seed=4, gain_std=0.1, max_seq=max_seq)
     ref, ref_logits = m.generate(prompt, 1, logit_steps=1)
@@ -343,7 +350,7 @@ def test_gemm_prefill_within_rounding(rt, n_prompt, max_seq):
     eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=max_seq, seed=4, gain_std=0.1, runtime=rt)
     eng.set_prefill("gemm")
     for mode in (qwen3.GRAPH, qwen3.EAGER):
-        print(f"gemm prefill n_prompt={n_prompt} mode={mode}", flush=True)
+        print(f"gemm prefill {preset} n_prompt={n_prompt} mode={mode}", flush=True)
         eng.set_mode(mode)
         out, _, _ = eng.generate(prompt, 1, stop_on_eos=False)
         got = orc.decode(eng.logits(), xpu.BF16).astype(np.float64)
@@ -357,17 +364,23 @@ def test_gemm_prefill_within_rounding(rt, n_prompt, max_seq):
         top2 = np.sort(want)[-2:]
         if top2[1] - top2[0] > 2 * dmax:
             assert out.tolist() == ref.tolist()
-    eng.set_prefill("batched")
+    # the exact forms on the same engine: batched where the shape has it,
+    # else stepwise
+    eng.set_prefill("batched" if preset == "small" else "stepwise")
     eng.generate(prompt, 1, stop_on_eos=False)
     assert np.array_equal(eng.logits(), ref_logits[0])
     eng.close()
 
 
 def test_gemm_prefill_mode_checks(rt):
-    cfg = orc.config("tiny")
+    # 8 query heads per kv head: no MFMA attention kernel (1, 2 or 4), and
+    # hidden 256 has no batched GEMV form either
+    cfg = orc.config("tiny", heads=8, kv_heads=1)
     eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=32, seed=1, gain_std=0.1, runtime=rt)
-    with pytest.raises(xpu.XpuError, match="prefill"):
+    with pytest.raises(xpu.XpuError, match="gemm prefill"):
         eng.set_prefill("gemm")
+    with pytest.raises(xpu.XpuError, match="batched prefill"):
+        eng.set_prefill("batched")
     with pytest.raises(xpu.XpuError, match="prefill mode"):
         xpu.check(eng.lib.xpu_qwen3_set_prefill(eng.handle, 3))
     eng.close()

@@ -351,8 +351,10 @@ int setup_launches(xpu_qwen3 &e) {
   return XPU_OK;
 }
 
-// Batched prefill needs every projection's K to be 512 times a chunk count
-// the module has kernels for (xpu_q3_pf_gemv_e<epi>_c<K/512>).
+// The batched GEMV form needs every projection's K to be 512 times a chunk
+// count the module has kernels for (xpu_q3_pf_gemv_e<epi>_c<K/512>); the
+// GEMM form needs none of those. The two share the embedding, RMSNorm and
+// QK-norm/RoPE/cache kernels and the chunk buffers.
 int setup_prefill(xpu_qwen3 &e) {
   const xpu_qwen3_config &c = e.c;
   const uint32_t qd = c.heads * c.head_dim;
@@ -369,10 +371,9 @@ int setup_prefill(xpu_qwen3 &e) {
   e.pf_rope_k = e.rt->find_exact("xpu_q3_pf_rope_cache");
   e.pf_attn_k = e.rt->find_exact("xpu_q3_pf_attention");
   e.pf_attn_short_k = e.rt->find_exact("xpu_q3_pf_attention_short");
-  e.pf_ok = e.pf_qkv_k && e.pf_o_k && e.pf_gu_k && e.pf_down_k && e.pf_embed_k && e.pf_norm_k && e.pf_rope_k &&
-            e.pf_attn_k && c.hidden % 8 == 0 && kpad_bytes(c.hidden) <= e.rt->max_shared &&
+  const bool common = e.pf_embed_k && e.pf_norm_k && e.pf_rope_k && c.hidden % 8 == 0;
+  e.pf_ok = common && e.pf_qkv_k && e.pf_o_k && e.pf_gu_k && e.pf_down_k && e.pf_attn_k &&
             32u * std::max({c.hidden, qd, c.intermediate}) <= e.rt->max_shared;
-  if (!e.pf_ok) return XPU_OK;
   const uint64_t qkv_rows = uint64_t{c.heads + 2 * c.kv_heads} * c.head_dim;
   // the MFMA form: every projection's K and N multiples of 8 (the NT GEMM
   // kernels read the weight rows in place) and 1, 2 or 4 query heads per kv
@@ -381,11 +382,12 @@ int setup_prefill(xpu_qwen3 &e) {
   e.pf_silu_k = e.rt->find_exact("xpu_q3_pf_silu_mul");
   if (group == 1 || group == 2 || group == 4)
     e.pf_attn_mfma_k = e.rt->find_exact("xpu_q3_pf_attention_mfma_g" + std::to_string(group));
-  e.pf_gemm_ok = e.pf_silu_k && e.pf_attn_mfma_k && e.rt->find_exact("xpu_gemm_bf16_nt_dma") &&
+  e.pf_gemm_ok = common && e.pf_silu_k && e.pf_attn_mfma_k && e.rt->find_exact("xpu_gemm_bf16_nt_dma") &&
                  c.intermediate % 8 == 0 && qd % 8 == 0 && qkv_rows % 8 == 0;
+  if (!e.pf_ok && !e.pf_gemm_ok) return XPU_OK;
   // chunks of 256 positions for the batched GEMV form; up to 4096 for the
   // GEMM form, whose GEMMs and attention fill the chip only with long chunks
-  e.pf_chunk = std::min<uint32_t>(e.max_seq, 256);
+  e.pf_chunk = e.pf_ok ? std::min<uint32_t>(e.max_seq, 256) : 0;
   e.pf_chunk_gemm = e.pf_gemm_ok ? std::min<uint32_t>(e.max_seq, 4096) : 0;
   const uint64_t T = std::max(e.pf_chunk, e.pf_chunk_gemm);
   const uint64_t sizes[7] = {T * c.hidden, T * c.hidden, T * qkv_rows, T * qd, T * qd, T * c.intermediate,
@@ -400,7 +402,7 @@ int setup_prefill(xpu_qwen3 &e) {
     *dst[i] = reinterpret_cast<uint16_t *>(p);
     p += (sizes[i] * 2 + 255) & ~uint64_t{255};
   }
-  e.batched_prefill = true;
+  e.batched_prefill = e.pf_ok;  // the default: the bit-identical form; the GEMM form is opt-in
   return XPU_OK;
 }
 
@@ -1028,7 +1030,7 @@ extern "C" int xpu_qwen3_set_mode(xpu_qwen3 *eng, int mode) {
 extern "C" int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int mode) {
   if (!eng) return set_error(XPU_ERR_INVALID, "null engine");
   if (mode < 0 || mode > 2) return set_error(XPU_ERR_INVALID, "prefill mode must be 0 (stepwise), 1 (batched) or 2 (gemm)");
-  if (mode && !eng->pf_ok)
+  if (mode == 1 && !eng->pf_ok)
     return set_error(XPU_ERR_INVALID, "batched prefill has no kernels for this model shape");
   if (mode == 2 && !eng->pf_gemm_ok)
     return set_error(XPU_ERR_INVALID, "gemm prefill has no kernels for this model shape");
