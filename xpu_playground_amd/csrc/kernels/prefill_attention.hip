@@ -9,7 +9,7 @@
 // (1 / sum)), out = bf16(sum_t p_t v_t) in FP32. Two things differ from the
 // decode path, which is bit-exact against the CPU oracle: the FP32
 // summation orders (the MFMA's), and the exponential, here the hardware's
-// exp2 (v_exp_f32 of (s - M) log2 e, a few FP32 ulps from the oracle's
+// exp2 (v_exp_f32 of s log2 e - M log2 e, a few FP32 ulps from the oracle's
 // canonical_exp; the reference's own kernel uses the device exp too). So
 // results agree with the decode path to rounding, not bitwise; the max is
 // exact. Two sweeps over the key tiles: the
@@ -176,6 +176,11 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
   // max grows; then the two half-waves' (m, sum) pairs are merged.
   constexpr float kLog2e = 1.44269504088896340736f;
   auto exp_hw = [&](float x) { return __builtin_amdgcn_exp2f(x * kLog2e); };
+  // exp(s - m) as exp2(s log2 e - m log2 e), one FMA per score with
+  // neg_ml = -m log2 e formed once per tile
+  auto exp_shift = [&](float sc, float neg_ml) {
+    return __builtin_amdgcn_exp2f(__builtin_fmaf(sc, kLog2e, neg_ml));
+  };
   float mx = ninf, sum = 0.0f;
   sweep(false, [&](uint32_t tile, uint32_t sb) {
     f32x16 s[2];
@@ -186,12 +191,12 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kt][r]);
-    const float m_new = fmaxf(mx, tmax);
+    const float m_new = fmaxf(mx, tmax), neg_ml = -m_new * kLog2e;
     float part = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) part = part + exp_hw(s[kt][r] - m_new);
+      for (int r = 0; r < 16; ++r) part = part + exp_shift(s[kt][r], neg_ml);
     // no valid key yet (m_new = -inf, every s - m_new NaN): the sum stays 0
     const float rescale = exp_hw(mx - m_new);
     sum = m_new == ninf ? 0.0f : (mx == ninf ? part : sum * rescale + part);
@@ -216,7 +221,7 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
 #pragma unroll
     for (uint32_t h = 1; h < H; ++h) merge2(mx, sum, merge[h][slot][0][lane], merge[h][slot][1][lane]);
   }
-  const float inv = 1.0f / sum;
+  const float inv = 1.0f / sum, neg_ml = -mx * kLog2e;
 
   // 2: p and O^T += V^T P^T; O^T tile dt: dims 32 dt + 8 (r / 4) + 4 hh + r % 4
   f32x16 o[4];
@@ -241,7 +246,8 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; r += 2)
-        pk[kt][r / 2] = dma::cvt_pack<kBf16>(exp_hw(s[kt][r] - mx) * inv, exp_hw(s[kt][r + 1] - mx) * inv);
+        pk[kt][r / 2] =
+            dma::cvt_pack<kBf16>(exp_shift(s[kt][r], neg_ml) * inv, exp_shift(s[kt][r + 1], neg_ml) * inv);
     const uint32_t vb = sb + 16384u;
 #pragma unroll
     for (uint32_t ks = 0; ks < 4; ++ks) {
