@@ -148,6 +148,10 @@ struct xpu_qwen3 {
   // for contexts of at least split_from positions (0: never), with its own
   // graph; scores [heads][att_spitch] and maxima [heads][att_parts]
   bool split_ok = false;
+  // the attention kernel's spare blocks prefetch the layer's o_proj,
+  // [gate; up] and down_proj only when they fit well inside the Infinity
+  // Cache (setup_launches)
+  bool attn_prefetch = false;
   uint32_t split_from = 257, att_spitch = 0, att_parts = 0;
   float *att_scores = nullptr, *att_max = nullptr;
   void *graph_split = nullptr;
@@ -323,8 +327,17 @@ int setup_launches(xpu_qwen3 &e) {
   if ((rc = pick("xpu_q3_norm_gemv_r2", c.hidden, "xpu_q3_norm_gemv_r2", e.qkv_l))) return rc;
   e.qkv_l.grid = std::min(cap, (qkv_rows + 7) / 8);
   if ((rc = find("xpu_q3_attention", e.attn_l))) return rc;
-  // one block per query head, the other compute units prefetch weights
-  e.attn_l.grid = std::max(c.heads, e.rt->compute_units);
+  // One block per query head; the other compute units prefetch the layer's
+  // remaining weights into the 256 MiB Infinity Cache, for the kernels that
+  // follow, when those fit in a quarter of it (Qwen3-0.6B: 23 MB). Larger
+  // layers (Qwen3-8B: 335 MB) would stream through the cache and evict
+  // themselves before use; their attention runs without spare blocks.
+  {
+    const uint64_t qd = uint64_t{c.heads} * c.head_dim, rest = uint64_t{c.hidden} * (qd + 3ull * c.intermediate) * 2;
+    constexpr uint64_t kPrefetchBudget = 64ull << 20;
+    e.attn_prefetch = rest <= kPrefetchBudget;
+  }
+  e.attn_l.grid = e.attn_prefetch ? std::max(c.heads, e.rt->compute_units) : c.heads;
   e.scores_l.k = e.rt->find_exact("xpu_q3_attn_scores");
   e.pv_l.k = e.rt->find_exact("xpu_q3_attn_pv");
   e.scores_l.grid = c.heads * e.att_parts;
@@ -433,7 +446,8 @@ int enqueue_fused_step(xpu_qwen3 &e, bool split) {
     // [gate; up] and down_proj (contiguous in the arena)
     const uint16_t *pf = L.o;
     const uint8_t *pf_end = reinterpret_cast<const uint8_t *>(L.down) + uint64_t{H} * I * 2;
-    const uint64_t pf_bytes = static_cast<uint64_t>(pf_end - reinterpret_cast<const uint8_t *>(L.o));
+    const uint64_t pf_bytes =
+        e.attn_prefetch ? static_cast<uint64_t>(pf_end - reinterpret_cast<const uint8_t *>(L.o)) : 0;
     const uint32_t pf_delay = 1;  // the spare blocks start ~512 cycles after the attention's loads
     if (split) {
       const uint32_t spitch = e.att_spitch, parts = e.att_parts;
