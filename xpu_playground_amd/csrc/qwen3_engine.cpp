@@ -298,8 +298,13 @@ uint16_t *tensor_location(xpu_qwen3 &e, int kind, uint32_t layer) {
 
 int setup_launches(xpu_qwen3 &e) {
   const xpu_qwen3_config &c = e.c;
-  // at most 4 blocks per CU for the decode GEMVs (2 measured the same, 1 slower)
+  // at most 4 blocks per CU for the decode GEMVs (Qwen3-0.6B: 2 measured
+  // the same, 1 slower); 2 for matrices past 32 MB (Qwen3-8B: 311 -> 320
+  // tok/s, 1 slower)
   const uint32_t cap = e.rt->compute_units * 4;
+  auto cap_for = [&](uint64_t rows, uint64_t K) {
+    return rows * K * 2 > (32ull << 20) ? e.rt->compute_units * 2 : cap;
+  };
   auto find = [&](const char *name, xpu_qwen3::Launch &l) -> int {
     l.k = e.rt->find_exact(name);
     return l.k ? XPU_OK : set_error(XPU_ERR_NOT_FOUND, std::string("kernel is absent from module: ") + name);
@@ -325,7 +330,7 @@ int setup_launches(xpu_qwen3 &e) {
     return find(lds_name, l);
   };
   if ((rc = pick("xpu_q3_norm_gemv_r2", c.hidden, "xpu_q3_norm_gemv_r2", e.qkv_l))) return rc;
-  e.qkv_l.grid = std::min(cap, (qkv_rows + 7) / 8);
+  e.qkv_l.grid = std::min(cap_for(qkv_rows, c.hidden), (qkv_rows + 7) / 8);
   if ((rc = find("xpu_q3_attention", e.attn_l))) return rc;
   // One block per query head; the other compute units prefetch the layer's
   // remaining weights into the 256 MiB Infinity Cache, for the kernels that
@@ -347,11 +352,11 @@ int setup_launches(xpu_qwen3 &e) {
   e.pv_l.shared = 4096 * 4 + 4096 * 16 * 2 + 64 * 4 + 64 * 4;
   e.split_ok = e.scores_l.k && e.pv_l.k && e.max_seq <= 64u * 4096u && e.pv_l.shared <= e.rt->max_shared;
   if ((rc = pick("xpu_q3_gemv_residual_r1", qd, "xpu_q3_gemv_residual_r1", e.o_l))) return rc;
-  e.o_l.grid = std::min(cap, (c.hidden + 3) / 4);
+  e.o_l.grid = std::min(cap_for(c.hidden, qd), (c.hidden + 3) / 4);
   if ((rc = pick("xpu_q3_norm_gemv_swiglu_r2", c.hidden, "xpu_q3_norm_gemv_swiglu_r2", e.gu_l))) return rc;
-  e.gu_l.grid = std::min(cap, (c.intermediate + 3) / 4);
+  e.gu_l.grid = std::min(cap_for(2ull * c.intermediate, c.hidden), (c.intermediate + 3) / 4);
   if ((rc = pick("xpu_q3_gemv_residual_r1", c.intermediate, "xpu_q3_gemv_residual_r1", e.down_l))) return rc;
-  e.down_l.grid = std::min(cap, (c.hidden + 3) / 4);
+  e.down_l.grid = std::min(cap_for(c.hidden, c.intermediate), (c.hidden + 3) / 4);
   if ((rc = pick("xpu_q3_norm_gemv_logits_r2", c.hidden, "xpu_q3_norm_gemv_logits_r2", e.logits_l))) return rc;
   // two blocks per CU: 8 MiB of lm_head rows in flight on 256 CUs, the
   // streaming optimum (8 blocks per CU, or a second row buffer per
