@@ -329,8 +329,13 @@ def test_mode_switch_mid_sequence_is_rejected(rt):
 # "small" also has the batched GEMV form; "tiny" (hidden 256) and the
 # reference's own Qwen3-8B shape (qwen3/model.hpp:11-22; two layers, 4096
 # ids; intermediate 12288, 4 query heads per kv head) only the GEMM form
+# (tiny with one layer, 4110 ids: two chunks of the GEMM form; the decode
+# step of the last prompt position attends over caches written by both, the
+# second chunk's from position 4096 on. With one layer the prompt's own
+# attention output is not used, the last layer stops at its caches; the MFMA
+# attention with p0 > 0 is covered by test_gpu_prefill_attention.py)
 GEMM_PROMPT_CASES = [("small", {}, 40, 96), ("small", {}, 300, 320), ("small", {}, 2, 16), ("tiny", {}, 30, 48),
-                     ("qwen3-8b", {"layers": 2, "vocab": 4096}, 24, 40)]
+                     ("qwen3-8b", {"layers": 2, "vocab": 4096}, 24, 40), ("tiny", {"layers": 1}, 4110, 4160)]
 
 
 @pytest.mark.parametrize("preset,over,n_prompt,max_seq", GEMM_PROMPT_CASES)
