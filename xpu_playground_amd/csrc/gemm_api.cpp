@@ -184,7 +184,8 @@ int gemm_nt(xpu_runtime *rt, const void *A, const void *W, void *C, uint32_t M, 
   const xpu::KernelInfo *k = rt->find_exact(name);
   if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: " + name);
   uint32_t kb = K, ldc = N, n_out = N;
-  const xpu_kernel_arg args[] = {{8, &A}, {8, &W}, {8, &C}, {4, &M}, {4, &N}, {4, &K}, {4, &kb}, {4, &ldc}, {4, &n_out}};
+  const xpu_kernel_arg args[] = {{8, &A}, {8, &W},  {8, &C},   {4, &M},    {4, &N},
+                                 {4, &K}, {4, &kb}, {4, &ldc}, {4, &n_out}};
   return rt->launch(*k, static_cast<uint32_t>(tiles), 1, 256, 0, args, 9);
 }
 

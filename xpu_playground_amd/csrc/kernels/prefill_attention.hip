@@ -291,7 +291,8 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] + po[(((h - 1) * kSlots + slot) * 64 + dt * 16 + r) * 64 + lane];
+        for (int r = 0; r < 16; ++r)
+          o[dt][r] = o[dt][r] + po[(((h - 1) * kSlots + slot) * 64 + dt * 16 + r) * 64 + lane];
   }
   if (t < T && t0 < T) {
     uint16_t *orow = out + (static_cast<uint64_t>(t) * heads + head) * kHeadDim;

@@ -1048,7 +1048,8 @@ extern "C" int xpu_qwen3_set_mode(xpu_qwen3 *eng, int mode) {
 
 extern "C" int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int mode) {
   if (!eng) return set_error(XPU_ERR_INVALID, "null engine");
-  if (mode < 0 || mode > 2) return set_error(XPU_ERR_INVALID, "prefill mode must be 0 (stepwise), 1 (batched) or 2 (gemm)");
+  if (mode < 0 || mode > 2)
+    return set_error(XPU_ERR_INVALID, "prefill mode must be 0 (stepwise), 1 (batched) or 2 (gemm)");
   if (mode == 1 && !eng->pf_ok)
     return set_error(XPU_ERR_INVALID, "batched prefill has no kernels for this model shape");
   if (mode == 2 && !eng->pf_gemm_ok)
