@@ -554,9 +554,9 @@ XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_res_dma, 2, 2, 2, 2, 2, false, true)
 // with 128 x 128 tiles (a 1024-wide projection of a few thousand tokens).
 // Its slices are short (8 MFMAs per wavefront), so four stages keep three
 // slices in flight to cover the memory latency; groups of 4 slices (K past
-// the last whole group reads zeros).
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_dma, 2, 1, 4, 1, 2, false, false)
-XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_res_dma, 2, 1, 4, 1, 2, false, true)
+// the last whole group reads zeros). 96 KiB of LDS: one block per CU.
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_dma, 2, 1, 4, 1, 1, false, false)
+XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_res_dma, 2, 1, 4, 1, 1, false, true)
 
 // 256 x 256: BK = 64, two stages, barrier after 4 MFMAs of a slice's last
 // k-step, each slice's DMA spread over two k-steps; _odd for an odd number
