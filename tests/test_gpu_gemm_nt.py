@@ -98,3 +98,44 @@ def test_nt_same_bits_as_kn(rt):
             continue
         got = launch_nt(rt, tag, False, a, w, np.zeros(m * n, np.uint16), m, n, k)
         assert np.array_equal(got, ref), tag
+
+
+def launch_splitk(rt, res, a, w, c0, m, n, k, spl):
+    """The split-K form: xpu_gemm_bf16_n64_nt_part_dma over K ranges of spl
+    slices (a multiple of 4), then xpu_gemm_splitk_reduce."""
+    assert k % 8 == 0 and n % 8 == 0 and spl % 4 == 0
+    slices = (k + 63) // 64
+    splits = (slices + spl - 1) // spl
+    tiles = ((m + 127) // 128) * ((n + 63) // 64)
+    words = m * n + 16
+    da, dw, dc = rt.upload(a), rt.upload(w), rt.alloc(words * 2)
+    dp = rt.alloc(splits * m * n * 4)
+    try:
+        rt.copy_to(dc, np.concatenate([c0, np.full(16, GUARD, np.uint16)]))
+        print(f"split-K {m}x{n}x{k} spl {spl} splits {splits} res {res}", flush=True)
+        args = Args().ptr(da).ptr(dw).ptr(dp).u32(m).u32(n).u32(k).u32(spl).u32(n).u32(n)
+        rt.launch_grid("xpu_gemm_bf16_n64_nt_part_dma", tiles * splits, 256, 0, args)
+        rargs = Args().ptr(dp).ptr(dc).u32(m).u32(n).u32(splits).u32(1 if res else 0)
+        rt.launch_grid("xpu_gemm_splitk_reduce", max(1, min((m * n // 8 + 255) // 256, 2048)), 256, 0, rargs)
+        rt.synchronize()
+        out = rt.download(dc, words, np.uint16)
+    finally:
+        for p in (da, dw, dc, dp):
+            rt.free(p)
+    assert np.all(out[m * n:] == GUARD), "store past C"
+    return out[:m * n].reshape(m, n)
+
+
+@pytest.mark.parametrize("res", [False, True])
+@pytest.mark.parametrize("m,n,k,spl", [(127, 1024, 3072, 4), (511, 1024, 2048, 8), (127, 4096, 1024, 4), (37, 56, 200, 4),
+                                       (300, 8, 1032, 8), (1, 64, 64, 4)])
+def test_splitk(rt, res, m, n, k, spl):
+    a = orc.uniform(m * k, 200 + m, xpu.BF16)
+    w = orc.uniform(n * k, 210 + n, xpu.BF16)
+    old = orc.uniform(m * n, 220 + k, xpu.BF16) if res else np.full(m * n, GUARD, np.uint16)
+    got = launch_splitk(rt, res, a, w, old, m, n, k, spl)
+    if res:
+        check_residual(got, old, a, w, m, n, k)
+    else:
+        wt = np.ascontiguousarray(w.reshape(n, k).T).reshape(-1)
+        check(got, a, wt, m, n, k, xpu.BF16)

@@ -158,6 +158,12 @@ int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, 
 // every pointer 16-byte aligned, row strides K, K and N), the projections of
 // the batched prompt (qwen3_engine.cpp); residual: C = bf16(C + bf16(A W^T)).
 // The block tile and the odd-slice form are chosen as for xpu_gemm.
+uint64_t gemm_nt_workspace_bound(const xpu_runtime *rt) {
+  // split K only with tiles <= CUs / 2, and splits <= ceil(CUs / tiles):
+  // splits x tiles <= CUs + tiles <= 1.5 CUs tiles of 128 x 64 FP32
+  return (static_cast<uint64_t>(rt->compute_units) * 3 / 2 + 1) * 128 * 64 * 4;
+}
+
 int gemm_nt(xpu_runtime *rt, const void *A, const void *W, void *C, uint32_t M, uint32_t N, uint32_t K,
             bool residual) {
   if (!rt || !A || !W || !C) return set_error(XPU_ERR_INVALID, "gemm_nt: null argument");
@@ -179,6 +185,31 @@ int gemm_nt(xpu_runtime *rt, const void *A, const void *W, void *C, uint32_t M, 
   if (tag == "_t128" && tiles < rt->compute_units) {
     tag = "_n64";
     tiles = count(128, 64);
+  }
+  // Split K where even 128 x 64 tiles leave half the compute units idle (a
+  // short prompt's projections): splits of a multiple of 4 slices (the
+  // kernel's stage group) so that tiles x splits about fills the CUs; FP32
+  // partials in the workspace, then one reduction (split order) that
+  // rounds and applies the residual.
+  if (tag == "_n64" && tiles * 2 <= rt->compute_units) {
+    const uint32_t want = static_cast<uint32_t>((rt->compute_units + tiles - 1) / tiles);
+    const uint32_t spl = ((slices + want - 1) / want + 3) / 4 * 4, splits = (slices + spl - 1) / spl;
+    if (splits >= 2) {
+      const xpu::KernelInfo *kp = rt->find_exact("xpu_gemm_bf16_n64_nt_part_dma");
+      const xpu::KernelInfo *kr = rt->find_exact("xpu_gemm_splitk_reduce");
+      if (!kp || !kr) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: split-K GEMM");
+      void *part = nullptr;
+      int rc = rt->scratch(static_cast<uint64_t>(splits) * M * N * 4, &part);
+      if (rc) return rc;
+      uint32_t kb = spl, ldc = N, n_out = N, res = residual ? 1u : 0u, nsplit = splits;
+      const xpu_kernel_arg pargs[] = {{8, &A}, {8, &W},  {8, &part}, {4, &M},    {4, &N},
+                                      {4, &K}, {4, &kb}, {4, &ldc},  {4, &n_out}};
+      if ((rc = rt->launch(*kp, static_cast<uint32_t>(tiles * splits), 1, 256, 0, pargs, 9))) return rc;
+      const uint64_t threads = static_cast<uint64_t>(M) * N / 8;
+      const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>((threads + 255) / 256, rt->compute_units * 8ull));
+      const xpu_kernel_arg rargs[] = {{8, &part}, {8, &C}, {4, &M}, {4, &N}, {4, &nsplit}, {4, &res}};
+      return rt->launch(*kr, grid, 1, 256, 0, rargs, 6);
+    }
   }
   const std::string name = "xpu_gemm_bf16" + tag + (odd ? "_odd" : "") + "_nt" + (residual ? "_res" : "") + "_dma";
   const xpu::KernelInfo *k = rt->find_exact(name);

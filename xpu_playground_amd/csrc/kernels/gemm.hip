@@ -149,17 +149,24 @@ template <int MI, int NJ, int BK, int S, bool BT = false> struct Cfg {
 // BT: B is given as its transpose, [N][K] row-major (the rows of a weight
 // matrix W for C = X W^T); its tile is staged and read like A's. RES: C is
 // updated in place, C = bf16(C + bf16(A B)) (a residual add), C16 only.
+// PART (with BT): split K. Block b computes tile b % tiles over slices
+// split * kb .. split * kb + kb - 1, split = b / tiles (kb, a multiple of S,
+// is the slices per split here), and stores its FP32 partial tile into
+// ((float *) C)[split][M][N]; xpu_gemm_splitk_reduce adds the splits.
 template <int DT, int MI, int NJ, int BK, int S, int P, int D, bool C16, bool ODD, bool BT = false,
-          bool RES = false>
+          bool RES = false, bool PART = false>
 XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
                      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {
   using G = Cfg<MI, NJ, BK, S, BT>;
   static_assert(!RES || C16, "the residual epilogue stores 16-byte chunks");
+  static_assert(!PART || (BT && !RES && !ODD), "split K: [n][k] weights, the reduction applies any residual");
   __shared__ __align__(1024) uint8_t lds[G::kLds];
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t tiles_m = (M + G::kBM - 1) / G::kBM, tiles_n = (N + G::kBN - 1) / G::kBN;
-  const TileCoord tc = tile_of_block(blockIdx.x, tiles_m, tiles_n);
+  const uint32_t split = PART ? blockIdx.x / (tiles_m * tiles_n) : 0u;
+  const uint32_t s_base = PART ? split * kb : 0u;  // first slice of this block
+  const TileCoord tc = tile_of_block(PART ? blockIdx.x % (tiles_m * tiles_n) : blockIdx.x, tiles_m, tiles_n);
   const uint32_t m0 = tc.tm * G::kBM, n0 = tc.tn * G::kBN;
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
 
@@ -187,7 +194,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     uint32_t a_base, b_base, st_base;
   };
   auto slice_of = [&](uint32_t s, uint32_t stage) {
-    const uint64_t k0 = static_cast<uint64_t>(s) * BK;
+    const uint64_t k0 = static_cast<uint64_t>(s_base + s) * BK;
     Slice d;
     d.r_a = rsrc(A + static_cast<uint64_t>(m0) * K + k0,
                  (static_cast<int64_t>(M - m0) * K - static_cast<int64_t>(k0)) * 2);
@@ -299,7 +306,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     acc[q / NJ][q % NJ] = mfma<DT>(f.b[q % NJ], f.a[q / NJ], acc[q / NJ][q % NJ]);
   };
 
-  const uint32_t nk = (K + BK - 1) / BK;
+  const uint32_t nk = PART ? kb : (K + BK - 1) / BK;
   static_assert(D >= 1 && D <= G::kKs, "a slice's DMA is issued within the k-steps before the next barrier");
   static_assert(P < G::kMf, "k-step schedule: MFMAs after the barrier carry the next slice's first reads");
   // fragment reads of the next k-step issued after MFMA q of an ordinary
@@ -440,6 +447,24 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   // 4 g..4 g + 3) as 16-byte rows into its own region (pitch kBNW + 4
   // floats), then reads it back 8 consecutive columns per lane and stores 16
   // bytes of C per lane.
+  if constexpr (PART) {
+    // FP32 partials straight from the accumulators: lane l holds columns
+    // 32 j + 8 g + 4 (l / 32) .. + 3 of row 32 i + l % 32 of its wave tile
+    float *part = reinterpret_cast<float *>(C) + static_cast<uint64_t>(split) * M * N;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t m = m0 + wm * G::kBMW + 32u * i + (lane & 31u);
+          const uint32_t n = n0 + wn * G::kBNW + 32u * j + 8u * g + 4u * (lane >> 5);
+          if (m < M && n < N)
+            *reinterpret_cast<f32x4 *>(part + static_cast<uint64_t>(m) * N + n) =
+                f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        }
+    return;
+  }
   constexpr uint32_t kEpPitch = G::kEpPitch;
   constexpr uint32_t kLpr = G::kBNW / 8u;  // lanes per staged row on the way out
   constexpr uint32_t kRpr = 64u / kLpr;    // rows per read instruction
@@ -557,6 +582,52 @@ XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_t128_nt_res_dma, 2, 2, 2, 2, 2, false, true)
 // the last whole group reads zeros). 96 KiB of LDS: one block per CU.
 XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_dma, 2, 1, 4, 1, 1, false, false)
 XPU_GEMM_NT_VARIANT(xpu_gemm_bf16_n64_nt_res_dma, 2, 1, 4, 1, 1, false, true)
+// split K for outputs that leave most compute units idle even at 128 x 64
+// (a short prompt's o_proj and down): FP32 partials of each K range (kb
+// slices, a multiple of 4), added by xpu_gemm_splitk_reduce
+extern "C" __global__ __launch_bounds__(256, 1) void xpu_gemm_bf16_n64_nt_part_dma(
+    const uint16_t *__restrict__ A, const uint16_t *__restrict__ W, uint16_t *__restrict__ C, uint32_t M,
+    uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {
+  XPU_STAMP(xpu::kStampGemm);
+  xpu::dma::body<xpu::kBf16, 2, 1, 64, 4, 1, 2, true, false, true, false, true>(A, W, C, M, N, K, kb, ldc, n_out);
+}
+
+// C (M x N bf16) from the FP32 partials P[splits][M][N] of the split-K GEMM,
+// added in split order: C = bf16(y) or, with residual, bf16(C + bf16(y));
+// N a multiple of 8, 8 outputs per thread, grid-stride.
+extern "C" __global__ __launch_bounds__(256) void xpu_gemm_splitk_reduce(const float *__restrict__ P,
+                                                                         uint16_t *__restrict__ C, uint32_t M,
+                                                                         uint32_t N, uint32_t splits,
+                                                                         uint32_t residual) {
+  const uint64_t mn = static_cast<uint64_t>(M) * N, total = mn / 8u;
+  for (uint64_t c = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < total;
+       c += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+    const float4 *p = reinterpret_cast<const float4 *>(P + c * 8u);
+    float4 lo = p[0], hi = p[1];
+    for (uint32_t s = 1; s < splits; ++s) {
+      const float4 a = p[s * (mn / 4u)], b = p[s * (mn / 4u) + 1];
+      lo = float4{lo.x + a.x, lo.y + a.y, lo.z + a.z, lo.w + a.w};
+      hi = float4{hi.x + b.x, hi.y + b.y, hi.z + b.z, hi.w + b.w};
+    }
+    const float y[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    uint16_t *dst = C + c * 8u;
+    const xpu::u32x4 old = residual ? *reinterpret_cast<const xpu::u32x4 *>(dst) : xpu::u32x4{0, 0, 0, 0};
+    const uint32_t ow[4] = {old.x, old.y, old.z, old.w};
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t h[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float v = y[2 * q + e];
+        h[e] = residual ? xpu::f32_to_bf16(xpu::bf16_to_f32((ow[q] >> (16 * e)) & 0xffffu) + xpu::round_bf16(v))
+                        : xpu::f32_to_bf16(v);
+      }
+      w[q] = h[0] | (h[1] << 16);
+    }
+    *reinterpret_cast<xpu::u32x4 *>(dst) = xpu::u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
 
 // 256 x 256: BK = 64, two stages, barrier after 4 MFMAs of a slice's last
 // k-step, each slice's DMA spread over two k-steps; _odd for an odd number

@@ -421,6 +421,12 @@ int setup_prefill(xpu_qwen3 &e) {
     p += (sizes[i] * 2 + 255) & ~uint64_t{255};
   }
   e.batched_prefill = e.pf_ok;  // the default: the bit-identical form; the GEMM form is opt-in
+  if (e.pf_gemm_ok) {
+    // the GEMM form's split-K partials, reserved now rather than grown (with
+    // a stream synchronization) in the middle of a prompt
+    void *ws = nullptr;
+    if ((rc = e.rt->scratch(xpu::gemm_nt_workspace_bound(e.rt), &ws))) return rc;
+  }
   return XPU_OK;
 }
 

@@ -56,6 +56,9 @@ int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, 
 // residual adds into C
 int gemm_nt(xpu_runtime *rt, const void *A, const void *W, void *C, uint32_t M, uint32_t N, uint32_t K,
             bool residual);
+// The most workspace gemm_nt requests (its split-K partials), so a caller
+// can reserve it once (xpu_runtime::scratch grows by synchronizing).
+uint64_t gemm_nt_workspace_bound(const xpu_runtime *rt);
 
 // Device address of the no-allocation scratch array on `device` (the
 // current device), looked up once per device; called by xpu_rt_create.
