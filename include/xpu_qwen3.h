@@ -119,9 +119,10 @@ int xpu_qwen3_set_mode(xpu_qwen3 *eng, int mode);
  *   0 stepwise: the prompt goes through decode one position at a time, as
  *     the reference does (main.cpp:343-344);
  *   1 batched (default when the module has kernels for the shape): the
- *     prompt positions before the last run as one batch per layer with the
- *     same arithmetic as the decode step, so the KV caches, tokens and
- *     logits are bit-identical to stepwise;
+ *     prompt positions run as one batch per layer with the same arithmetic
+ *     as the decode step (the last position's last-layer MLP, final norm,
+ *     lm_head and argmax on the decode step's own kernels), so the KV
+ *     caches, tokens and logits are bit-identical to stepwise;
  *   2 gemm: as batched in chunks of up to 4096 positions, with the four
  *     projections on the MFMA GEMM and the causal attention on MFMA (FP32
  *     sums in the MFMA's order, the hardware exp), so the caches differ
@@ -150,8 +151,8 @@ int xpu_qwen3_logits(xpu_qwen3 *eng, uint16_t *out, uint64_t count);
 int xpu_qwen3_hidden(xpu_qwen3 *eng, uint16_t *out, uint64_t count);
 
 /* Prompt + greedy loop (main.cpp:342-352): the prompt goes through decode one
- * position at a time; token i of out is the argmax after position
- * n_prompt - 1 + i; stops after an EOS id (151645, 151643) when
+ * position at a time (or the batched forms, xpu_qwen3_set_prefill); token i
+ * of out is the argmax after position n_prompt - 1 + i; stops after an EOS id (151645, 151643) when
  * stop_on_eos. *n_out = number of ids written. prompt_ms / decode_ms (may be
  * NULL): device time of the prompt steps and of the n_out - 1 decode steps. */
 int xpu_qwen3_generate(xpu_qwen3 *eng, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_new,

@@ -434,11 +434,43 @@ int launch(xpu_qwen3 &e, const xpu_qwen3::Launch &l, uint32_t block, std::initia
   return e.rt->launch(*l.k, l.grid, 1, block, l.shared, args.begin(), static_cast<uint32_t>(args.size()));
 }
 
+// o_proj + residual, RMSNorm + [gate; up] + SiLU, down + residual of layer
+// L for the residual stream in e.x, from the attention output `attn`.
+int enqueue_layer_mlp(xpu_qwen3 &e, const Layer &L, const uint16_t *attn) {
+  const xpu_qwen3_config &c = e.c;
+  const uint32_t H = c.hidden, I = c.intermediate, qd = c.heads * c.head_dim;
+  const float eps = c.rms_eps;
+  int rc;
+  if ((rc = launch(e, e.o_l, 256, {{8, &L.o}, {8, &attn}, {8, &e.x}, {4, &H}, {4, &qd}}))) return rc;
+  if ((rc = launch(e, e.gu_l, 256,
+                   {{8, &L.gu}, {8, &e.x}, {8, &L.post_norm}, {8, &e.h}, {4, &I}, {4, &H}, {4, &eps}})))
+    return rc;
+  return launch(e, e.down_l, 256, {{8, &L.down}, {8, &e.h}, {8, &e.x}, {4, &H}, {4, &I}});
+}
+
+// Final RMSNorm + lm_head + argmax of e.x; the finish kernel stores the
+// token and advances state (position, token, RoPE rows).
+int enqueue_head(xpu_qwen3 &e) {
+  const xpu_qwen3_config &c = e.c;
+  const uint32_t H = c.hidden, V = c.vocab, max_seq = e.max_seq;
+  const float eps = c.rms_eps;
+  int rc;
+  if ((rc = launch(e, e.logits_l, 256,
+                   {{8, &e.lm_head}, {8, &e.x}, {8, &e.final_norm}, {8, &e.logits}, {4, &V}, {4, &H}, {4, &eps},
+                    {8, &e.part_val}, {8, &e.part_idx}, {8, &e.part_bad}})))
+    return rc;
+  const uint32_t nparts = e.logits_l.grid;
+  return launch(e, e.finish_l, 1024,
+                {{8, &e.part_val}, {8, &e.part_idx}, {8, &e.part_bad}, {4, &nparts}, {8, &e.state},
+                 {8, &e.prompt}, {8, &e.gen}, {4, &max_seq}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &e.rope_row},
+                 {4, &max_seq}});
+}
+
 // One token through the fused kernels (reads position/token from state).
 int enqueue_fused_step(xpu_qwen3 &e, bool split) {
   const xpu_qwen3_config &c = e.c;
   const uint32_t H = c.hidden, I = c.intermediate, V = c.vocab, heads = c.heads, kv = c.kv_heads;
-  const uint32_t qkv_rows = (heads + 2 * kv) * c.head_dim, qd = heads * c.head_dim, max_seq = e.max_seq;
+  const uint32_t qkv_rows = (heads + 2 * kv) * c.head_dim, max_seq = e.max_seq;
   const float eps = c.rms_eps;
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
   const uint64_t cache_layer = uint64_t{kv} * max_seq * c.head_dim;
@@ -476,28 +508,19 @@ int enqueue_fused_step(xpu_qwen3 &e, bool split) {
                       {8, &vc}, {8, &e.attn}, {8, &e.state}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps},
                       {4, &scale}, {8, &pf}, {8, &pf_bytes}, {4, &pf_delay}})))
       return rc;
-    if ((rc = launch(e, e.o_l, 256, {{8, &L.o}, {8, &e.attn}, {8, &e.x}, {4, &H}, {4, &qd}}))) return rc;
-    if ((rc = launch(e, e.gu_l, 256,
-                     {{8, &L.gu}, {8, &e.x}, {8, &L.post_norm}, {8, &e.h}, {4, &I}, {4, &H}, {4, &eps}})))
-      return rc;
-    if ((rc = launch(e, e.down_l, 256, {{8, &L.down}, {8, &e.h}, {8, &e.x}, {4, &H}, {4, &I}}))) return rc;
+    if ((rc = enqueue_layer_mlp(e, L, e.attn))) return rc;
   }
-  if ((rc = launch(e, e.logits_l, 256,
-                   {{8, &e.lm_head}, {8, &e.x}, {8, &e.final_norm}, {8, &e.logits}, {4, &V}, {4, &H}, {4, &eps},
-                    {8, &e.part_val}, {8, &e.part_idx}, {8, &e.part_bad}})))
-    return rc;
-  const uint32_t nparts = e.logits_l.grid;
-  return launch(e, e.finish_l, 1024,
-                {{8, &e.part_val}, {8, &e.part_idx}, {8, &e.part_bad}, {4, &nparts}, {8, &e.state},
-                 {8, &e.prompt}, {8, &e.gen}, {4, &max_seq}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &e.rope_row},
-                 {4, &max_seq}});
+  return enqueue_head(e);
 }
 
 // K/V cache entries of prompt positions [0, P) (prompt ids already in
 // e.prompt), in chunks of pf_chunk positions (pf_chunk_gemm in the GEMM
 // form). The last layer's o_proj and MLP are skipped: only the caches are
-// wanted.
-int run_prefill(xpu_qwen3 &e, uint32_t P) {
+// wanted. With `head`, position P - 1 also yields the next token: its row of
+// the residual stream goes to e.x and the decode step's kernels finish it
+// (the last layer's o_proj and MLP, then the final norm, lm_head and argmax
+// with state[0] = P - 1), so no separate decode step runs for it.
+int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
   const xpu_qwen3_config &c = e.c;
   uint32_t H = c.hidden, I = c.intermediate, V = c.vocab, heads = c.heads, kv = c.kv_heads, max_seq = e.max_seq;
   uint32_t qkv_rows = (heads + 2 * kv) * c.head_dim, qd = heads * c.head_dim;
@@ -548,7 +571,15 @@ int run_prefill(xpu_qwen3 &e, uint32_t P) {
                       {4, &max_seq}, {4, &scale}})))
           return rc;
       }
-      if (l + 1 == c.layers) break;
+      if (l + 1 == c.layers) {
+        if (head && p0 + T == P) {
+          XPU_HIP_RETURN(hipMemcpyAsync(e.x, e.pf_x + uint64_t{T - 1} * H, uint64_t{H} * 2, hipMemcpyDeviceToDevice,
+                                        rt->stream));
+          if ((rc = enqueue_layer_mlp(e, L, e.pf_a + uint64_t{T - 1} * qd))) return rc;
+          if ((rc = enqueue_head(e))) return rc;
+        }
+        break;
+      }
       if (e.gemm_prefill) {
         if ((rc = xpu::gemm_nt(rt, e.pf_a, L.o, e.pf_x, T, H, qd, true))) return rc;
       } else if ((rc = go(e.pf_o_k, (H + 3) / 4, 1, 256, pf_lds(qd),
@@ -1164,8 +1195,10 @@ extern "C" int xpu_qwen3_generate(xpu_qwen3 *eng, const uint32_t *prompt, uint32
     *n_out = produced;
   } else {
     if ((rc = xpu_rt_copy_to_device(eng->rt, eng->prompt, prompt, n_prompt * 4ull))) return rc;
-    // batched prefill fills the caches of positions 0..n_prompt-2; the last
-    // prompt position runs as a decode step (it yields the first new token)
+    // batched prefill of every prompt position, the last one finished by
+    // the decode step's tail kernels (they yield the first new token); a
+    // one-id prompt runs as a decode step
+    const bool whole = eng->batched_prefill && n_prompt >= 2;
     const uint32_t first = eng->batched_prefill ? n_prompt - 1 : 0;
     const uint32_t st[4] = {first, prompt[first], 0, n_prompt};
     if ((rc = xpu_rt_copy_to_device(eng->rt, eng->state, st, sizeof(st)))) return rc;
@@ -1174,8 +1207,9 @@ extern "C" int xpu_qwen3_generate(xpu_qwen3 *eng, const uint32_t *prompt, uint32
     for (auto &v : ev)
       if ((rc = xpu_rt_event_create(eng->rt, &v))) return rc;
     rc = xpu_rt_event_record(eng->rt, ev[0]);
-    if (!rc && first) rc = run_prefill(*eng, first);
-    for (uint32_t s = first; !rc && s < steps; ++s) {
+    if (!rc && whole) rc = run_prefill(*eng, n_prompt, true);
+    if (!rc && whole) rc = xpu_rt_event_record(eng->rt, ev[1]);
+    for (uint32_t s = whole ? n_prompt : first; !rc && s < steps; ++s) {
       rc = run_fused_step(*eng, s);
       if (!rc && s + 1 == n_prompt) rc = xpu_rt_event_record(eng->rt, ev[1]);
     }
