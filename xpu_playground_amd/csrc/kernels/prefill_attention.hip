@@ -3,25 +3,26 @@
 // positions 0 .. own position, K and V read from the chunk-major caches
 // [kv_head][16][max_seq][8] that xpu_q3_pf_rope_cache filled.
 //
-// The rounding points are the decode attention's (qwen3/kernels.hpp:157-192
-// as restated by the oracle): s = bf16(bf16(q . k) * scale), the row max M
-// over the bf16 scores, e = exp(s - M), the FP32 sum of the e, p = bf16(e *
-// (1 / sum)), out = bf16(sum_t p_t v_t) in FP32. Two things differ from the
-// decode path, which is bit-exact against the CPU oracle: the FP32
-// summation orders (the MFMA's), and the exponential, here the hardware's
-// exp2 (v_exp_f32 of s log2 e - M log2 e, a few FP32 ulps from the oracle's
-// canonical_exp; the reference's own kernel uses the device exp too). So
-// results agree with the decode path to rounding, not bitwise; the max is
-// exact. Two sweeps over the key tiles: the
-// row max with the sum of exp(s - max) (rescaled as the max grows), then p
-// and P.V; QK^T is recomputed in the second sweep rather than stored.
+// Rounding: s = bf16(bf16(q . k) * scale) as in the decode attention
+// (qwen3/kernels.hpp:157-192 as restated by the oracle), then an online
+// softmax in one sweep over the key tiles, as the reference's own kernel
+// runs it (FP32 running max and sum, kernels.hpp:174-190): per query a
+// running max m, p = bf16(exp(s - m)) as the P.V MFMA operand, the FP32 sum
+// of exp(s - m) and the FP32 output rescaled by exp(m_old - m_new) when m
+// grows, and out = bf16(O / sum) at the end. The decode path (bit-exact
+// against the CPU oracle) instead rounds p = bf16(exp(s - M) / sum) with
+// the final max M; the exponential here is the hardware's exp2 (v_exp_f32
+// of s log2 e - m log2 e; the reference's kernel uses the device exp too),
+// and the FP32 sums run in the MFMA's order. So results agree with the
+// decode path to rounding (about half the output codes equal, the rest one
+// bf16 step away), not bitwise.
 //
 // Block: one kv head, 4 wavefronts of 32 query rows each: G query heads x
 // U query sub-tiles x H key halves (G U H = 4; QT = 32 U queries). Key
 // tiles of 64 positions: half h takes tiles h, h + H, ..., so the causal
 // work of a block is spread over its waves, and the halves merge their
-// (max, sum) after the first sweep and their FP32 partial outputs after the
-// second through LDS, in half order. Tiles are staged by LDS-DMA, two stages
+// (max, sum, FP32 partial output) through LDS after the sweep, in half
+// order. Tiles are staged by LDS-DMA, two stages
 // of H tile slots of K [16 chunks][64 keys][8] and V [64 keys][16 chunks,
 // XOR-swizzled][8]. Per wave and tile:
 // S^T = K Q^T as two 32 x 32 MFMA tiles (A: K rows from LDS, B: the wave's Q
@@ -171,9 +172,12 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     __syncthreads();  // the next sweep's first DMA reuses stage 0
   };
 
-  // 1: the row max M and the sum of exp(s - M) in one sweep: per lane a
-  // running max m and sum, the sum rescaled by exp(m_old - m_new) when the
-  // max grows; then the two half-waves' (m, sum) pairs are merged.
+  // One sweep, online softmax: per lane (query) a running max m, the FP32
+  // sum of exp(s - m) and the FP32 O^T columns, both rescaled by
+  // exp(m_old - m_new) when the max grows; p = bf16(exp(s - m)) feeds the
+  // P.V MFMA, and the output is divided by the sum at the end. The two
+  // half-waves of a query (lanes l and l ^ 32) merge each tile's max, so
+  // they share m.
   constexpr float kLog2e = 1.44269504088896340736f;
   auto exp_hw = [&](float x) { return __builtin_amdgcn_exp2f(x * kLog2e); };
   // exp(s - m) as exp2(s log2 e - m log2 e), one FMA per score with
@@ -182,48 +186,7 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     return __builtin_amdgcn_exp2f(__builtin_fmaf(sc, kLog2e, neg_ml));
   };
   float mx = ninf, sum = 0.0f;
-  sweep(false, [&](uint32_t tile, uint32_t sb) {
-    f32x16 s[2];
-    scores(sb, s);
-    mask_scores(tile, s);
-    float tmax = ninf;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kt][r]);
-    const float m_new = fmaxf(mx, tmax), neg_ml = -m_new * kLog2e;
-    float part = 0.0f;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) part = part + exp_shift(s[kt][r], neg_ml);
-    // no valid key yet (m_new = -inf, every s - m_new NaN): the sum stays 0
-    const float rescale = exp_hw(mx - m_new);
-    sum = m_new == ninf ? 0.0f : (mx == ninf ? part : sum * rescale + part);
-    mx = m_new;
-  });
-  // merge two (max, sum) pairs: the same two terms in either order
-  auto merge2 = [&](float &m, float &sm, float m2, float s2) {
-    const float m_row = fmaxf(m, m2);
-    const float a = m == ninf ? 0.0f : sm * exp_hw(m - m_row);
-    const float b = m2 == ninf ? 0.0f : s2 * exp_hw(m2 - m_row);
-    sm = a + b;
-    m = m_row;
-  };
-  merge2(mx, sum, xor32_f(mx), xor32_f(sum));  // the two half-waves
-  if constexpr (H > 1) {
-    // the key halves, merged in half order by every wave alike
-    merge[half][slot][0][lane] = mx;
-    merge[half][slot][1][lane] = sum;
-    __syncthreads();
-    mx = merge[0][slot][0][lane];
-    sum = merge[0][slot][1][lane];
-#pragma unroll
-    for (uint32_t h = 1; h < H; ++h) merge2(mx, sum, merge[h][slot][0][lane], merge[h][slot][1][lane]);
-  }
-  const float inv = 1.0f / sum, neg_ml = -mx * kLog2e;
-
-  // 2: p and O^T += V^T P^T; O^T tile dt: dims 32 dt + 8 (r / 4) + 4 hh + r % 4
+  // O^T tile dt: dims 32 dt + 8 (r / 4) + 4 hh + r % 4 of the lane's query
   f32x16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -238,16 +201,37 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     f32x16 s[2];
     scores(sb, s);
     mask_scores(tile, s);
-    // p = bf16(exp(s - M) * inv): the packing conversion is the rounding
-    // (M is finite: position 0 is every query's key; masked s - M = -inf
-    // gives 0)
-    uint32_t pk[2][8];
+    float tmax = ninf;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; r += 2)
-        pk[kt][r / 2] =
-            dma::cvt_pack<kBf16>(exp_shift(s[kt][r], neg_ml) * inv, exp_shift(s[kt][r + 1], neg_ml) * inv);
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kt][r]);
+    const float m_new = fmaxf(mx, fmaxf(tmax, xor32_f(tmax)));
+    if (__builtin_amdgcn_ballot_w64(m_new != mx)) {  // wave-uniform: some query's max grew
+      // no valid key before (mx = -inf): o and sum are still 0
+      const float a = mx == ninf ? 0.0f : exp_hw(mx - m_new);
+      sum *= a;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= a;
+    }
+    mx = m_new;
+    // no valid key yet (m = -inf): every score is -inf and gives p = 0
+    const float neg_ml = mx == ninf ? 0.0f : -mx * kLog2e;
+    // p = bf16(exp(s - m)): the packing conversion is the rounding; masked
+    // scores give 0
+    uint32_t pk[2][8];
+    float part = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float e0 = exp_shift(s[kt][r], neg_ml), e1 = exp_shift(s[kt][r + 1], neg_ml);
+        part = part + e0 + e1;
+        pk[kt][r / 2] = dma::cvt_pack<kBf16>(e0, e1);
+      }
+    sum += part;
     const uint32_t vb = sb + 16384u;
 #pragma unroll
     for (uint32_t ks = 0; ks < 4; ++ks) {
@@ -273,12 +257,15 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
       }
     }
   });
+  sum = sum + xor32_f(sum);  // the query's two half-waves (same m)
 
   if constexpr (H > 1) {
-    // half h > 0 leaves its partial O^T in the (now idle) stage memory; half
-    // 0 adds them in half order
+    // half h > 0 leaves (m, sum) and its partial O^T in LDS (the stage
+    // memory is idle after the sweep); half 0 merges them in half order
     float *po = reinterpret_cast<float *>(lds);
     if (half > 0) {
+      merge[half][slot][0][lane] = mx;
+      merge[half][slot][1][lane] = sum;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -287,21 +274,30 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     __syncthreads();
     if (half > 0) return;
 #pragma unroll
-    for (uint32_t h = 1; h < H; ++h)
+    for (uint32_t h = 1; h < H; ++h) {
+      const float m2 = merge[h][slot][0][lane], s2 = merge[h][slot][1][lane];
+      const float m_row = fmaxf(mx, m2);
+      const float a = mx == ninf ? 0.0f : exp_hw(mx - m_row);
+      const float b = m2 == ninf ? 0.0f : exp_hw(m2 - m_row);
+      sum = sum * a + s2 * b;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          o[dt][r] = o[dt][r] + po[(((h - 1) * kSlots + slot) * 64 + dt * 16 + r) * 64 + lane];
+          o[dt][r] = o[dt][r] * a + po[(((h - 1) * kSlots + slot) * 64 + dt * 16 + r) * 64 + lane] * b;
+      mx = m_row;
+    }
   }
+  // position 0 is a key of every query, so sum >= 1 for a query in range
+  const float inv = 1.0f / sum;
   if (t < T && t0 < T) {
     uint16_t *orow = out + (static_cast<uint64_t>(t) * heads + head) * kHeadDim;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const u32x2 w = {dma::cvt_pack<kBf16>(o[dt][4 * q], o[dt][4 * q + 1]),
-                         dma::cvt_pack<kBf16>(o[dt][4 * q + 2], o[dt][4 * q + 3])};
+        const u32x2 w = {dma::cvt_pack<kBf16>(o[dt][4 * q] * inv, o[dt][4 * q + 1] * inv),
+                         dma::cvt_pack<kBf16>(o[dt][4 * q + 2] * inv, o[dt][4 * q + 3] * inv)};
         *reinterpret_cast<u32x2 *>(orow + 32u * dt + 8u * q + 4u * hh) = w;
       }
   }
