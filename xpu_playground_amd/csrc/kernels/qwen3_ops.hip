@@ -1175,26 +1175,47 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_rmsnorm(const uint16
 
 // Hb[t][i] = bf16(bf16(silu(g)) u) for g = GU[t][i], u = GU[t][I + i]: the
 // SiLU-multiply after the MFMA form of the prompt's [gate; up] projection
-// (GU [T][2I], its gate and up halves side by side), the same rounding
-// points as the fused kernels (silu_mul_code). One thread per 8 outputs
-// (I % 8 == 0).
+// (GU [T][2I], its gate and up halves side by side). The rounding points
+// are silu_mul_code's; silu(g) = g * rcp(1 + exp2(-g log2 e)) takes the
+// hardware exp2 and reciprocal (a few FP32 ulps from the canonical exp and
+// the IEEE division; this prompt form is checked by tolerance). Block
+// (x, y): 8 outputs per thread at columns 8 (256 x + thread) of tokens
+// kPfSiluTok y .. + kPfSiluTok - 1, all loads issued before the math
+// (grid ceil(I / 2048) x ceil(T / kPfSiluTok); I % 8 == 0).
+constexpr uint32_t kPfSiluTok = 4;
 extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_silu_mul(const uint16_t *__restrict__ GU,
                                                                      uint16_t *__restrict__ Hb, uint32_t I,
                                                                      uint32_t T) {
-  const uint32_t per_row = I / 8u;
-  const uint64_t total = static_cast<uint64_t>(T) * per_row;
-  for (uint64_t c = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < total;
-       c += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    const uint64_t t = c / per_row, i = (c % per_row) * 8u;
-    const u32x4 g = *reinterpret_cast<const u32x4 *>(GU + t * 2u * I + i);
-    const u32x4 u = *reinterpret_cast<const u32x4 *>(GU + t * 2u * I + I + i);
-    const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+  const uint32_t i = (blockIdx.x * 256u + threadIdx.x) * 8u, t0 = blockIdx.y * kPfSiluTok;
+  if (i >= I) return;
+  constexpr float kLog2e = 1.44269504088896340736f;
+  u32x4 g[kPfSiluTok], u[kPfSiluTok];
+#pragma unroll
+  for (uint32_t k = 0; k < kPfSiluTok; ++k) {
+    const uint64_t t = min(t0 + k, T - 1u);  // tokens past the last re-read it (not stored)
+    g[k] = *reinterpret_cast<const u32x4 *>(GU + t * 2u * I + i);
+    u[k] = *reinterpret_cast<const u32x4 *>(GU + t * 2u * I + I + i);
+  }
+#pragma unroll
+  for (uint32_t k = 0; k < kPfSiluTok; ++k) {
+    if (t0 + k >= T) break;
+    const uint32_t gw[4] = {g[k].x, g[k].y, g[k].z, g[k].w}, uw[4] = {u[k].x, u[k].y, u[k].z, u[k].w};
     uint32_t hw[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      hw[q] = silu_mul_code(xpu::bf16_to_f32(gw[q] & 0xffffu), xpu::bf16_to_f32(uw[q] & 0xffffu)) |
-              (silu_mul_code(xpu::bf16_to_f32(gw[q] >> 16), xpu::bf16_to_f32(uw[q] >> 16)) << 16);
-    *reinterpret_cast<u32x4 *>(Hb + t * I + i) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+    for (int q = 0; q < 4; ++q) {
+      uint32_t h[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float gv = xpu::bf16_to_f32((gw[q] >> (16 * e)) & 0xffffu);
+        const float uv = xpu::bf16_to_f32((uw[q] >> (16 * e)) & 0xffffu);
+        // g -> -inf: exp2 = inf, rcp = 0, act = -0; g -> +inf: act = g
+        const float act =
+            xpu::round_bf16(gv * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gv * kLog2e)));
+        h[e] = xpu::f32_to_bf16(act * uv);
+      }
+      hw[q] = h[0] | (h[1] << 16);
+    }
+    *reinterpret_cast<u32x4 *>(Hb + static_cast<uint64_t>(t0 + k) * I + i) = u32x4{hw[0], hw[1], hw[2], hw[3]};
   }
 }
 

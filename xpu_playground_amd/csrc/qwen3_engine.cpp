@@ -590,9 +590,12 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
                    {{8, &e.pf_x}, {8, &L.post_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}, {4, &T}})))
         return rc;
       if (e.gemm_prefill) {
-        const uint32_t two_i = 2 * I, silu_grid = std::min<uint32_t>((T * (I / 8) + 255) / 256, 4096);
+        const uint32_t two_i = 2 * I;
         if ((rc = xpu::gemm_nt(rt, e.pf_xn, L.gu, e.pf_gu, T, two_i, H, false))) return rc;
-        if ((rc = go(e.pf_silu_k, silu_grid, 1, 256, 0, {{8, &e.pf_gu}, {8, &e.pf_h}, {4, &I}, {4, &T}}))) return rc;
+        // 8 columns per thread, 4 tokens per block row
+        if ((rc = go(e.pf_silu_k, (I + 2047) / 2048, (T + 3) / 4, 256, 0,
+                     {{8, &e.pf_gu}, {8, &e.pf_h}, {4, &I}, {4, &T}})))
+          return rc;
         if ((rc = xpu::gemm_nt(rt, e.pf_h, L.down, e.pf_x, T, H, I, true))) return rc;
         continue;
       }
