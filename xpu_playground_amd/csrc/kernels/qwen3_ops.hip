@@ -1400,37 +1400,46 @@ XPU_Q3_PF_GEMV(2, 2, 2)
 XPU_Q3_PF_GEMV(2, 2, 4)
 XPU_Q3_PF_GEMV(2, 2, 8)
 
-// QK-norm + RoPE of every token of the chunk: 16 head rows per 256-thread
-// block, one per 16 lanes: head h of tokens 16 b .. 16 b + 15 for block
-// (b, h) (grid ceil(T / 16) x (heads + kv_heads)), so a chunk's cache
-// writes of a wavefront are 64 contiguous bytes. h < heads: roped q of head
-// h into Q[t]; else kv head h - heads: roped k and the v row into the
-// engine caches at position p0 + t.
+// QK-norm + RoPE of every token of the chunk: 32 head rows per 256-thread
+// block, two per 16 lanes: head h of tokens 32 b .. 32 b + 31 for block
+// (b, h) (grid ceil(T / 32) x (heads + kv_heads)), lanes of row r taking
+// tokens 32 b + r and 32 b + 16 + r, both rows' loads issued before either
+// row's math; a chunk's cache writes of a wavefront are 64 contiguous
+// bytes. h < heads: roped q of head h into Q[t]; else kv head h - heads:
+// roped k and the v row into the engine caches at position p0 + t.
+constexpr uint32_t kPfRopeRows = 2;  // token rows per 16 lanes
 extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_rope_cache(
     const uint16_t *__restrict__ QKV, const uint16_t *__restrict__ qnorm_w, const uint16_t *__restrict__ knorm_w,
     const uint16_t *__restrict__ rope_cos, const uint16_t *__restrict__ rope_sin, uint16_t *__restrict__ kcache,
     uint16_t *__restrict__ vcache, uint16_t *__restrict__ Q, uint32_t p0, uint32_t T, uint32_t heads,
     uint32_t kv_heads, uint32_t max_seq, float eps) {
   const uint32_t l16 = threadIdx.x & 15u, h = blockIdx.y;
-  // tokens past the last are clamped onto it (recomputed, stored identically)
-  const uint32_t t = min(blockIdx.x * 16u + (threadIdx.x >> 4), T - 1u), pos = p0 + t;
   const uint32_t row_len = (heads + 2 * kv_heads) * xpu::kHeadDim;
-  const uint16_t *row = QKV + static_cast<uint64_t>(t) * row_len;
   const bool is_q = h < heads;
   const uint32_t kvh = is_q ? 0 : h - heads;
-  const uint16_t *src = row + h * xpu::kHeadDim;  // q heads, then k heads
-  const u32x4 hx = *reinterpret_cast<const u32x4 *>(src + l16 * 8u);
   const u32x4 hw = *reinterpret_cast<const u32x4 *>((is_q ? qnorm_w : knorm_w) + l16 * 8u);
-  const u32x4 hc = *reinterpret_cast<const u32x4 *>(rope_cos + static_cast<uint64_t>(pos) * xpu::kHeadDim + l16 * 8u);
-  const u32x4 hs = *reinterpret_cast<const u32x4 *>(rope_sin + static_cast<uint64_t>(pos) * xpu::kHeadDim + l16 * 8u);
-  // K and V: chunk-major [kv_head][16][max_seq][8]
-  const uint64_t kslot = static_cast<uint64_t>(kvh) * max_seq * xpu::kHeadDim + static_cast<uint64_t>(pos) * 8u;
-  uint16_t *dst = is_q ? Q + static_cast<uint64_t>(t) * heads * xpu::kHeadDim + h * xpu::kHeadDim : kcache + kslot;
-  xpu::head_norm_rope_rows16(hx, hw, hc, hs, eps, dst, is_q ? 8u : static_cast<uint64_t>(max_seq) * 8u);
-  if (!is_q) {
-    const uint16_t *vsrc = row + (heads + kv_heads + kvh) * xpu::kHeadDim;
-    *reinterpret_cast<u32x4 *>(vcache + kslot + l16 * static_cast<uint64_t>(max_seq) * 8u) =
-        *reinterpret_cast<const u32x4 *>(vsrc + l16 * 8u);
+  uint32_t t[kPfRopeRows];
+  u32x4 hx[kPfRopeRows], hc[kPfRopeRows], hs[kPfRopeRows], hv[kPfRopeRows];
+#pragma unroll
+  for (uint32_t r = 0; r < kPfRopeRows; ++r) {
+    // tokens past the last are clamped onto it (recomputed, stored identically)
+    t[r] = min(blockIdx.x * 16u * kPfRopeRows + 16u * r + (threadIdx.x >> 4), T - 1u);
+    const uint16_t *row = QKV + static_cast<uint64_t>(t[r]) * row_len;
+    const uint64_t pos = p0 + t[r];
+    hx[r] = *reinterpret_cast<const u32x4 *>(row + h * xpu::kHeadDim + l16 * 8u);  // q heads, then k heads
+    hc[r] = *reinterpret_cast<const u32x4 *>(rope_cos + pos * xpu::kHeadDim + l16 * 8u);
+    hs[r] = *reinterpret_cast<const u32x4 *>(rope_sin + pos * xpu::kHeadDim + l16 * 8u);
+    // the v row (kv heads only; q heads re-read their own row, unused)
+    hv[r] = *reinterpret_cast<const u32x4 *>(row + (is_q ? h : heads + kv_heads + kvh) * xpu::kHeadDim + l16 * 8u);
+  }
+#pragma unroll
+  for (uint32_t r = 0; r < kPfRopeRows; ++r) {
+    const uint32_t pos = p0 + t[r];
+    // K and V: chunk-major [kv_head][16][max_seq][8]
+    const uint64_t kslot = static_cast<uint64_t>(kvh) * max_seq * xpu::kHeadDim + static_cast<uint64_t>(pos) * 8u;
+    uint16_t *dst = is_q ? Q + static_cast<uint64_t>(t[r]) * heads * xpu::kHeadDim + h * xpu::kHeadDim : kcache + kslot;
+    xpu::head_norm_rope_rows16(hx[r], hw, hc[r], hs[r], eps, dst, is_q ? 8u : static_cast<uint64_t>(max_seq) * 8u);
+    if (!is_q) *reinterpret_cast<u32x4 *>(vcache + kslot + l16 * static_cast<uint64_t>(max_seq) * 8u) = hv[r];
   }
 }
 

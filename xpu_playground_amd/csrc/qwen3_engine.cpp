@@ -552,7 +552,7 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
                           {{8, &L.qkv}, {8, &e.pf_xn}, {8, &e.pf_qkv}, {4, &qkv_rows}, {4, &T}}))) {
         return rc;
       }
-      if ((rc = go(e.pf_rope_k, (T + 15) / 16, heads + kv, 256, 0,
+      if ((rc = go(e.pf_rope_k, (T + 31) / 32, heads + kv, 256, 0,
                    {{8, &e.pf_qkv}, {8, &L.q_norm}, {8, &L.k_norm}, {8, &e.cos_t}, {8, &e.sin_t}, {8, &kc},
                     {8, &vc}, {8, &e.pf_q}, {4, &p0}, {4, &T}, {4, &heads}, {4, &kv}, {4, &max_seq}, {4, &eps}})))
         return rc;
