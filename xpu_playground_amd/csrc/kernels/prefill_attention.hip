@@ -7,9 +7,10 @@
 // (qwen3/kernels.hpp:157-192 as restated by the oracle), then an online
 // softmax in one sweep over the key tiles, as the reference's own kernel
 // runs it (FP32 running max and sum, kernels.hpp:174-190): per query a
-// running max m, p = bf16(exp(s - m)) as the P.V MFMA operand, the FP32 sum
-// of exp(s - m) and the FP32 output rescaled by exp(m_old - m_new) when m
-// grows, and out = bf16(O / sum) at the end. The decode path (bit-exact
+// reference max m, p = bf16(exp(s - m)) as the P.V MFMA operand, the FP32
+// sum of exp(s - m) and the FP32 output rescaled by exp(m_old - m_new) when
+// a score passes m by more than 8 ln 2 (so p <= 256 and rescales are rare),
+// and out = bf16(O / sum) at the end. The decode path (bit-exact
 // against the CPU oracle) instead rounds p = bf16(exp(s - M) / sum) with
 // the final max M; the exponential here is the hardware's exp2 (v_exp_f32
 // of s log2 e - m log2 e; the reference's kernel uses the device exp too),
@@ -172,13 +173,14 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     __syncthreads();  // the next sweep's first DMA reuses stage 0
   };
 
-  // One sweep, online softmax: per lane (query) a running max m, the FP32
+  // One sweep, online softmax: per lane (query) a reference max m, the FP32
   // sum of exp(s - m) and the FP32 O^T columns, both rescaled by
-  // exp(m_old - m_new) when the max grows; p = bf16(exp(s - m)) feeds the
-  // P.V MFMA, and the output is divided by the sum at the end. The two
+  // exp(m_old - m_new) when m moves; p = bf16(exp(s - m)) feeds the P.V
+  // MFMA, and the output is divided by the sum at the end. The two
   // half-waves of a query (lanes l and l ^ 32) merge each tile's max, so
   // they share m.
   constexpr float kLog2e = 1.44269504088896340736f;
+  constexpr float kLazy = 5.54517744447956247533f;  // 8 ln 2
   auto exp_hw = [&](float x) { return __builtin_amdgcn_exp2f(x * kLog2e); };
   // exp(s - m) as exp2(s log2 e - m log2 e), one FMA per score with
   // neg_ml = -m log2 e formed once per tile
@@ -206,8 +208,13 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kt][r]);
-    const float m_new = fmaxf(mx, fmaxf(tmax, xor32_f(tmax)));
-    if (__builtin_amdgcn_ballot_w64(m_new != mx)) {  // wave-uniform: some query's max grew
+    // the reference max m moves only when a score exceeds it by more than
+    // 8 ln 2, so exp(s - m) <= 256 (exact in scale for bf16 p and the FP32
+    // sums) and the rescale of o and sum is rare after the first tiles
+    const float m_tile = fmaxf(tmax, xor32_f(tmax));
+    const bool grow = m_tile > mx + kLazy;  // mx = -inf: any valid key
+    if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform: some query's reference moves
+      const float m_new = grow ? m_tile : mx;
       // no valid key before (mx = -inf): o and sum are still 0
       const float a = mx == ninf ? 0.0f : exp_hw(mx - m_new);
       sum *= a;
@@ -215,8 +222,8 @@ XPU_DEVICE void prefill_attention(const uint16_t *__restrict__ Q, const uint16_t
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= a;
+      mx = m_new;
     }
-    mx = m_new;
     // no valid key yet (m = -inf): every score is -inf and gives p = 0
     const float neg_ml = mx == ninf ? 0.0f : -mx * kLog2e;
     // p = bf16(exp(s - m)): the packing conversion is the rounding; masked
