@@ -205,11 +205,13 @@ def test_command_line_matches_oracle(tmp_path):
 
 
 @pytest.mark.parametrize("preset,n_prompt,max_seq", [("small", 40, 96), ("small", 2, 16), ("small", 1, 16),
-                                                      ("small", 300, 320)])
+                                                      ("small", 300, 320), ("small", 256, 272), ("small", 257, 272)])
 def test_batched_prefill_bit_identical(rt, preset, n_prompt, max_seq):
-    # the prompt positions before the last in one batch per layer (chunks
-    # of 256 positions): same tokens, logits and hidden state as feeding the
-    # prompt through decode one position at a time, and as the oracle
+    # every prompt position in one batch per layer (chunks of 256 positions;
+    # 257 leaves the last position alone in its chunk), the last position
+    # finished by the decode step's kernels: same tokens, logits and hidden
+    # state as feeding the prompt through decode one position at a time, and
+    # as the oracle, for the first generated token and after 16 more
     cfg = orc.config(preset)
     new = min(16, max_seq - n_prompt)
     prompt = orc.tokens(n_prompt, 12, cfg.vocab)
@@ -229,6 +231,12 @@ def test_batched_prefill_bit_identical(rt, preset, n_prompt, max_seq):
         assert np.array_equal(logits, ref_logits[new - 1]), key
         assert np.array_equal(hidden, m.hidden()), key
     print({k: round(v[3], 3) for k, v in results.items()})
+    # the first generated token alone: the prompt's own last step
+    eng.set_prefill(True)
+    eng.set_mode(qwen3.GRAPH)
+    out, _, _ = eng.generate(prompt, 1, stop_on_eos=False)
+    assert out.tolist() == ref.tolist()[:1]
+    assert np.array_equal(eng.logits(), ref_logits[0])
     eng.close()
 
 
@@ -335,7 +343,8 @@ def test_mode_switch_mid_sequence_is_rejected(rt):
 # attention output is not used, the last layer stops at its caches; the MFMA
 # attention with p0 > 0 is covered by test_gpu_prefill_attention.py)
 GEMM_PROMPT_CASES = [("small", {}, 40, 96), ("small", {}, 300, 320), ("small", {}, 2, 16), ("tiny", {}, 30, 48),
-                     ("qwen3-8b", {"layers": 2, "vocab": 4096}, 24, 40), ("tiny", {"layers": 1}, 4110, 4160)]
+                     ("qwen3-8b", {"layers": 2, "vocab": 4096}, 24, 40), ("tiny", {"layers": 1}, 4110, 4160),
+                     ("tiny", {"layers": 1}, 4097, 4112)]
 
 
 @pytest.mark.parametrize("preset,over,n_prompt,max_seq", GEMM_PROMPT_CASES)
