@@ -1093,12 +1093,13 @@ extern "C" __global__ __launch_bounds__(1024) void xpu_q3_argmax_finish(
 
 // ------------------------------------------------------------ batched prefill
 //
-// Part 3: the prompt positions before the last one go through the model as
-// one batch per layer (only their K/V cache entries are needed; the last
-// prompt position runs through the decode step, which produces the first
-// generated token). Every value is computed with the same operations in the
-// same order as the decode kernels, so the cache contents are bit-identical
-// to decoding the prompt one position at a time (qwen3/main.cpp:343-344).
+// Part 3: the prompt positions go through the model as one batch per layer
+// (the K/V cache entries of every position; the engine finishes the last
+// position's last layer and head with the decode step's kernels, which
+// produce the first generated token). Every value is computed with the same
+// operations in the same order as the decode kernels, so the cache contents
+// and that token's logits are bit-identical to decoding the prompt one
+// position at a time (qwen3/main.cpp:343-344).
 // Buffers hold T tokens of a chunk: X, Xn [T][H], QKV [T][(Hq+2Hkv)*128],
 // Q and A [T][Hq*128], Hb [T][I].
 
