@@ -1225,7 +1225,10 @@ namespace {
 // Batched canonical GEMV: Out[t][row] for rows of W (M x K, K = 512 NC) and
 // token rows In[t] (T x K). A wavefront holds R rows (PAIRED: rows i and
 // I + i of a [gate; up] matrix, M = I) in registers for the whole token
-// loop; the block stages TT token rows at a time in LDS. Each (row, token)
+// loop; the block stages TT token rows at a time in LDS, for token group
+// blockIdx.y of gridDim.y (whole tiles; more rows per wavefront share each
+// staged token's unpacking among more FMAs, and the token groups keep the
+// block count up). Each (row, token)
 // dot product is the decode GEMV's: lane l, slot s accumulate elements
 // c*512 + 8 l + s over chunks c in order (FMA), then fold8 and the xor
 // butterfly. EPI 0: Out = bf16(y); 1: Out = bf16(Out + bf16(y)) (residual);
@@ -1289,7 +1292,7 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
     for (int c = 0; c < NC; ++c) a[r][c] = xpu::load_nt16(p + c * 512u);
   }
   // the rows unpacked to FP32 once, when that fits the registers
-  constexpr bool kHoist = R * NC <= 8;
+  constexpr bool kHoist = R * NC <= 12;
   float af[kHoist ? R : 1][kHoist ? NC : 1][8];
   if constexpr (kHoist) {
 #pragma unroll
@@ -1312,12 +1315,16 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
 #pragma unroll
     for (int q = 0; q < kLoads; ++q) *reinterpret_cast<u32x4 *>(buf + (threadIdx.x + q * 256u) * 8u) = stage[q];
   };
-  load_tile(0);
+  // token group blockIdx.y of gridDim.y: tokens [t_beg, t_end), whole tiles
+  const uint32_t per_group = ((T + gridDim.y - 1) / gridDim.y + TT - 1) / TT * TT;
+  const uint32_t t_beg = blockIdx.y * per_group, t_end = min(T, t_beg + per_group);
+  if (t_beg >= t_end) return;  // whole block
+  load_tile(t_beg);
   store_tile(xt);
   __syncthreads();
   uint32_t cur = 0;
-  for (uint32_t t0 = 0; t0 < T; t0 += TT) {
-    const bool more = t0 + TT < T;
+  for (uint32_t t0 = t_beg; t0 < t_end; t0 += TT) {
+    const bool more = t0 + TT < t_end;
     if (more) load_tile(t0 + TT);
     const uint16_t *tile = xt + cur * kTile;
     static_assert(TT == 8, "token_butterfly8 reduces 8 tokens");
@@ -1384,21 +1391,23 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
 
 }  // namespace
 
+// xpu_q3_pf_gemv_e<EPI>_c<NC>_r<R>: R as large as fits the registers
+// without spills (the engine takes the largest R the module has)
 #define XPU_Q3_PF_GEMV(EPI, R, NC)                                                                  \
-  extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_gemv_e##EPI##_c##NC(                 \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_gemv_e##EPI##_c##NC##_r##R(          \
       const uint16_t *__restrict__ W, const uint16_t *__restrict__ In, uint16_t *Out, uint32_t M,  \
       uint32_t T) {                                                                                 \
     pf_gemv<R, NC, 8, EPI>(W, In, Out, M, T);                                                       \
   }
-XPU_Q3_PF_GEMV(0, 2, 2)
-XPU_Q3_PF_GEMV(0, 2, 4)
+XPU_Q3_PF_GEMV(0, 4, 2)
+XPU_Q3_PF_GEMV(0, 4, 4)
 XPU_Q3_PF_GEMV(0, 2, 8)
-XPU_Q3_PF_GEMV(1, 1, 2)
-XPU_Q3_PF_GEMV(1, 1, 4)
-XPU_Q3_PF_GEMV(1, 1, 6)
+XPU_Q3_PF_GEMV(1, 2, 2)
+XPU_Q3_PF_GEMV(1, 2, 4)
+XPU_Q3_PF_GEMV(1, 2, 6)
 XPU_Q3_PF_GEMV(1, 1, 8)
-XPU_Q3_PF_GEMV(2, 2, 2)
-XPU_Q3_PF_GEMV(2, 2, 4)
+XPU_Q3_PF_GEMV(2, 4, 2)
+XPU_Q3_PF_GEMV(2, 4, 4)
 XPU_Q3_PF_GEMV(2, 2, 8)
 
 // QK-norm + RoPE of every token of the chunk: 32 head rows per 256-thread

@@ -173,6 +173,8 @@ struct xpu_qwen3 {
   const xpu::KernelInfo *pf_attn_short_k = nullptr;  // chunks whose contexts stay within 256 positions
   const xpu::KernelInfo *pf_embed_k = nullptr, *pf_norm_k = nullptr, *pf_rope_k = nullptr, *pf_attn_k = nullptr,
                         *pf_qkv_k = nullptr, *pf_o_k = nullptr, *pf_gu_k = nullptr, *pf_down_k = nullptr;
+  // rows per wavefront of those four batched GEMV kernels (their _r<R>)
+  uint32_t pf_qkv_r = 0, pf_o_r = 0, pf_gu_r = 0, pf_down_r = 0;
 
   ~xpu_qwen3() {
     if (graph) xpu_rt_graph_destroy(graph);
@@ -376,14 +378,23 @@ int setup_launches(xpu_qwen3 &e) {
 int setup_prefill(xpu_qwen3 &e) {
   const xpu_qwen3_config &c = e.c;
   const uint32_t qd = c.heads * c.head_dim;
-  auto gemv = [&](int epi, uint32_t K) -> const xpu::KernelInfo * {
+  // the kernel with the most rows per wavefront the module has
+  auto gemv = [&](int epi, uint32_t K, uint32_t &r) -> const xpu::KernelInfo * {
     if (K % 512u) return nullptr;
-    return e.rt->find_exact("xpu_q3_pf_gemv_e" + std::to_string(epi) + "_c" + std::to_string(K / 512u));
+    for (uint32_t rows : {4u, 2u, 1u}) {
+      const xpu::KernelInfo *k = e.rt->find_exact("xpu_q3_pf_gemv_e" + std::to_string(epi) + "_c" +
+                                                  std::to_string(K / 512u) + "_r" + std::to_string(rows));
+      if (k) {
+        r = rows;
+        return k;
+      }
+    }
+    return nullptr;
   };
-  e.pf_qkv_k = gemv(0, c.hidden);
-  e.pf_o_k = gemv(1, qd);
-  e.pf_gu_k = gemv(2, c.hidden);
-  e.pf_down_k = gemv(1, c.intermediate);
+  e.pf_qkv_k = gemv(0, c.hidden, e.pf_qkv_r);
+  e.pf_o_k = gemv(1, qd, e.pf_o_r);
+  e.pf_gu_k = gemv(2, c.hidden, e.pf_gu_r);
+  e.pf_down_k = gemv(1, c.intermediate, e.pf_down_r);
   e.pf_embed_k = e.rt->find_exact("xpu_q3_pf_embed");
   e.pf_norm_k = e.rt->find_exact("xpu_q3_pf_rmsnorm");
   e.pf_rope_k = e.rt->find_exact("xpu_q3_pf_rope_cache");
@@ -538,6 +549,11 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
   const uint32_t chunk = e.gemm_prefill ? e.pf_chunk_gemm : e.pf_chunk;
   for (uint32_t p0 = 0; p0 < P; p0 += chunk) {
     uint32_t T = std::min(chunk, P - p0);
+    // batched GEMV grids: 4 wavefronts of R rows (R / 2 output pairs for
+    // [gate; up]) per block; past one token tile, the tokens split into
+    // R / 2 groups (R for the residual forms), which keeps the block count
+    // of 2-row (1-row) wavefronts over all tokens
+    auto groups = [&](uint32_t r, uint32_t base) { return T > 8 ? std::max(1u, r / base) : 1u; };
     if ((rc = go(e.pf_embed_k, T, 1, 256, 0, {{8, &e.embed}, {8, &e.prompt}, {4, &p0}, {8, &e.pf_x}, {4, &H}, {4, &V}})))
       return rc;
     for (uint32_t l = 0; l < c.layers; ++l) {
@@ -548,7 +564,8 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
         return rc;
       if (e.gemm_prefill) {
         if ((rc = xpu::gemm_nt(rt, e.pf_xn, L.qkv, e.pf_qkv, T, qkv_rows, H, false))) return rc;
-      } else if ((rc = go(e.pf_qkv_k, (qkv_rows + 7) / 8, 1, 256, pf_lds(H),
+      } else if ((rc = go(e.pf_qkv_k, (qkv_rows + 4 * e.pf_qkv_r - 1) / (4 * e.pf_qkv_r), groups(e.pf_qkv_r, 2), 256,
+                          pf_lds(H),
                           {{8, &L.qkv}, {8, &e.pf_xn}, {8, &e.pf_qkv}, {4, &qkv_rows}, {4, &T}}))) {
         return rc;
       }
@@ -582,7 +599,7 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
       }
       if (e.gemm_prefill) {
         if ((rc = xpu::gemm_nt(rt, e.pf_a, L.o, e.pf_x, T, H, qd, true))) return rc;
-      } else if ((rc = go(e.pf_o_k, (H + 3) / 4, 1, 256, pf_lds(qd),
+      } else if ((rc = go(e.pf_o_k, (H + 4 * e.pf_o_r - 1) / (4 * e.pf_o_r), groups(e.pf_o_r, 1), 256, pf_lds(qd),
                           {{8, &L.o}, {8, &e.pf_a}, {8, &e.pf_x}, {4, &H}, {4, &T}}))) {
         return rc;
       }
@@ -599,9 +616,12 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
         if ((rc = xpu::gemm_nt(rt, e.pf_h, L.down, e.pf_x, T, H, I, true))) return rc;
         continue;
       }
-      if ((rc = go(e.pf_gu_k, (I + 3) / 4, 1, 256, pf_lds(H), {{8, &L.gu}, {8, &e.pf_xn}, {8, &e.pf_h}, {4, &I}, {4, &T}})))
+      if ((rc = go(e.pf_gu_k, (I + 2 * e.pf_gu_r - 1) / (2 * e.pf_gu_r), groups(e.pf_gu_r, 2), 256, pf_lds(H),
+                   {{8, &L.gu}, {8, &e.pf_xn}, {8, &e.pf_h}, {4, &I}, {4, &T}})))
         return rc;
-      if ((rc = go(e.pf_down_k, (H + 3) / 4, 1, 256, pf_lds(I), {{8, &L.down}, {8, &e.pf_h}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
+      if ((rc = go(e.pf_down_k, (H + 4 * e.pf_down_r - 1) / (4 * e.pf_down_r), groups(e.pf_down_r, 1), 256,
+                   pf_lds(I),
+                   {{8, &L.down}, {8, &e.pf_h}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
         return rc;
     }
   }
