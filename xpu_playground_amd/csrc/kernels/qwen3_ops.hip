@@ -1268,7 +1268,7 @@ XPU_DEVICE float token_butterfly8(float (&v)[8]) {
   return s;
 }
 
-template <int R, int NC, int TT, int EPI>
+template <int R, int NC, int TT, int EPI, bool HOIST = (R * NC <= 12)>
 XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restrict__ In, uint16_t *Out, uint32_t M,
                         uint32_t T) {
   constexpr uint32_t K = 512u * NC;
@@ -1292,7 +1292,7 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
     for (int c = 0; c < NC; ++c) a[r][c] = xpu::load_nt16(p + c * 512u);
   }
   // the rows unpacked to FP32 once, when that fits the registers
-  constexpr bool kHoist = R * NC <= 12;
+  constexpr bool kHoist = HOIST;
   float af[kHoist ? R : 1][kHoist ? NC : 1][8];
   if constexpr (kHoist) {
 #pragma unroll
@@ -1392,18 +1392,26 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
 }  // namespace
 
 // xpu_q3_pf_gemv_e<EPI>_c<NC>_r<R>: R as large as fits the registers
-// without spills (the engine takes the largest R the module has)
+// without spills (the engine takes the largest R the module has); _H: the
+// rows held unpacked regardless of size
 #define XPU_Q3_PF_GEMV(EPI, R, NC)                                                                  \
   extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_gemv_e##EPI##_c##NC##_r##R(          \
       const uint16_t *__restrict__ W, const uint16_t *__restrict__ In, uint16_t *Out, uint32_t M,  \
       uint32_t T) {                                                                                 \
     pf_gemv<R, NC, 8, EPI>(W, In, Out, M, T);                                                       \
   }
+#define XPU_Q3_PF_GEMV_H(EPI, R, NC)                                                                \
+  extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_gemv_e##EPI##_c##NC##_r##R(          \
+      const uint16_t *__restrict__ W, const uint16_t *__restrict__ In, uint16_t *Out, uint32_t M,  \
+      uint32_t T) {                                                                                 \
+    pf_gemv<R, NC, 8, EPI, true>(W, In, Out, M, T);                                                 \
+  }
 XPU_Q3_PF_GEMV(0, 4, 2)
 XPU_Q3_PF_GEMV(0, 4, 4)
 XPU_Q3_PF_GEMV(0, 2, 8)
 XPU_Q3_PF_GEMV(1, 2, 2)
 XPU_Q3_PF_GEMV(1, 2, 4)
+XPU_Q3_PF_GEMV_H(1, 4, 4)
 XPU_Q3_PF_GEMV(1, 2, 6)
 XPU_Q3_PF_GEMV(1, 1, 8)
 XPU_Q3_PF_GEMV(2, 4, 2)
