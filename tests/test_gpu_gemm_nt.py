@@ -139,3 +139,42 @@ def test_splitk(rt, res, m, n, k, spl):
     else:
         wt = np.ascontiguousarray(w.reshape(n, k).T).reshape(-1)
         check(got, a, wt, m, n, k, xpu.BF16)
+
+
+@pytest.mark.parametrize("m,n,k,spl", [(127, 1024, 3072, 4), (300, 512, 1032, 4), (1, 1024, 256, 4),
+                                       (129, 1024, 3072, 8), (64, 512, 4096, 4)])
+def test_splitk_reduce_norm(rt, m, n, k, spl):
+    # the reduction fused with the RMSNorm of its rows writes the same C as
+    # xpu_gemm_splitk_reduce and the same normalised rows as
+    # xpu_q3_pf_rmsnorm on that C, bit for bit
+    slices = (k + 63) // 64
+    splits = (slices + spl - 1) // spl
+    tiles = ((m + 127) // 128) * ((n + 63) // 64)
+    a = orc.uniform(m * k, 230 + m, xpu.BF16)
+    w = orc.uniform(n * k, 240 + n, xpu.BF16)
+    old = orc.uniform(m * n, 250 + k, xpu.BF16)
+    gains = orc.encode(1.0 + 0.1 * orc.decode(orc.uniform(n, 260, xpu.BF16), xpu.BF16), xpu.BF16)
+    eps = 1e-6
+    da, dw, dg = rt.upload(a), rt.upload(w), rt.upload(gains)
+    dc1, dc2 = rt.upload(old), rt.upload(old)
+    dx1, dx2 = rt.alloc(m * n * 2), rt.alloc(m * n * 2)
+    dp = rt.alloc(splits * m * n * 4)
+    try:
+        print(f"split-K reduce + norm {m}x{n}x{k} spl {spl} splits {splits}", flush=True)
+        args = Args().ptr(da).ptr(dw).ptr(dp).u32(m).u32(n).u32(k).u32(spl).u32(n).u32(n)
+        rt.launch_grid("xpu_gemm_bf16_n64_nt_part_dma", tiles * splits, 256, 0, args)
+        rt.launch_grid("xpu_gemm_splitk_reduce_norm", (m + 3) // 4, 256, 0,
+                       Args().ptr(dp).ptr(dc1).u32(m).u32(n).u32(splits).u32(1).ptr(dg).ptr(dx1).f32(eps))
+        rt.launch_grid("xpu_gemm_splitk_reduce", max(1, min((m * n // 8 + 255) // 256, 2048)), 256, 0,
+                       Args().ptr(dp).ptr(dc2).u32(m).u32(n).u32(splits).u32(1))
+        rt.launch_grid("xpu_q3_pf_rmsnorm", (m + 3) // 4, 256, 0,
+                       Args().ptr(dc2).ptr(dg).ptr(dx2).u32(n).f32(eps).u32(m))
+        rt.synchronize()
+        c1, c2 = rt.download(dc1, m * n, np.uint16), rt.download(dc2, m * n, np.uint16)
+        x1, x2 = rt.download(dx1, m * n, np.uint16), rt.download(dx2, m * n, np.uint16)
+    finally:
+        for p in (da, dw, dg, dc1, dc2, dx1, dx2, dp):
+            rt.free(p)
+    assert np.array_equal(c1, c2)
+    assert np.array_equal(x1, x2)
+    check_residual(c1.reshape(m, n), old, a, w, m, n, k)

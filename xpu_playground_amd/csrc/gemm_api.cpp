@@ -165,7 +165,8 @@ uint64_t gemm_nt_workspace_bound(const xpu_runtime *rt) {
 }
 
 int gemm_nt(xpu_runtime *rt, const void *A, const void *W, void *C, uint32_t M, uint32_t N, uint32_t K,
-            bool residual) {
+            bool residual, const void *norm_w, void *Xn, float eps, bool *normed) {
+  if (normed) *normed = false;
   if (!rt || !A || !W || !C) return set_error(XPU_ERR_INVALID, "gemm_nt: null argument");
   if (M == 0 || N == 0 || K == 0 || K % 8 || N % 8 || (reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(W) |
                                                        reinterpret_cast<uintptr_t>(C)) % 16)
@@ -205,6 +206,14 @@ int gemm_nt(xpu_runtime *rt, const void *A, const void *W, void *C, uint32_t M, 
       const xpu_kernel_arg pargs[] = {{8, &A}, {8, &W},  {8, &part}, {4, &M},    {4, &N},
                                       {4, &K}, {4, &kb}, {4, &ldc},  {4, &n_out}};
       if ((rc = rt->launch(*kp, static_cast<uint32_t>(tiles * splits), 1, 256, 0, pargs, 9))) return rc;
+      const xpu::KernelInfo *kn = rt->find_exact("xpu_gemm_splitk_reduce_norm");
+      if (norm_w && Xn && normed && kn && (N == 512 || N == 1024)) {
+        const xpu_kernel_arg nargs[] = {{8, &part}, {8, &C},      {4, &M},  {4, &N},  {4, &nsplit},
+                                        {4, &res},  {8, &norm_w}, {8, &Xn}, {4, &eps}};
+        if ((rc = rt->launch(*kn, (M + 3) / 4, 1, 256, 0, nargs, 9))) return rc;
+        *normed = true;
+        return XPU_OK;
+      }
       const uint64_t threads = static_cast<uint64_t>(M) * N / 8;
       const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>((threads + 255) / 256, rt->compute_units * 8ull));
       const xpu_kernel_arg rargs[] = {{8, &part}, {8, &C}, {4, &M}, {4, &N}, {4, &nsplit}, {4, &res}};

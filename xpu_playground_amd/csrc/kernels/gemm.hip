@@ -629,6 +629,99 @@ extern "C" __global__ __launch_bounds__(256) void xpu_gemm_splitk_reduce(const f
   }
 }
 
+// The same reduction fused with the RMSNorm of the rows it completes (the
+// next kernel's input in the Qwen3 prompt): one wavefront per row, lane l
+// holding columns 512 c + 8 l .. + 7 (N = 512 or 1024); row = bf16(C +
+// bf16(y)) (or bf16(y)) as xpu_gemm_splitk_reduce writes it, then Xn =
+// bf16(w * bf16(row * (1 / sqrt(sum(row^2) / N + eps)))) with the sum of
+// squares in the order of xpu_q3_pf_rmsnorm (per-lane slots over the
+// chunks, fold8, 64-lane butterfly). The partials of up to 4 splits, both
+// chunks and the residual are loaded before any addition; the splits are
+// still added in order. Grid ceil(M / 4) blocks of 256.
+extern "C" __global__ __launch_bounds__(256) void xpu_gemm_splitk_reduce_norm(
+    const float *__restrict__ P, uint16_t *__restrict__ C, uint32_t M, uint32_t N, uint32_t splits,
+    uint32_t residual, const uint16_t *__restrict__ norm_w, uint16_t *__restrict__ Xn, float eps) {
+  constexpr uint32_t kChunks = 2, kBatch = 4;  // N <= 1024; splits loaded 4 at a time
+  const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+  if (row >= M) return;  // whole wavefronts
+  const uint32_t nc = N / 512u;
+  const uint64_t mn4 = static_cast<uint64_t>(M) * N / 4u;  // one split, in float4
+  const float4 *p[kChunks];
+  xpu::u32x4 old[kChunks];
+  float4 lo[kChunks], hi[kChunks];
+#pragma unroll
+  for (uint32_t c = 0; c < kChunks; ++c) {
+    const uint32_t cc = c < nc ? c : 0u;  // a chunk past N re-reads chunk 0 (not used)
+    const uint64_t off = static_cast<uint64_t>(row) * N + cc * 512u + lane * 8u;
+    p[c] = reinterpret_cast<const float4 *>(P + off);
+    old[c] = residual ? *reinterpret_cast<const xpu::u32x4 *>(C + off) : xpu::u32x4{0, 0, 0, 0};
+    lo[c] = p[c][0];
+    hi[c] = p[c][1];
+  }
+  for (uint32_t s0 = 1; s0 < splits; s0 += kBatch) {
+    float4 a[kBatch][kChunks], b[kBatch][kChunks];
+#pragma unroll
+    for (uint32_t k = 0; k < kBatch; ++k) {
+      const uint64_t s = min(s0 + k, splits - 1u);  // past the last split: re-read it (not added)
+#pragma unroll
+      for (uint32_t c = 0; c < kChunks; ++c) {
+        a[k][c] = p[c][s * mn4];
+        b[k][c] = p[c][s * mn4 + 1];
+      }
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kBatch; ++k) {
+      if (s0 + k >= splits) break;  // uniform
+#pragma unroll
+      for (uint32_t c = 0; c < kChunks; ++c) {
+        lo[c] = float4{lo[c].x + a[k][c].x, lo[c].y + a[k][c].y, lo[c].z + a[k][c].z, lo[c].w + a[k][c].w};
+        hi[c] = float4{hi[c].x + b[k][c].x, hi[c].y + b[k][c].y, hi[c].z + b[k][c].z, hi[c].w + b[k][c].w};
+      }
+    }
+  }
+  xpu::u32x4 xc[kChunks];
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (uint32_t c = 0; c < kChunks; ++c) {
+    if (c >= nc) break;  // uniform
+    const float y[8] = {lo[c].x, lo[c].y, lo[c].z, lo[c].w, hi[c].x, hi[c].y, hi[c].z, hi[c].w};
+    const uint32_t ow[4] = {old[c].x, old[c].y, old[c].z, old[c].w};
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t h[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float v = y[2 * q + e];
+        h[e] = residual ? xpu::f32_to_bf16(xpu::bf16_to_f32((ow[q] >> (16 * e)) & 0xffffu) + xpu::round_bf16(v))
+                        : xpu::f32_to_bf16(v);
+      }
+      w[q] = h[0] | (h[1] << 16);
+    }
+    xc[c] = xpu::u32x4{w[0], w[1], w[2], w[3]};
+    *reinterpret_cast<xpu::u32x4 *>(C + static_cast<uint64_t>(row) * N + c * 512u + lane * 8u) = xc[c];
+    float f[8];
+    xpu::unpack8<xpu::kBf16>(xc[c], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(f[e], f[e], acc[e]);
+  }
+  const float ss = xpu::wave_butterfly(xpu::fold8(acc));
+  const float scale = 1.0f / __builtin_sqrtf(ss / static_cast<float>(N) + eps);
+#pragma unroll
+  for (uint32_t c = 0; c < kChunks; ++c) {
+    if (c >= nc) break;
+    const uint64_t off = static_cast<uint64_t>(row) * N + c * 512u + lane * 8u;
+    float xf[8], wf[8];
+    xpu::unpack8<xpu::kBf16>(xc[c], xf);
+    xpu::unpack8<xpu::kBf16>(*reinterpret_cast<const xpu::u32x4 *>(norm_w + c * 512u + lane * 8u), wf);
+    uint32_t code[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) code[e] = xpu::f32_to_bf16(wf[e] * xpu::round_bf16(xf[e] * scale));
+    *reinterpret_cast<xpu::u32x4 *>(Xn + off) = xpu::u32x4{code[0] | (code[1] << 16), code[2] | (code[3] << 16),
+                                                         code[4] | (code[5] << 16), code[6] | (code[7] << 16)};
+  }
+}
+
 // 256 x 256: BK = 64, two stages, barrier after 4 MFMAs of a slice's last
 // k-step, each slice's DMA spread over two k-steps; _odd for an odd number
 // of 64-deep slices

@@ -556,12 +556,17 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
     auto groups = [&](uint32_t r, uint32_t base) { return T > 8 ? std::max(1u, r / base) : 1u; };
     if ((rc = go(e.pf_embed_k, T, 1, 256, 0, {{8, &e.embed}, {8, &e.prompt}, {4, &p0}, {8, &e.pf_x}, {4, &H}, {4, &V}})))
       return rc;
+    // the GEMM form's split-K reductions of o_proj and down_proj can write
+    // the RMSNorm that follows them (xn_ready: pf_xn holds this layer's
+    // normalised input)
+    bool xn_ready = false;
     for (uint32_t l = 0; l < c.layers; ++l) {
       const Layer &L = e.layers[l];
       uint16_t *kc = e.kcache + l * cache_layer, *vc = e.vcache + l * cache_layer;
-      if ((rc = go(e.pf_norm_k, (T + 3) / 4, 1, 256, 0,
-                   {{8, &e.pf_x}, {8, &L.in_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}, {4, &T}})))
+      if (!xn_ready && (rc = go(e.pf_norm_k, (T + 3) / 4, 1, 256, 0,
+                                {{8, &e.pf_x}, {8, &L.in_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}, {4, &T}})))
         return rc;
+      xn_ready = false;
       if (e.gemm_prefill) {
         if ((rc = xpu::gemm_nt(rt, e.pf_xn, L.qkv, e.pf_qkv, T, qkv_rows, H, false))) return rc;
       } else if ((rc = go(e.pf_qkv_k, (qkv_rows + 4 * e.pf_qkv_r - 1) / (4 * e.pf_qkv_r), groups(e.pf_qkv_r, 2), 256,
@@ -597,14 +602,16 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
         }
         break;
       }
+      bool normed = false;
       if (e.gemm_prefill) {
-        if ((rc = xpu::gemm_nt(rt, e.pf_a, L.o, e.pf_x, T, H, qd, true))) return rc;
+        if ((rc = xpu::gemm_nt(rt, e.pf_a, L.o, e.pf_x, T, H, qd, true, L.post_norm, e.pf_xn, eps, &normed)))
+          return rc;
       } else if ((rc = go(e.pf_o_k, (H + 4 * e.pf_o_r - 1) / (4 * e.pf_o_r), groups(e.pf_o_r, 1), 256, pf_lds(qd),
                           {{8, &L.o}, {8, &e.pf_a}, {8, &e.pf_x}, {4, &H}, {4, &T}}))) {
         return rc;
       }
-      if ((rc = go(e.pf_norm_k, (T + 3) / 4, 1, 256, 0,
-                   {{8, &e.pf_x}, {8, &L.post_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}, {4, &T}})))
+      if (!normed && (rc = go(e.pf_norm_k, (T + 3) / 4, 1, 256, 0,
+                              {{8, &e.pf_x}, {8, &L.post_norm}, {8, &e.pf_xn}, {4, &H}, {4, &eps}, {4, &T}})))
         return rc;
       if (e.gemm_prefill) {
         const uint32_t two_i = 2 * I;
@@ -613,7 +620,10 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
         if ((rc = go(e.pf_silu_k, (I + 2047) / 2048, (T + 3) / 4, 256, 0,
                      {{8, &e.pf_gu}, {8, &e.pf_h}, {4, &I}, {4, &T}})))
           return rc;
-        if ((rc = xpu::gemm_nt(rt, e.pf_h, L.down, e.pf_x, T, H, I, true))) return rc;
+        // (the last layer stops after its attention, so layer l + 1 exists)
+        if ((rc = xpu::gemm_nt(rt, e.pf_h, L.down, e.pf_x, T, H, I, true, e.layers[l + 1].in_norm, e.pf_xn, eps,
+                               &xn_ready)))
+          return rc;
         continue;
       }
       if ((rc = go(e.pf_gu_k, (I + 2 * e.pf_gu_r - 1) / (2 * e.pf_gu_r), groups(e.pf_gu_r, 2), 256, pf_lds(H),

@@ -54,8 +54,13 @@ int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, 
 
 // C = A W^T for W given [N][K], bf16, aligned operands (gemm_api.cpp);
 // residual adds into C
+// norm_w / Xn (optional): where the product goes through the split-K
+// reduction, that kernel also writes Xn = RMSNorm(C) with gains norm_w and
+// eps and sets *normed (N = 512 or 1024); otherwise
+// *normed is false and the caller normalises.
 int gemm_nt(xpu_runtime *rt, const void *A, const void *W, void *C, uint32_t M, uint32_t N, uint32_t K,
-            bool residual);
+            bool residual, const void *norm_w = nullptr, void *Xn = nullptr, float eps = 0.0f,
+            bool *normed = nullptr);
 // The most workspace gemm_nt requests (its split-K partials), so a caller
 // can reserve it once (xpu_runtime::scratch grows by synchronizing).
 uint64_t gemm_nt_workspace_bound(const xpu_runtime *rt);
