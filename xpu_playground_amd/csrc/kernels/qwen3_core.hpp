@@ -302,22 +302,27 @@ constexpr uint32_t kVPitch = kHeadDim + 8;      // LDS row pitch of the V tile (
 // position reads kcur/vcur (the new token, contiguous rows not yet visible in
 // the cache).
 // p_t = bf16(exp(s_t - max) * (1 / sum_t exp)), out = bf16(sum_t p_t v_t).
-// sbuf: kAttnChunk floats of LDS; vtile: kAttnTile * kVPitch codes of LDS;
-// red: >= 4*128 floats of LDS. Position t is handled by thread t % 256 in
-// the score pass; V rows go through vtile so that the P.V pass reads LDS.
-template <bool HAS_CURRENT>
+// sbuf: kAttnChunk floats of LDS; vtile: VT * kVPitch codes of LDS (VT V
+// rows per tile, a multiple of 64 up to 256: the tiles only stage the rows,
+// the chains run over them in the same order whatever VT is); red: >= 4*128
+// floats of LDS. Position t is handled by thread t % 256 in the score pass;
+// V rows go through vtile so that the P.V pass reads LDS.
+template <bool HAS_CURRENT, uint32_t VT = kAttnTile>
 XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const uint16_t *vbase,
                                KvLayout lay, uint32_t n, const uint16_t *kcur,
                                const uint16_t *vcur, float scale, uint16_t *out, float *sbuf,
                                uint16_t *vtile, float *red, float local_max);
 
-template <bool HAS_CURRENT>
+// KPF: the score pass loads each thread's next K row while it scores the
+// current one (64 more VGPRs; off where two blocks share a CU instead).
+template <bool HAS_CURRENT, uint32_t VT = kAttnTile, bool KPF = true>
 XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const uint16_t *vbase,
                                KvLayout lay, uint32_t n, const uint16_t *kcur,
                                const uint16_t *vcur, float scale, uint16_t *out, float *sbuf,
                                uint16_t *vtile, float *red) {
+  static_assert(VT % 64 == 0 && VT <= kAttnTile, "V tiles of whole 64-row steps, at most one row per thread");
   const uint32_t tid = threadIdx.x;
-  const bool single_tile = n <= kAttnTile;
+  const bool single_tile = n <= VT;
   // V row t: chunk j at vrow_of(t) + j * vchunk_of(t) (the new token's row,
   // kept contiguous in vcur, when HAS_CURRENT and t is the last position)
   auto vrow_of = [&](uint32_t t) -> const uint16_t * {
@@ -339,34 +344,40 @@ XPU_DEVICE void attention_head(const uint16_t *qs, const uint16_t *kbase, const 
   // row of its next position is loaded before the current score is computed.
   static_assert(kAttnChunk % kAttnTile == 0, "chunks hold whole tiles");
   float local_max = -__builtin_inff();
-  u32x4 knext[16];
-  if (tid < n) load_head_row(kbase + static_cast<uint64_t>(tid) * lay.kstride, knext, lay.kchunk);
+  u32x4 knext[16];  // (unused without KPF)
+  if constexpr (KPF)
+    if (tid < n) load_head_row(kbase + static_cast<uint64_t>(tid) * lay.kstride, knext, lay.kchunk);
   for (uint32_t t = tid; t < n; t += kAttnTile) {
     u32x4 kcur_row[16];
+    if constexpr (KPF) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) kcur_row[j] = knext[j];
-    if (t + kAttnTile < n)
-      load_head_row(kbase + static_cast<uint64_t>(t + kAttnTile) * lay.kstride, knext, lay.kchunk);
+      for (int j = 0; j < 16; ++j) kcur_row[j] = knext[j];
+      if (t + kAttnTile < n)
+        load_head_row(kbase + static_cast<uint64_t>(t + kAttnTile) * lay.kstride, knext, lay.kchunk);
+    } else {
+      load_head_row(kbase + static_cast<uint64_t>(t) * lay.kstride, kcur_row, lay.kchunk);
+    }
     const float s = (HAS_CURRENT && t + 1 == n) ? attention_score(qs, kcur, scale)
                                                  : attention_score_regs(qs, kcur_row, scale);
     if (single_tile) stage_v_row(t, t);
     sbuf[t % kAttnChunk] = s;
     local_max = fmaxf(local_max, s);
   }
-  attention_tail<HAS_CURRENT>(qs, kbase, vbase, lay, n, kcur, vcur, scale, out, sbuf, vtile, red, local_max);
+  attention_tail<HAS_CURRENT, VT>(qs, kbase, vbase, lay, n, kcur, vcur, scale, out, sbuf, vtile, red, local_max);
 }
 
 // Passes 2 and 3 of attention_head, after the scores (sbuf, when one chunk
 // holds them), the V rows (vtile, when one tile holds them) and each
 // thread's running max are in place.
-template <bool HAS_CURRENT>
+template <bool HAS_CURRENT, uint32_t VT>
 XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const uint16_t *vbase,
                                KvLayout lay, uint32_t n, const uint16_t *kcur,
                                const uint16_t *vcur, float scale, uint16_t *out, float *sbuf,
                                uint16_t *vtile, float *red, float local_max) {
+  constexpr int kVJ = static_cast<int>(VT / 16);  // V rows per thread and tile
   const uint32_t tid = threadIdx.x;
   const uint32_t nchunks = (n + kAttnChunk - 1) / kAttnChunk;
-  const bool single_tile = n <= kAttnTile;
+  const bool single_tile = n <= VT;
   auto score_of = [&](uint32_t t) -> float {
     if (HAS_CURRENT && t + 1 == n) return attention_score(qs, kcur, scale);
     return attention_score(qs, kbase + static_cast<uint64_t>(t) * lay.kstride, scale, lay.kchunk);
@@ -380,16 +391,16 @@ XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const 
   // reads 16 consecutive rows of each of 4 chunks, 256 contiguous bytes
   // each)
   const uint32_t v_chunk = tid >> 4, v_row0 = tid & 15u;
-  auto load_v_tile = [&](uint32_t t0, uint32_t tlen, u32x4 (&vv)[16]) {
+  auto load_v_tile = [&](uint32_t t0, uint32_t tlen, u32x4 (&vv)[kVJ]) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < kVJ; ++j) {
       const uint32_t r = j * 16u + v_row0;
       if (r < tlen) vv[j] = *reinterpret_cast<const u32x4 *>(vrow_of(t0 + r) + v_chunk * vchunk_of(t0 + r));
     }
   };
-  auto store_v_tile = [&](uint32_t tlen, const u32x4 (&vv)[16]) {
+  auto store_v_tile = [&](uint32_t tlen, const u32x4 (&vv)[kVJ]) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < kVJ; ++j) {
       const uint32_t r = j * 16u + v_row0;
       if (r < tlen) *reinterpret_cast<u32x4 *>(vtile + r * kVPitch + v_chunk * 8u) = vv[j];
     }
@@ -436,17 +447,17 @@ XPU_DEVICE void attention_tail(const uint16_t *qs, const uint16_t *kbase, const 
     }
     __syncthreads();
     float part[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
-    // V tiles of 256 rows go through vtile; the next tile's row of this
-    // thread is loaded into registers while the current tile is used
-    u32x4 vnext[16];
-    if (!single_tile) load_v_tile(base, min(kAttnTile, len), vnext);
-    for (uint32_t i0 = 0; i0 < len; i0 += kAttnTile) {
-      const uint32_t tile_len = min(kAttnTile, len - i0);
+    // V tiles of VT rows go through vtile; the next tile's rows of this
+    // thread are loaded into registers while the current tile is used
+    u32x4 vnext[kVJ];
+    if (!single_tile) load_v_tile(base, min(VT, len), vnext);
+    for (uint32_t i0 = 0; i0 < len; i0 += VT) {
+      const uint32_t tile_len = min(VT, len - i0);
       if (!single_tile) {
         store_v_tile(tile_len, vnext);
         __syncthreads();
-        const uint32_t next_len = i0 + kAttnTile < len ? min(kAttnTile, len - i0 - kAttnTile) : 0u;
-        if (next_len) load_v_tile(base + i0 + kAttnTile, next_len, vnext);
+        const uint32_t next_len = i0 + VT < len ? min(VT, len - i0 - VT) : 0u;
+        if (next_len) load_v_tile(base + i0 + VT, next_len, vnext);
       }
       // 64 rows per step: the operands of 4 groups of 16 rows are read
       // (index clamped into the tile) before their FMAs, each chain in

@@ -1463,21 +1463,24 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_rope_cache(
 
 // Attention of every token of the chunk: block (head, t) over cache
 // positions 0..p0 + t (all written by xpu_q3_pf_rope_cache and earlier
-// steps), the general attention_head of the decode path.
-extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_attention(
+// steps), the general attention_head of the decode path with V tiles of
+// kPfVTile rows (same operations in the same order): 53 KiB of LDS, so two
+// of these latency-bound blocks share a compute unit.
+constexpr uint32_t kPfVTile = 128;
+extern "C" __global__ __launch_bounds__(256, 2) void xpu_q3_pf_attention(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache,
     uint16_t *__restrict__ A, uint32_t p0, uint32_t heads, uint32_t kv_heads, uint32_t max_seq, float scale) {
   __shared__ float sbuf[xpu::kAttnChunk];
   __shared__ float red[4 * xpu::kHeadDim];
   __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
-  __shared__ __align__(16) uint16_t vtile[xpu::kAttnTile * xpu::kVPitch];
+  __shared__ __align__(16) uint16_t vtile[kPfVTile * xpu::kVPitch];
   const uint32_t head = blockIdx.x, t = blockIdx.y;
   const uint32_t kv = head / (heads / kv_heads);
   const uint64_t qoff = (static_cast<uint64_t>(t) * heads + head) * xpu::kHeadDim;
   if (threadIdx.x < xpu::kHeadDim) qs[threadIdx.x] = Q[qoff + threadIdx.x];
   __syncthreads();
   const uint64_t head_base = static_cast<uint64_t>(kv) * max_seq * xpu::kHeadDim;
-  xpu::attention_head<false>(qs, kcache + head_base, vcache + head_base,
+  xpu::attention_head<false, kPfVTile, false>(qs, kcache + head_base, vcache + head_base,
                              xpu::KvLayout{8u, static_cast<uint64_t>(max_seq) * 8u, 8u, static_cast<uint64_t>(max_seq) * 8u},
                              p0 + t + 1, nullptr,
                              nullptr, scale, A + qoff, sbuf, vtile, red);
