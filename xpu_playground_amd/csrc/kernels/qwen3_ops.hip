@@ -1277,7 +1277,10 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
   constexpr uint32_t kTile = TT * K;                 // codes per token tile
   constexpr int kLoads = kTile / (256 * 8);          // 16-byte staging loads per thread
   static_assert(kTile % (256 * 8) == 0, "tile must split evenly over the block");
-  extern __shared__ __align__(16) uint16_t xt[];     // two tiles
+  // two tiles for K <= 2048; one past that (48 KiB at K = 3072, so up to
+  // three blocks share a compute unit), its next tile stored after a barrier
+  constexpr bool kDouble = NC <= 4;
+  extern __shared__ __align__(16) uint16_t xt[];
   const uint32_t wave = threadIdx.x >> 6, lane = xpu::lane_id();
   const uint32_t o0 = (blockIdx.x * 4u + wave) * kOuts;  // first output of this wavefront
   const uint32_t rows_total = kPaired ? 2u * M : M;
@@ -1326,7 +1329,7 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
   for (uint32_t t0 = t_beg; t0 < t_end; t0 += TT) {
     const bool more = t0 + TT < t_end;
     if (more) load_tile(t0 + TT);
-    const uint16_t *tile = xt + cur * kTile;
+    const uint16_t *tile = xt + (kDouble ? cur * kTile : 0u);
     static_assert(TT == 8, "token_butterfly8 reduces 8 tokens");
     // token by token: each slot's FMA chain over the chunks, then its fold,
     // so only one token's accumulators are live
@@ -1382,7 +1385,8 @@ XPU_DEVICE void pf_gemv(const uint16_t *__restrict__ W, const uint16_t *__restri
       }
     }
     if (more) {
-      store_tile(xt + (cur ^ 1u) * kTile);
+      if constexpr (!kDouble) __syncthreads();  // every wavefront is done with the tile
+      store_tile(xt + (kDouble ? (cur ^ 1u) * kTile : 0u));
       __syncthreads();
       cur ^= 1u;
     }

@@ -402,7 +402,12 @@ int setup_prefill(xpu_qwen3 &e) {
   e.pf_attn_short_k = e.rt->find_exact("xpu_q3_pf_attention_short");
   const bool common = e.pf_embed_k && e.pf_norm_k && e.pf_rope_k && c.hidden % 8 == 0;
   e.pf_ok = common && e.pf_qkv_k && e.pf_o_k && e.pf_gu_k && e.pf_down_k && e.pf_attn_k &&
-            32u * std::max({c.hidden, qd, c.intermediate}) <= e.rt->max_shared;
+            [&] {
+              // the batched GEMVs' LDS: two tiles of 8 token rows for K <= 2048, one past that
+              for (uint32_t K : {c.hidden, qd, c.intermediate})
+                if ((K <= 2048u ? 2u : 1u) * 16u * K > e.rt->max_shared) return false;
+              return true;
+            }();
   const uint64_t qkv_rows = uint64_t{c.heads + 2 * c.kv_heads} * c.head_dim;
   // the MFMA form: every projection's K and N multiples of 8 (the NT GEMM
   // kernels read the weight rows in place) and 1, 2 or 4 query heads per kv
@@ -537,7 +542,9 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
   uint32_t qkv_rows = (heads + 2 * kv) * c.head_dim, qd = heads * c.head_dim;
   float eps = c.rms_eps;
   // two tiles of 8 token rows of K codes (xpu_q3_pf_gemv_*)
-  auto pf_lds = [](uint32_t K) { return 2u * 8u * K * 2u; };
+  // LDS of the batched GEMVs: two tiles of 8 token rows for K <= 2048, one
+  // past that
+  auto pf_lds = [](uint32_t K) { return (K <= 2048u ? 2u : 1u) * 8u * K * 2u; };
   float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
   const uint64_t cache_layer = uint64_t{kv} * max_seq * c.head_dim;
   xpu_runtime *rt = e.rt;
@@ -629,7 +636,10 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
       if ((rc = go(e.pf_gu_k, (I + 2 * e.pf_gu_r - 1) / (2 * e.pf_gu_r), groups(e.pf_gu_r, 2), 256, pf_lds(H),
                    {{8, &L.gu}, {8, &e.pf_xn}, {8, &e.pf_h}, {4, &I}, {4, &T}})))
         return rc;
-      if ((rc = go(e.pf_down_k, (H + 4 * e.pf_down_r - 1) / (4 * e.pf_down_r), groups(e.pf_down_r, 1), 256,
+      // (one LDS tile past K = 2048: three times the token groups, up to
+      // three blocks per compute unit)
+      if ((rc = go(e.pf_down_k, (H + 4 * e.pf_down_r - 1) / (4 * e.pf_down_r),
+                   groups(e.pf_down_r, 1) * (I > 2048 && T > 8 ? 3u : 1u), 256,
                    pf_lds(I),
                    {{8, &L.down}, {8, &e.pf_h}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
         return rc;
