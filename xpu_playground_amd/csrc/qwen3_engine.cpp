@@ -576,7 +576,7 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
       xn_ready = false;
       if (e.gemm_prefill) {
         if ((rc = xpu::gemm_nt(rt, e.pf_xn, L.qkv, e.pf_qkv, T, qkv_rows, H, false))) return rc;
-      } else if ((rc = go(e.pf_qkv_k, (qkv_rows + 4 * e.pf_qkv_r - 1) / (4 * e.pf_qkv_r), groups(e.pf_qkv_r, 2), 256,
+      } else if ((rc = go(e.pf_qkv_k, (qkv_rows + 4 * e.pf_qkv_r - 1) / (4 * e.pf_qkv_r), groups(e.pf_qkv_r, 2) * (T > 8 ? 3u : 2u) / 2u, 256,
                           pf_lds(H),
                           {{8, &L.qkv}, {8, &e.pf_xn}, {8, &e.pf_qkv}, {4, &qkv_rows}, {4, &T}}))) {
         return rc;
@@ -613,7 +613,7 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
       if (e.gemm_prefill) {
         if ((rc = xpu::gemm_nt(rt, e.pf_a, L.o, e.pf_x, T, H, qd, true, L.post_norm, e.pf_xn, eps, &normed)))
           return rc;
-      } else if ((rc = go(e.pf_o_k, (H + 4 * e.pf_o_r - 1) / (4 * e.pf_o_r), groups(e.pf_o_r, 1), 256, pf_lds(qd),
+      } else if ((rc = go(e.pf_o_k, (H + 4 * e.pf_o_r - 1) / (4 * e.pf_o_r), groups(e.pf_o_r, 1) * (T > 8 ? 2u : 1u), 256, pf_lds(qd),
                           {{8, &L.o}, {8, &e.pf_a}, {8, &e.pf_x}, {4, &H}, {4, &T}}))) {
         return rc;
       }
