@@ -636,10 +636,10 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
       if ((rc = go(e.pf_gu_k, (I + 2 * e.pf_gu_r - 1) / (2 * e.pf_gu_r), groups(e.pf_gu_r, 2), 256, pf_lds(H),
                    {{8, &L.gu}, {8, &e.pf_xn}, {8, &e.pf_h}, {4, &I}, {4, &T}})))
         return rc;
-      // (one LDS tile past K = 2048: three times the token groups, up to
-      // three blocks per compute unit)
+      // (one LDS tile past K = 2048: twice the token groups, two blocks per
+      // compute unit as its registers allow)
       if ((rc = go(e.pf_down_k, (H + 4 * e.pf_down_r - 1) / (4 * e.pf_down_r),
-                   groups(e.pf_down_r, 1) * (I > 2048 && T > 8 ? 3u : 1u), 256,
+                   groups(e.pf_down_r, 1) * (I > 2048 && T > 8 ? 2u : 1u), 256,
                    pf_lds(I),
                    {{8, &L.down}, {8, &e.pf_h}, {8, &e.pf_x}, {4, &H}, {4, &T}})))
         return rc;
