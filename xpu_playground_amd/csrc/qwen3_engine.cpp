@@ -559,7 +559,9 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
     // batched GEMV grids: 4 wavefronts of R rows (R / 2 output pairs for
     // [gate; up]) per block; past one token tile, the tokens split into
     // R / 2 groups (R for the residual forms), which keeps the block count
-    // of 2-row (1-row) wavefronts over all tokens
+    // of 2-row (1-row) wavefronts over all tokens, times the factor at each
+    // launch that fills the blocks per compute unit its registers and LDS
+    // allow (measured: QKV 3/2, o_proj 2, down_proj 2)
     auto groups = [&](uint32_t r, uint32_t base) { return T > 8 ? std::max(1u, r / base) : 1u; };
     if ((rc = go(e.pf_embed_k, T, 1, 256, 0, {{8, &e.embed}, {8, &e.prompt}, {4, &p0}, {8, &e.pf_x}, {4, &H}, {4, &V}})))
       return rc;
