@@ -561,7 +561,7 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
     // R / 2 groups (R for the residual forms), which keeps the block count
     // of 2-row (1-row) wavefronts over all tokens, times the factor at each
     // launch that fills the blocks per compute unit its registers and LDS
-    // allow (measured: QKV 3/2, o_proj 2, down_proj 2)
+    // allow (measured: QKV and [gate; up] 3/2, o_proj 2, down_proj 2)
     auto groups = [&](uint32_t r, uint32_t base) { return T > 8 ? std::max(1u, r / base) : 1u; };
     if ((rc = go(e.pf_embed_k, T, 1, 256, 0, {{8, &e.embed}, {8, &e.prompt}, {4, &p0}, {8, &e.pf_x}, {4, &H}, {4, &V}})))
       return rc;
@@ -635,7 +635,8 @@ int run_prefill(xpu_qwen3 &e, uint32_t P, bool head) {
           return rc;
         continue;
       }
-      if ((rc = go(e.pf_gu_k, (I + 2 * e.pf_gu_r - 1) / (2 * e.pf_gu_r), groups(e.pf_gu_r, 2), 256, pf_lds(H),
+      if ((rc = go(e.pf_gu_k, (I + 2 * e.pf_gu_r - 1) / (2 * e.pf_gu_r), groups(e.pf_gu_r, 2) * (T > 8 ? 3u : 2u) / 2u,
+                   256, pf_lds(H),
                    {{8, &L.gu}, {8, &e.pf_xn}, {8, &e.pf_h}, {4, &I}, {4, &T}})))
         return rc;
       // (one LDS tile past K = 2048: twice the token groups, two blocks per
