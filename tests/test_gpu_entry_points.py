@@ -101,7 +101,7 @@ def test_peak_launcher_gemv_and_gemm_modes():
 
 
 def test_run_gemv_in_process(capfd):
-    # the exported C symbol itself (SURVEY boundary: extern "C" run_gemv)
+    # the exported C symbol itself (the reference boundary: extern "C" run_gemv, gemv.cpp:157)
     lib = xpu.library()
     argv = [b"gemv", b"--m", b"2048", b"--k", b"3072", b"--type", b"fp16", b"--iterations", b"3",
             b"--warmups", b"1"]
