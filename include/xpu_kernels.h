@@ -28,14 +28,14 @@ extern "C" {
 
 /* y[M] = A[M x K] . x[K]; lda >= K is the row pitch in elements (K for a
  * packed matrix). Replaces gemv::Kernel<T> (gemv_kernel.hpp:21-63) launched
- * by gemv.cpp:170-172 / peak_l0.cpp:849-856. Each y[r] is the canonical-order
+ * by gemv.cpp:105-108 / peak_l0.cpp:849-856. Each y[r] is the canonical-order
  * FP32 sum rounded to the storage type. */
 int xpu_gemv(xpu_runtime *rt, int dtype, const void *A, const void *x, void *y,
              uint32_t M, uint32_t K, uint64_t lda);
 
 /* C[M x N] = A[M x K] . B[K x N], row-major, FP32 accumulation on MFMA.
  * Replaces gemm::Kernel<T, Large> (gemm_kernel.hpp:25-143) launched by
- * gemm.cpp:243-246 / peak_l0.cpp:929-934, and the choice between its large
+ * gemm.cpp:98-101 / peak_l0.cpp:929-934, and the choice between its large
  * and small tile (gemm.cpp:145): the block tile (256x256, 128x256 or
  * 128x128) is the one with the least estimated time at this shape on this
  * GPU's compute units (xpu_gemm_tile). */
@@ -109,13 +109,6 @@ int xpu_peak_read(xpu_runtime *rt, const void *input, uint64_t bytes, void *sink
 int run_peak_compute(int argc, char **argv);
 int run_peak_mem(int argc, char **argv);
 
-/* run_peak_sync (no reference counterpart): the cost of one dependent step
- *   between launches of one block per compute unit: a kernel boundary on a
- *   stream and in a graph (--launches N empty kernels, default 2000), and an
- *   all-to-all handoff inside one cooperative launch in four publication
- *   forms (--stages N, default 500). 0 on success, 1 on error or when the
- *   in-kernel data check fails. */
-int run_peak_sync(int argc, char **argv);
 
 #ifdef __cplusplus
 }

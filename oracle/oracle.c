@@ -335,7 +335,8 @@ void orc_gemm_f64(const uint16_t *a, const uint16_t *b, double *c, uint32_t m,
   free(bd);
 }
 
-/* gemm.cpp:254-262 check order: FP32, ascending k */
+/* gemv.cpp:126-130 check order (the FP32 host sum, ascending k), applied to
+ * each GEMM element */
 void orc_gemm_f32_rows(const uint16_t *a, const uint16_t *b, float *c, uint32_t m,
                        uint32_t n, uint32_t k, int dtype, const uint32_t *rows,
                        uint32_t nrows) {

@@ -172,6 +172,11 @@ def test_header_length_and_truncation(tmp_path):
     ('{"a": tru}', "a value"),
     ('{} {}', "end of document"),
     ('{"a": "tab\there"}', "raw control character"),
+    # qwen3/model.cpp:204-205: a repeated member name fails, also after
+    # unescaping and inside nested objects
+    ('{"a": 1, "a": 2}', 'duplicate object key "a"'),
+    ('{"a": 1, "\\u0061": 2}', 'duplicate object key "a"'),
+    ('{"x": [{"b": 1, "c": 2, "b": 3}]}', 'duplicate object key "b"'),
 ])
 def test_json_reader_rejects_malformed_documents(tmp_path, text, match):
     (tmp_path / "config.json").write_text(text)
@@ -189,8 +194,35 @@ def test_json_reader_escapes_nesting_and_exact_integers(tmp_path):
     (tmp_path / "config.json").write_text(text.replace('"hidden_act"', '"model_type": "qwen3", "hidden_act"'))
     cfg = qwen3.read_config(str(tmp_path))
     assert cfg.rope_theta == 5e5 and cfg.tied == 0 and cfg.vocab == 151936
+    # the same names in different objects are not duplicates; a second
+    # hidden_size in the top-level object is
+    (tmp_path / "config.json").write_text(text.replace('"hidden_act"', '"model_type": "qwen3", "hidden_act"')
+                                          .replace('"list": [', '"list": [{"hidden_size": 1}, '))
+    assert qwen3.read_config(str(tmp_path)).hidden == 1024
+    (tmp_path / "config.json").write_text(text.replace('"hidden_act"', '"model_type": "qwen3", "hidden_act"')
+                                          .replace('"list": [', '"hidden_size": 2048, "list": ['))
+    with pytest.raises(XpuError, match='duplicate object key "hidden_size"'):
+        qwen3.read_config(str(tmp_path))
     for bad in ("1024.0", "1e3", "-1", "18446744073709551616", "4294967296"):
         (tmp_path / "config.json").write_text(
             json.dumps({**valid, "model_type": "qwen3"}).replace('"hidden_size": 1024', f'"hidden_size": {bad}'))
         with pytest.raises(XpuError, match="hidden_size"):
             qwen3.read_config(str(tmp_path))
+
+
+def test_safetensors_header_with_a_repeated_tensor_name(tmp_path):
+    # a header naming one tensor twice is malformed JSON for the reader
+    # (qwen3/model.cpp:204-205), not a second definition that wins
+    write_checkpoint(str(tmp_path), tiny(), seed=1, gain_std=0.0)
+    path = tmp_path / "model.safetensors"
+    header, start, size = read_header(path)
+    name = "model.norm.weight"
+    text = json.dumps(header)
+    entry = json.dumps({name: header[name]})[1:-1]
+    text = text[:-1] + ", " + entry + "}"
+    data = path.read_bytes()[start:]
+    with open(path, "wb") as fh:
+        fh.write(len(text).to_bytes(8, "little"))
+        fh.write(text.encode())
+        fh.write(data)
+    rejects(tmp_path, f'duplicate object key "{name}"')

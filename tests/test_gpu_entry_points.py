@@ -47,14 +47,14 @@ def run(program, args, timeout=300):
 
 
 GEMV_CASES = [
-    # BASELINE configs[0] and [1]
-    (["--m", "4096", "--k", "4096", "--type", "bf16"], "BF16", 4096, 4096),
-    (["--size", "16384", "--type", "fp16"], "FP16", 16384, 16384),
-    # the reference's own hash initialisation (gemv.cpp:91-103) and its
-    # default type
+    # BASELINE configs[0] and [1]: seeded U[-1,1] inputs
+    (["--m", "4096", "--k", "4096", "--type", "bf16", "--init", "uniform"], "BF16", 4096, 4096),
+    (["--size", "16384", "--type", "fp16", "--init", "uniform"], "FP16", 16384, 16384),
+    # the reference's own hash initialisation (gemv.cpp:91-103, the default)
     (["--size", "4096", "--init", "reference"], "BF16", 4096, 4096),
-    # ragged K (16-bit-load kernel) and a short matrix
+    # ragged K (16-bit-load kernel) and a short matrix, hash and uniform
     (["--m", "1000", "--k", "1001", "--type", "fp16"], "FP16", 1000, 1001),
+    (["--m", "1000", "--k", "1001", "--type", "fp16", "--init", "uniform"], "FP16", 1000, 1001),
     (["--m", "7", "--k", "64"], "BF16", 7, 64),
 ]
 
@@ -73,11 +73,13 @@ def test_run_gemv(args, type_, m, k):
 
 
 GEMM_CASES = [
-    (["--size", "4096", "--type", "bf16"], "BF16", (4096, 4096, 4096)),        # configs[2]
-    (["--m", "3000", "--n", "4097", "--k", "2050", "--type", "fp16"], "FP16", (3000, 4097, 2050)),  # configs[3]
+    (["--size", "4096", "--type", "bf16", "--init", "uniform"], "BF16", (4096, 4096, 4096)),  # configs[2]
+    (["--m", "3000", "--n", "4097", "--k", "2050", "--type", "fp16", "--init", "uniform"], "FP16",
+     (3000, 4097, 2050)),  # configs[3]
     (["--size", "4096", "--init", "constant"], "BF16", (4096, 4096, 4096)),    # gemm.cpp:81-85 KAT
-    (["--m", "300", "--n", "200", "--k", "100", "--init", "constant", "--type", "fp16"], "FP16", (300, 200, 100)),
+    (["--m", "300", "--n", "200", "--k", "100", "--type", "fp16"], "FP16", (300, 200, 100)),
     (["--m", "33", "--n", "65", "--k", "17"], "BF16", (33, 65, 17)),
+    (["--m", "33", "--n", "65", "--k", "17", "--init", "uniform"], "BF16", (33, 65, 17)),
 ]
 
 
@@ -90,6 +92,27 @@ def test_run_gemm(args, type_, shape):
     assert float(best.group(1)) >= float(median.group(1)) >= 0
     if shape == (4096, 4096, 4096):
         assert float(median.group(1)) > 200.0
+
+
+def test_bare_programs_use_the_reference_inputs():
+    # A caller that passes none of this build's extra flags gets the
+    # reference's inputs and checks: gemv the hash initialisation of its
+    # padded 16384^2 bf16 matrix (gemv.cpp:21,79-103), gemm the constant
+    # A = 0.5, B = 0.25 at 4096^3 bf16 with the known answer 0.125 K = 512
+    # (gemm.cpp:19,81-85,109-117), each with the reference's iteration counts.
+    out = run("gemv", [])
+    assert check_output(out, GEMV_LINES)[1].groups() == ("BF16", "16384", "16384")
+    assert re.search(r"^Input: reference hash \(gemv.cpp:91-103\), row stride 16384$", out, re.M), out
+    out = run("gemm", [])
+    assert check_output(out, GEMM_LINES)[1].groups() == ("BF16", "4096", "4096", "4096")
+    assert re.search(r"^Input: constant A = 0.5, B = 0.25 \(gemm.cpp:81-85\), expected 0.125 \* K = 512$", out,
+                     re.M), out
+    # the known-answer check, not the FP64 comparison of uniform inputs
+    assert "Accuracy" not in out
+    # a K that the reference pads: the hash runs over its 32-column row
+    # stride, so every element carries the reference's value
+    out = run("gemv", ["--m", "40", "--k", "1001", "--iterations", "2", "--warmups", "1"])
+    assert re.search(r"^Input: reference hash .*row stride 1024$", out, re.M), out
 
 
 def test_peak_launcher_gemv_and_gemm_modes():

@@ -38,13 +38,12 @@ def test_peak_read_rate():
     assert 1000.0 < gbs < 9000.0
 
 
-def test_peak_sync_handoff_costs():
-    # a kernel boundary against in-kernel all-to-all handoffs (peak sync):
-    # every variant completes its stages with the data it waited for
-    import re
-
-    exe = os.path.join(xpu.BUILD_DIR, "peak")
-    out = subprocess.run([exe, "sync", "--launches", "200", "--stages", "100"], capture_output=True, text=True,
+def test_handoff_probe_costs():
+    # The test-only probe (tests/handoff_probe): a kernel boundary against
+    # in-kernel all-to-all handoffs. Every variant completes its stages (the
+    # waits are bounded) with the data it waited for.
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "handoff_probe", "build", "handoff_probe")
+    out = subprocess.run([exe, "--launches", "200", "--stages", "100"], capture_output=True, text=True,
                          timeout=120)
     assert out.returncode == 0, out.stderr
     assert "Data check: PASS" in out.stdout

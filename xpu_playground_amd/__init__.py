@@ -142,7 +142,6 @@ def _declare(lib):
         "xpu_peak_mfma": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]),
         "xpu_peak_read": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_uint32]),
         "run_peak_compute": (c_int, [c_int, POINTER(c_char_p)]),
-        "run_peak_sync": (c_int, [c_int, POINTER(c_char_p)]),
         "run_peak_mem": (c_int, [c_int, POINTER(c_char_p)]),
         "run_qwen3": (c_int, [c_int, POINTER(c_char_p)]),
     }

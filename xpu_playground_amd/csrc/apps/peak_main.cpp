@@ -1,5 +1,5 @@
 // Benchmark launcher with the modes of the reference's peak_sycl
-// (peak_sycl.cpp:8-20,47-50): mem, compute, gemv, gemm, plus sync. The reference
+// (peak_sycl.cpp:8-20,47-50): mem, compute, gemv, gemm. The reference
 // execv()s a sibling program per mode; here each mode is an entry point of
 // the same library, called in-process with the mode removed from argv.
 #include "xpu_kernels.h"
@@ -14,8 +14,7 @@ void usage(const char *program) {
             << "  " << program << " mem [--size-mib N] [--iterations N]\n"
             << "  " << program << " compute [--waves-per-simd N] [--rounds N] [--iterations N]\n"
             << "  " << program << " gemv [--size N | --m M --k K] [--type bf16|fp16]\n"
-            << "  " << program << " gemm [--size N | --m M --n N --k K] [--type bf16|fp16]\n"
-            << "  " << program << " sync [--launches N] [--stages N]\n";
+            << "  " << program << " gemm [--size N | --m M --n N --k K] [--type bf16|fp16]\n";
 }
 
 }  // namespace
@@ -36,7 +35,6 @@ int main(int argc, char **argv) {
   if (mode == "compute") return run_peak_compute(argc - 1, argv + 1);
   if (mode == "gemv") return run_gemv(argc - 1, argv + 1);
   if (mode == "gemm") return run_gemm(argc - 1, argv + 1);
-  if (mode == "sync") return run_peak_sync(argc - 1, argv + 1);
   std::cerr << "Error: unknown benchmark mode: " << mode << '\n';
   return 1;
 }

@@ -103,7 +103,10 @@ struct GemvOptions {
   uint32_t m = 16384, k = 16384;          // gemv.cpp:21
   unsigned iterations = 50, warmups = 5;  // gemv.cpp:22
   int dtype = XPU_DTYPE_BF16;
-  bool reference_init = false;            // --init reference: gemv.cpp:91-103 hash
+  // gemv.cpp:91-103: the reference's hash initialisation is its only input,
+  // so it is the default here too; --init uniform selects the seeded
+  // U[-1,1] data of the benchmark configurations
+  bool reference_init = true;
   uint64_t seed = 1;
   uint32_t rotate = 1;                    // distinct copies of A cycled by the timed loop
   uint32_t check_rows = 64;               // gemv.cpp:119 checks min(M, 64) rows
@@ -112,7 +115,7 @@ struct GemvOptions {
 [[noreturn]] void gemv_usage(const char *program, int status) {
   std::ostream &out = status ? std::cerr : std::cout;
   out << "Usage: " << program << " [--size N | --m M --k K] [--type bf16|fp16]\n"
-      << "       [--iterations N] [--warmups N] [--init uniform|reference] [--seed N]\n"
+      << "       [--iterations N] [--warmups N] [--init reference|uniform] [--seed N]\n"
       << "       [--rotate N] [--check-rows N]\n";
   std::exit(status);
 }
@@ -163,7 +166,15 @@ extern "C" int run_gemv(int argc, char **argv) {
     xpu_runtime *rt = guard.rt;
     std::cout << "Device: " << rt->name << " (" << rt->arch << ", " << rt->compute_units
               << " CUs)\n";
-    const uint64_t matrix_bytes = static_cast<uint64_t>(o.m) * o.k * 2;
+    // The reference hashes the linear index of its matrix padded to 32
+    // columns (gemv.cpp:79-80,91-98); with the same row stride here every
+    // element gets the reference's value. The product still covers K columns
+    // only: the reference's padding columns keep hash data and enter its sum
+    // when K % 32 != 0, which is the reference's bug, not its contract.
+    const uint64_t ld64 = o.reference_init ? (static_cast<uint64_t>(o.k) + 31u) / 32u * 32u : o.k;
+    if (ld64 > UINT32_MAX) throw std::overflow_error("matrix dimension is too large");
+    const uint32_t ld = static_cast<uint32_t>(ld64);
+    const uint64_t matrix_bytes = static_cast<uint64_t>(o.m) * ld * 2;
     check(xpu_rt_require_device_and_memory(rt, matrix_bytes * o.rotate + (o.k + o.m) * 4ull));
     std::vector<void *> matrices(o.rotate);
     void *x = nullptr, *y = nullptr;
@@ -171,7 +182,7 @@ extern "C" int run_gemv(int argc, char **argv) {
     check(xpu_rt_alloc(rt, o.k * 2ull, 256, &x));
     check(xpu_rt_alloc(rt, o.m * 2ull, 256, &y));
     for (uint32_t c = 0; c < o.rotate; ++c) {
-      if (o.reference_init) check(xpu_fill_reference_gemv(rt, o.dtype, matrices[c], x, o.m, o.k, o.k));
+      if (o.reference_init) check(xpu_fill_reference_gemv(rt, o.dtype, matrices[c], x, o.m, o.k, ld));
       else check(xpu_fill_uniform(rt, o.dtype, matrices[c], static_cast<uint64_t>(o.m) * o.k, o.seed + c));
     }
     if (!o.reference_init)
@@ -183,7 +194,7 @@ extern "C" int run_gemv(int argc, char **argv) {
     check(xpu_rt_event_create(rt, &start));
     check(xpu_rt_event_create(rt, &stop));
     for (unsigned i = 0; i < o.warmups; ++i)
-      check(xpu_gemv(rt, o.dtype, matrices[i % o.rotate], x, y, o.m, o.k, o.k));
+      check(xpu_gemv(rt, o.dtype, matrices[i % o.rotate], x, y, o.m, o.k, ld));
     check(xpu_rt_synchronize(rt));
     // gemv.cpp:109-118: one timed launch per iteration; the reference counts
     // 2*M*K FLOP and 2*M*K matrix bytes (:109-110)
@@ -193,7 +204,7 @@ extern "C" int run_gemv(int argc, char **argv) {
     std::vector<double> rates, bandwidths, alg_bandwidths, times;
     for (unsigned i = 0; i < o.iterations; ++i) {
       check(xpu_rt_event_record(rt, start));
-      check(xpu_gemv(rt, o.dtype, matrices[(o.warmups + i) % o.rotate], x, y, o.m, o.k, o.k));
+      check(xpu_gemv(rt, o.dtype, matrices[(o.warmups + i) % o.rotate], x, y, o.m, o.k, ld));
       check(xpu_rt_event_record(rt, stop));
       float ms = 0;
       check(xpu_rt_event_elapsed_ms(start, stop, &ms));
@@ -214,7 +225,7 @@ extern "C" int run_gemv(int argc, char **argv) {
     const uint32_t rows = std::min(o.m, o.check_rows);
     double err2 = 0, ref2 = 0, max_ulps = 0;
     if (rows) {
-      std::vector<uint16_t> hy(rows), ha(static_cast<size_t>(rows) * o.k), hx(o.k);
+      std::vector<uint16_t> hy(rows), ha(static_cast<size_t>(rows) * ld), hx(o.k);
       check(xpu_rt_copy_from_device(rt, hy.data(), y, rows * 2ull));
       check(xpu_rt_copy_from_device(rt, ha.data(), checked, ha.size() * 2));
       check(xpu_rt_copy_from_device(rt, hx.data(), x, o.k * 2ull));
@@ -224,7 +235,7 @@ extern "C" int run_gemv(int argc, char **argv) {
         float expected = 0.0f;
         double exact = 0.0;
         for (uint32_t c = 0; c < o.k; ++c) {
-          const float a = xpu::decode16(ha[static_cast<size_t>(r) * o.k + c], o.dtype);
+          const float a = xpu::decode16(ha[static_cast<size_t>(r) * ld + c], o.dtype);
           expected += a * xf[c];
           exact += static_cast<double>(a) * xf[c];
         }
@@ -242,8 +253,12 @@ extern "C" int run_gemv(int argc, char **argv) {
     const double rel_l2 = ref2 > 0 ? std::sqrt(err2 / ref2) : std::sqrt(err2);
     const double med_alg = xpu::median_of(alg_bandwidths);
     std::cout << "Type: " << (o.dtype ? "FP16" : "BF16") << ", shape: " << o.m << 'x' << o.k
-              << '\n'
-              << std::fixed << std::setprecision(2) << "Median: " << xpu::median_of(rates)
+              << '\n';
+    if (o.reference_init)
+      std::cout << "Input: reference hash (gemv.cpp:91-103), row stride " << ld << '\n';
+    else
+      std::cout << "Input: uniform [-1,1), seed " << o.seed << '\n';
+    std::cout << std::fixed << std::setprecision(2) << "Median: " << xpu::median_of(rates)
               << " GFLOP/s, " << xpu::median_of(bandwidths) << " GB/s\n"
               << "Best:   " << xpu::max_of(rates) << " GFLOP/s, " << xpu::max_of(bandwidths)
               << " GB/s\n"

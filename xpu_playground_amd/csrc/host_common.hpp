@@ -113,7 +113,7 @@ template <typename T> T parse_unsigned(std::string_view text, std::string_view o
   return value;
 }
 
-// median as in gemv.cpp:200-204 (mean of the two middle values when even)
+// median as in gemv.cpp:135-139 (mean of the two middle values when even)
 inline double median_of(std::vector<double> v) {
   if (v.empty()) return 0.0;
   std::sort(v.begin(), v.end());

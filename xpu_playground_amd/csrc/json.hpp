@@ -9,6 +9,7 @@
 // exactly (digits only, overflow rejected) rather than through a double.
 #pragma once
 
+#include <algorithm>
 #include <cerrno>
 #include <cstdint>
 #include <cstdlib>
@@ -91,6 +92,7 @@ private:
         if (peek() == close) {
           ++pos_;
           c.end = static_cast<uint32_t>(d_.tape_.size());
+          if (c.type == Type::Object) unique_names(open.back());
           open.pop_back();
           continue;
         }
@@ -131,6 +133,23 @@ private:
       while (pos_ < in_.size() && (in_[pos_] == ' ' || in_[pos_] == '\t' || in_[pos_] == '\n' || in_[pos_] == '\r'))
         ++pos_;
     }
+    // An object whose member names repeat is rejected, as the reference's
+    // reader does (qwen3/model.cpp:204-205): the names are sorted and
+    // compared neighbour to neighbour once the object is closed.
+    void unique_names(uint32_t object) const {
+      std::vector<std::string_view> names;
+      names.reserve(d_.tape_[object].count);
+      const uint32_t end = d_.tape_[object].end;
+      for (uint32_t k = object + 1; k < end; k = d_.tape_[k + 1].end)
+        names.push_back(std::string_view(d_.text_).substr(d_.tape_[k].off, d_.tape_[k].len));
+      std::sort(names.begin(), names.end());
+      for (size_t i = 1; i < names.size(); ++i)
+        if (names[i] == names[i - 1])
+          throw std::runtime_error(d_.source_ + ": malformed JSON: duplicate object key \"" +
+                                   std::string(names[i]) + "\" in the object that ends at offset " +
+                                   std::to_string(pos_ - 1));
+    }
+
     uint32_t push(Type t) {
       if (d_.tape_.size() >= 0xfffffff0u) fail("a smaller document");
       d_.tape_.push_back(Entry{t, static_cast<uint32_t>(d_.tape_.size() + 1), 0, 0, 0, 0.0});

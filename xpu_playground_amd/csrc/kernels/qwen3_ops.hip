@@ -42,7 +42,7 @@ extern "C" __global__ __launch_bounds__(256) void QwenRmsNorm(
   for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) output[i] = xs[i];
 }
 
-// kernels_entry.cpp:271-277: bf16 GEMV with lda = columns
+// kernels_entry.cpp:23-29: bf16 GEMV with lda = columns
 extern "C" __global__ __launch_bounds__(256) void QwenGemv(
     const uint16_t *__restrict__ matrix, const uint16_t *__restrict__ vector,
     uint16_t *__restrict__ output, uint32_t rows, uint32_t columns) {

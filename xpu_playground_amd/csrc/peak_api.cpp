@@ -214,121 +214,3 @@ extern "C" int run_peak_mem(int argc, char **argv) {
     return 1;
   }
 }
-
-namespace {
-
-struct SyncOptions {
-  unsigned launches = 2000;  // dependent empty launches per timing
-  unsigned stages = 500;     // in-kernel handoffs per launch
-};
-
-[[noreturn]] void sync_usage(const char *program, int status) {
-  std::ostream &out = status ? std::cerr : std::cout;
-  out << "Usage: " << program << " [--launches N] [--stages N]\n"
-      << "  --launches N  dependent empty kernel launches timed on the stream and in a graph (default: 2000)\n"
-      << "  --stages N    all-to-all handoffs inside one cooperative launch, per variant (default: 500)\n";
-  std::exit(status);
-}
-
-}  // namespace
-
-// What a dependent step between kernels of one block per compute unit
-// costs: a kernel boundary (the end of one launch to the start of the next,
-// on the stream and inside a captured graph) against an all-to-all handoff
-// inside one persistent launch, in the four publication forms of
-// kernels/peak.hip (xpu_peak_handoff_v*). The decode step of the Qwen3
-// engine is a chain of such dependent steps (142 per token at 0.6B).
-extern "C" int run_peak_sync(int argc, char **argv) {
-  try {
-    SyncOptions o;
-    for (int i = 1; i < argc; ++i) {
-      const std::string_view arg(argv[i]);
-      if (arg == "-h" || arg == "--help") sync_usage(argv[0], 0);
-      if (++i == argc) throw std::invalid_argument(std::string(arg) + " requires a value");
-      const std::string_view value(argv[i]);
-      if (arg == "--launches") o.launches = xpu::parse_positive<unsigned>(value, arg);
-      else if (arg == "--stages") o.stages = xpu::parse_positive<unsigned>(value, arg);
-      else throw std::invalid_argument("unknown option: " + std::string(arg));
-    }
-    RuntimeGuard guard;
-    check(xpu_rt_create(nullptr, -1, &guard.rt));
-    xpu_runtime *rt = guard.rt;
-    std::cout << "Device: " << rt->name << " (" << rt->arch << ", " << rt->compute_units << " CUs)\n";
-    const uint32_t G = rt->compute_units;
-    const xpu::KernelInfo *empty = rt->find_exact("xpu_peak_empty");
-    if (!empty) throw std::runtime_error("kernel is absent from module: xpu_peak_empty");
-    void *start = nullptr, *stop = nullptr;
-    check(xpu_rt_event_create(rt, &start));
-    check(xpu_rt_event_create(rt, &stop));
-    auto chain = [&] {
-      for (unsigned i = 0; i < o.launches; ++i) check(rt->launch(*empty, G, 1, 256, 0, nullptr, 0));
-    };
-    chain();
-    check(xpu_rt_synchronize(rt));
-    check(xpu_rt_event_record(rt, start));
-    chain();
-    check(xpu_rt_event_record(rt, stop));
-    float ms = 0;
-    check(xpu_rt_event_elapsed_ms(start, stop, &ms));
-    const double stream_us = ms * 1e3 / o.launches;
-    check(xpu_rt_capture_begin(rt));
-    chain();
-    void *graph = nullptr;
-    check(xpu_rt_capture_end(rt, &graph));
-    check(xpu_rt_graph_launch(rt, graph));
-    check(xpu_rt_synchronize(rt));
-    check(xpu_rt_event_record(rt, start));
-    check(xpu_rt_graph_launch(rt, graph));
-    check(xpu_rt_event_record(rt, stop));
-    check(xpu_rt_event_elapsed_ms(start, stop, &ms));
-    xpu_rt_graph_destroy(graph);
-    const double graph_us = ms * 1e3 / o.launches;
-    std::cout << std::fixed << std::setprecision(3) << "Kernel boundary, " << G
-              << " blocks per launch: " << stream_us << " us per dependent launch on a stream, " << graph_us
-              << " us in a graph\n";
-
-    int wall_khz = 0;
-    if (hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, rt->device) != hipSuccess || wall_khz <= 0)
-      throw std::runtime_error("cannot query the constant-rate clock frequency");
-    const uint32_t groups = (G + 31) / 32;
-    void *flags = nullptr, *counters = nullptr, *out = nullptr, *err = nullptr, *times = nullptr;
-    check(xpu_rt_alloc(rt, G * 4ull, 256, &flags));
-    check(xpu_rt_alloc(rt, groups * 32 * 4ull, 256, &counters));
-    check(xpu_rt_alloc(rt, 2ull * G * 64 * 4, 256, &out));
-    check(xpu_rt_alloc(rt, 8, 256, &err));
-    check(xpu_rt_alloc(rt, G * 8ull, 256, &times));
-    const char *labels[] = {"fences in every wave (C++ release/acquire)", "one fence pair per block",
-                            "device-coherent data, flag per block", "device-coherent data, counter per 32 blocks"};
-    const int variants[] = {0, 1, 3, 4};
-    bool data_ok = true;
-    for (int i = 0; i < 4; ++i) {
-      const std::string name = "xpu_peak_handoff_v" + std::to_string(variants[i]);
-      const xpu::KernelInfo *k = rt->find_exact(name);
-      if (!k) throw std::runtime_error("kernel is absent from module: " + name);
-      check(xpu_rt_memset(rt, flags, 0, G * 4ull));
-      check(xpu_rt_memset(rt, counters, 0, groups * 32 * 4ull));
-      check(xpu_rt_memset(rt, out, 0, 2ull * G * 64 * 4));
-      check(xpu_rt_memset(rt, err, 0, 8));
-      uint32_t stages = o.stages;
-      const xpu_kernel_arg args[] = {{8, &flags}, {8, &counters}, {8, &out}, {8, &err}, {4, &stages}, {8, &times}};
-      check(rt->launch(*k, G, 1, 256, 0, args, 6, true));
-      check(xpu_rt_synchronize(rt));
-      uint32_t e[2] = {0, 0};
-      check(xpu_rt_copy_from_device(rt, e, err, 8));
-      if (e[0]) throw std::runtime_error(name + ": a wait passed its bound");
-      if (e[1]) data_ok = false;
-      std::vector<uint64_t> t(G);
-      check(xpu_rt_copy_from_device(rt, t.data(), times, G * 8ull));
-      const uint64_t slowest = *std::max_element(t.begin(), t.end());
-      std::cout << "In-kernel all-to-all handoff, " << labels[i] << ": " << std::setprecision(3)
-                << slowest / (wall_khz * 1e-3) / o.stages << " us per stage\n";
-    }
-    xpu_rt_event_destroy(start);
-    xpu_rt_event_destroy(stop);
-    std::cout << "Data check: " << (data_ok ? "PASS" : "FAIL") << '\n';
-    return data_ok ? 0 : 1;
-  } catch (const std::exception &error) {
-    std::cerr << "Error: " << error.what() << '\n';
-    return 1;
-  }
-}
