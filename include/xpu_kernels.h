@@ -38,7 +38,12 @@ int xpu_gemv(xpu_runtime *rt, int dtype, const void *A, const void *x, void *y,
  * gemm.cpp:98-101 / peak_l0.cpp:929-934, and the choice between its large
  * and small tile (gemm.cpp:145): the block tile (256x256, 128x256 or
  * 128x128) is the one with the least estimated time at this shape on this
- * GPU's compute units (xpu_gemm_tile). */
+ * GPU's compute units (xpu_gemm_tile). Any M, N, K and 2-byte aligned
+ * pointers: the operands are read in place (the reference pads them on the
+ * host, gemm.cpp:75-85). Outputs that leave most compute units idle even
+ * with 128 x 128 tiles, with 8 or more 64-deep K-slices, split K over the
+ * idle units (FP32 partials in the runtime's workspace, added in split
+ * order). Asynchronous on the runtime's stream. */
 int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
              uint32_t M, uint32_t N, uint32_t K);
 
@@ -47,21 +52,21 @@ int xpu_gemm(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
  * large_tile expression of gemm.cpp:145. */
 int xpu_gemm_tile(const xpu_runtime *rt, uint32_t M, uint32_t N, uint32_t *rows, uint32_t *cols);
 
-/* Size of the scratch array behind xpu_gemm_noalloc: 32 MiB per GPU. */
-#define XPU_GEMM_NOALLOC_SCRATCH_BYTES (32ull << 20)
+/* Size of the scratch array behind xpu_gemm_noalloc: 16 MiB per GPU. */
+#define XPU_GEMM_NOALLOC_SCRATCH_BYTES (16ull << 20)
 
 /* xpu_gemm without allocation. No counterpart in the reference: for callers
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). Same kernels and results
- * as xpu_gemm, bit for bit; the zero-padded copies of operands whose rows are
- * not 16-byte aligned (K or N not a multiple of 8, or a misaligned pointer)
- * go into a fixed device array of XPU_GEMM_NOALLOC_SCRATCH_BYTES per GPU,
- * set up when the first runtime on that GPU is created and held until the
- * process ends, instead of the runtime's workspace. Needs of more than that
- * (rows x padded columns x 2 bytes, A and B together) fail with
- * XPU_ERR_INVALID before any launch; aligned operands need none. Calls no
- * hipMalloc/hipFree. All calls on one GPU share the array: calls that
- * overlap on one GPU (other streams or runtimes) race. */
+ * as xpu_gemm, bit for bit. Where xpu_gemm splits K (outputs that leave most
+ * compute units idle, with 8 or more 64-deep K-slices), its FP32 partials
+ * (splits x M x round_up(N, 4) x 4 bytes) go into a fixed device array of
+ * XPU_GEMM_NOALLOC_SCRATCH_BYTES per GPU, set up when the first runtime on
+ * that GPU is created and held until the process ends, instead of the
+ * runtime's workspace; other shapes use no scratch. Needs above the array
+ * fail with XPU_ERR_INVALID before any launch. Calls no hipMalloc/hipFree.
+ * All calls on one GPU share the array: calls that overlap on one GPU (other
+ * streams or runtimes) race. */
 int xpu_gemm_noalloc(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C,
                      uint32_t M, uint32_t N, uint32_t K);
 

@@ -50,10 +50,10 @@ def test_gemm_small_shapes(rt, dtype, m, n, k):
 @pytest.mark.parametrize("dtype", [xpu.BF16, xpu.FP16])
 @pytest.mark.parametrize("m,n,k", [(256, 256, 64), (255, 257, 65), (64, 40, 24)])
 def test_gemm_pointers_two_bytes_past_alignment(rt, dtype, m, n, k):
-    # A, B and C start 2 bytes past a 16-byte boundary: both operands go
-    # through the padding copy from 2-byte aligned rows, and every C row starts
-    # 2 bytes past a dword (or a 16-byte) boundary, the unaligned-C epilogue's
-    # cases. Guard codes around C catch any store outside it.
+    # A, B and C start 2 bytes past a 16-byte boundary: both operands are
+    # staged from 2-byte aligned rows in place, and every C row starts 2 bytes
+    # past a dword (or a 16-byte) boundary, the unaligned-C epilogue's cases.
+    # Guard codes around C catch any store outside it.
     print(f"gemm unaligned pointers dtype={dtype} {m}x{n}x{k}", flush=True)
     a = orc.uniform(m * k, 30 + m, dtype)
     b = orc.uniform(k * n, 40 + n, dtype)

@@ -25,9 +25,9 @@ GUARD = 0x7E7E
 
 
 def launch_tile(rt, tag, dtype, a, b, m, n, k, c_offset):
-    """One launch of a tile variant. The kernels read A and B in place, so K
-    and N are multiples of 8 here (xpu_gemm pads other shapes first); C
-    starts c_offset bytes past a 16-byte boundary (the _dmau stores for 2)."""
+    """One launch of a tile variant on 16-byte aligned A and B (K and N
+    multiples of 8 here; ragged shapes and offsets: test_gpu_gemm_edges.py);
+    C starts c_offset bytes past a 16-byte boundary (the _dmau stores for 2)."""
     assert k % 8 == 0 and n % 8 == 0 and a.size == m * k and b.size == k * n
     bm, bn = TILES[tag]
     words = m * n + 32

@@ -15,38 +15,6 @@ namespace {
 
 uint64_t round_up8(uint64_t v) { return (v + 7) & ~uint64_t{7}; }
 
-// Copies a rows x cols matrix (row stride src_ld) into dst with dst_cols
-// columns, zero-filling columns cols..dst_cols-1 (kernels/gemm.hip
-// xpu_pad_rows).
-// blocks of 256 threads, each thread 4 chunks per step (kernels/gemm.hip
-// kPadUnroll), at most 8 resident blocks per compute unit
-uint32_t pad_grid(const xpu_runtime *rt, uint32_t rows, uint32_t dst_cols) {
-  const uint64_t threads = (static_cast<uint64_t>(rows) * (dst_cols / 8) + 3) / 4;
-  return std::max(1u, static_cast<uint32_t>(std::min<uint64_t>((threads + 255) / 256, rt->compute_units * 8ull)));
-}
-
-int pad_rows(xpu_runtime *rt, const void *src, uint64_t src_ld, uint32_t rows, uint32_t cols, void *dst,
-             uint32_t dst_cols) {
-  const xpu::KernelInfo *k = rt->find_exact("xpu_pad_rows");
-  if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: xpu_pad_rows");
-  const xpu_kernel_arg args[] = {{8, &src}, {8, &src_ld}, {4, &rows}, {4, &cols}, {8, &dst}, {4, &dst_cols}};
-  return rt->launch(*k, pad_grid(rt, rows, dst_cols), 1, 256, 0, args, 6);
-}
-
-// Both operands in one launch (xpu_pad_rows2), the blocks split in
-// proportion to the two pad_rows grids.
-int pad_rows2(xpu_runtime *rt, const void *src_a, uint64_t ld_a, uint32_t rows_a, uint32_t cols_a, void *dst_a,
-              uint32_t dst_cols_a, const void *src_b, uint64_t ld_b, uint32_t rows_b, uint32_t cols_b, void *dst_b,
-              uint32_t dst_cols_b) {
-  const xpu::KernelInfo *k = rt->find_exact("xpu_pad_rows2");
-  if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: xpu_pad_rows2");
-  const uint32_t blocks_a = pad_grid(rt, rows_a, dst_cols_a), blocks_b = pad_grid(rt, rows_b, dst_cols_b);
-  const xpu_kernel_arg args[] = {{8, &src_a}, {8, &ld_a},   {4, &rows_a},     {4, &cols_a}, {8, &dst_a},
-                                 {4, &dst_cols_a}, {8, &src_b}, {8, &ld_b}, {4, &rows_b}, {4, &cols_b},
-                                 {8, &dst_b}, {4, &dst_cols_b}, {4, &blocks_a}};
-  return rt->launch(*k, blocks_a + blocks_b, 1, 256, 0, args, 13);
-}
-
 // Block tiles of the MFMA kernels (kernels/gemm.hip), largest first. Rates
 // are FLOP per compute unit relative to the large tile, measured at shapes
 // where every compute unit is busy: a 128 x 256 block alone on a unit runs at
@@ -103,46 +71,68 @@ int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, 
   const uint64_t kp = round_up8(K), np = round_up8(N);
   if (kp * 256 * 2 >= (1ull << 31) || np * 64 * 2 >= (1ull << 31))
     return set_error(XPU_ERR_INVALID, "xpu_gemm: K must be below 4M and N below 16M");
-  // A and B rows must be 16-byte aligned: otherwise the operand is copied,
-  // zero-padded to a multiple of 8 columns, into the runtime's workspace
-  const bool a_direct = reinterpret_cast<uintptr_t>(A) % 16 == 0 && K % 8 == 0;
-  const bool b_direct = reinterpret_cast<uintptr_t>(B) % 16 == 0 && N % 8 == 0;
-  const uint64_t a_bytes = a_direct ? 0 : (static_cast<uint64_t>(M) * kp * 2 + 255) & ~uint64_t{255};
-  const uint64_t b_bytes = b_direct ? 0 : static_cast<uint64_t>(K) * np * 2;
+  if ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) % 2)
+    return set_error(XPU_ERR_INVALID, "xpu_gemm: A, B and C must be 2-byte aligned (16-bit elements)");
+  // A and B are read in place at any K, N and alignment: the kernels stage
+  // unaligned rows by LDS-DMA and handle the K and N edges themselves
+  // (kernels/gemm.hip); nothing is copied or padded
   const void *a_use = A, *b_use = B;
-  if (a_bytes + b_bytes) {
-    void *ws = fixed_workspace;
-    int rc = XPU_OK;
-    if (!ws) rc = rt->scratch(a_bytes + b_bytes, &ws);
-    else if (a_bytes + b_bytes > fixed_capacity)
-      rc = set_error(XPU_ERR_INVALID, "xpu_gemm_noalloc: the operands need " + std::to_string(a_bytes + b_bytes) +
-                                          " bytes of padded copies, above the " + std::to_string(fixed_capacity) +
-                                          "-byte scratch array (A rows need K % 8 == 0 and 16-byte alignment, B "
-                                          "rows N % 8 == 0, to be read in place)");
-    if (rc) return rc;
-    void *bp = static_cast<char *>(ws) + a_bytes;
-    if (!a_direct && !b_direct) {
-      if ((rc = pad_rows2(rt, A, K, M, K, ws, static_cast<uint32_t>(kp), B, N, K, N, bp, static_cast<uint32_t>(np))))
-        return rc;
-    } else if (!a_direct) {
-      if ((rc = pad_rows(rt, A, K, M, K, ws, static_cast<uint32_t>(kp)))) return rc;
-    } else if ((rc = pad_rows(rt, B, N, K, N, bp, static_cast<uint32_t>(np)))) {
-      return rc;
-    }
-    if (!a_direct) a_use = ws;
-    if (!b_direct) b_use = bp;
-  }
-  const uint32_t k_run = static_cast<uint32_t>(a_direct ? K : kp);  // reduction length seen by the kernel
-  const uint32_t n_run = static_cast<uint32_t>(b_direct ? N : np);  // columns of the B operand
+  const uint32_t k_run = K, n_run = N;
   const bool c16 = reinterpret_cast<uintptr_t>(C) % 16 == 0 && N % 8 == 0;
   const GemmTile &tile = choose_tile(rt->compute_units, M, n_run);
+  // K % 8 != 0 or N odd: the _edge form cuts the chunk that straddles
+  // column K and restores the elements the range check cuts at the
+  // operands' ends (kernels/gemm.hip)
+  const bool edge = K % 8 != 0 || N % 2 != 0;
+  const char *dt = dtype ? "fp16" : "bf16";
+  // Split K where even 128 x 128 tiles leave at least half the compute
+  // units idle and the reduction is long (8 or more 64-deep slices): about
+  // CUs / tiles ranges of a multiple of 2 slices; FP32 partials
+  // [split][M][pitch] in the workspace (the runtime's, or the caller's fixed
+  // array), then one reduction in split order that rounds to the output
+  // type. Within the GEMM's tolerance, not bit-equal to one chain (the FP32
+  // sum is re-associated at the range boundaries).
+  {
+    const uint64_t t128 = ((static_cast<uint64_t>(M) + 127) / 128) * ((static_cast<uint64_t>(N) + 127) / 128);
+    const uint32_t nslices = (K + 63) / 64;
+    if (std::string(tile.tag) == "_t128" && t128 * 2 <= rt->compute_units && nslices >= 8) {
+      const uint32_t want = static_cast<uint32_t>((rt->compute_units + t128 - 1) / t128);
+      const uint32_t spl = ((nslices + want - 1) / want + 1) / 2 * 2, splits = (nslices + spl - 1) / spl;
+      if (splits >= 2) {
+        const uint32_t pitch = (N + 3) / 4 * 4;
+        const uint64_t bytes = static_cast<uint64_t>(splits) * M * pitch * 4;
+        void *ws = fixed_workspace;
+        int rc = XPU_OK;
+        if (!ws) rc = rt->scratch(bytes, &ws);
+        else if (bytes > fixed_capacity)
+          rc = set_error(XPU_ERR_INVALID, "xpu_gemm_noalloc: the split-K partials need " + std::to_string(bytes) +
+                                              " bytes, above the " + std::to_string(fixed_capacity) +
+                                              "-byte scratch array");
+        if (rc) return rc;
+        const std::string pname = std::string("xpu_gemm_") + dt + "_t128_part_dma" + (edge ? "_edge" : "");
+        const xpu::KernelInfo *kp = rt->find_exact(pname);
+        const xpu::KernelInfo *kr = rt->find_exact("xpu_gemm_splitk_reduce_any");
+        if (!kp || !kr) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: " + pname);
+        uint32_t kb = spl, ldp = pitch, n_out = N;
+        const xpu_kernel_arg pargs[] = {{8, &a_use}, {8, &b_use}, {8, &ws},  {4, &M},     {4, &n_run},
+                                        {4, &k_run}, {4, &kb},    {4, &ldp}, {4, &n_out}};
+        if ((rc = rt->launch(*kp, static_cast<uint32_t>(t128 * splits), 1, 256, 0, pargs, 9))) return rc;
+        const uint64_t threads = static_cast<uint64_t>(M) * ((N + 3) / 4);
+        const uint32_t grid =
+            static_cast<uint32_t>(std::min<uint64_t>((threads + 255) / 256, rt->compute_units * 8ull));
+        uint32_t ldc = N, ns = splits, d = static_cast<uint32_t>(dtype);
+        const xpu_kernel_arg rargs[] = {{8, &ws}, {8, &C}, {4, &M}, {4, &n_run}, {4, &ldp}, {4, &ldc}, {4, &ns}, {4, &d}};
+        return rt->launch(*kr, grid, 1, 256, 0, rargs, 8);
+      }
+    }
+  }
   // the 256 x 256 kernels come in a form for an odd number (3 or more) of
   // 64-deep K-slices, which skips the slice of zeros that closes the last
   // pair and the last slice's k-steps past K
   const uint32_t slices = (k_run + 63) / 64;
   const bool odd = tile.tag[0] == '\0' && slices % 2 == 1 && slices >= 3;
-  const std::string name = std::string("xpu_gemm_") + (dtype ? "fp16" : "bf16") + tile.tag + (odd ? "_odd" : "") +
-                           (c16 ? "_dma" : "_dmau");
+  const std::string name = std::string("xpu_gemm_") + dt + tile.tag + (odd ? "_odd" : "") +
+                           (c16 ? "_dma" : "_dmau") + (edge ? "_edge" : "");
   const xpu::KernelInfo *k = rt->find_exact(name);
   if (!k) return set_error(XPU_ERR_NOT_FOUND, "kernel is absent from module: " + name);
   const uint64_t tiles = ((static_cast<uint64_t>(M) + tile.rows - 1) / tile.rows) *

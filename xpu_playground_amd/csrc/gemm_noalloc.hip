@@ -1,18 +1,20 @@
 // xpu_gemm_noalloc: the GEMM entry point for callers that cannot allocate
 // device memory (code under HIP graph capture, tight serving loops). The
-// padded operand copies that xpu_gemm stages in the runtime's grow-only
-// workspace go into `scratch`, a file-scope device array of fixed size that
-// each GPU holds from the first runtime created on it until the process
-// ends. Built by hipcc into the host library (host + gfx950 device code);
-// the GEMM kernels themselves are those of the runtime's code object.
+// FP32 split-K partials that xpu_gemm keeps in the runtime's grow-only
+// workspace (outputs that leave most compute units idle, long reductions)
+// go into `scratch`, a file-scope device array of fixed size that each GPU
+// holds from the first runtime created on it until the process ends. Built
+// by hipcc into the host library (host + gfx950 device code); the GEMM
+// kernels themselves are those of the runtime's code object.
 //
 // `scratch` names a host-side stand-in in host code: its device address on
 // each GPU comes from hipGetSymbolAddress, looked up once per device with
 // that device current (xpu_rt_create), and only that address is passed to
 // kernels. Every call on one GPU shares its array, which keeps the last
-// call's contents; the padding kernel writes every byte a call reads
-// (zeros included), so nothing needs clearing. Calls that overlap on one
-// GPU (several runtimes or streams) race on the array.
+// call's contents; every partial a reduction reads is written by the same
+// call first (each split's blocks store their whole tile range), so nothing
+// needs clearing. Calls that overlap on one GPU (several runtimes or
+// streams) race on the array.
 #include "../../include/xpu_kernels.h"
 #include "runtime_internal.hpp"
 

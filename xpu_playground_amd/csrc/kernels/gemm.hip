@@ -33,13 +33,26 @@
 // (an odd slice count of 3 or more) run the last slice on its own, only its
 // k-steps below K.
 //
-// Edges: loads past row M of A and past row K of B read zero through the
-// buffer range check; 16-byte chunks past column K of A or N of B are sent
-// beyond the descriptor range, so K and N must be multiples of 8 with A and
-// B 16-byte aligned; the host pads other shapes into a workspace first
-// (xpu_pad_rows below, the device counterpart of the reference's host
-// padding, gemm.cpp:75-85). Stores are masked to M x n_out; the _dmau
-// variants take C rows that are only 2-byte aligned.
+// Edges, for any M, N, K and operands at any 2-byte alignment (the
+// reference pads on the host instead, gemm.cpp:75-85):
+// - The LDS-DMA moves 16 bytes from any byte address (checked on gfx950 at
+//   every offset 0..15), so rows of A and B that are not 16-byte aligned
+//   (K or N not a multiple of 8, or an unaligned base) are staged in place.
+// - Loads past row M of A and past row K of B read zero through the buffer
+//   range check; 16-byte chunks that start at or past column K of A or N of
+//   B are sent beyond the descriptor range.
+// - The chunk of A that straddles column K holds the next row's first
+//   elements: in the last K-slice each wavefront zeroes them in the rows it
+//   staged, after its DMA has landed and before the barrier that publishes
+//   the slice (fix_tail). B rows past K are zero, and B columns past N only
+//   reach C columns that are not stored.
+// - The range check zeroes whole dwords (any dword whose end passes the
+//   range reads 0), so with K odd the last element of A, A[M-1][K-1], shares
+//   a dword with the byte past A's end and reads 0, and with N odd so does
+//   B[K-1][N-1]. fix_tail puts each back from a plain 2-byte load. Nothing
+//   is read past either operand.
+// Stores are masked to M x n_out; the _dmau variants take C rows that are
+// only 2-byte aligned.
 #include "device_common.hpp"
 
 #include <type_traits>
@@ -149,17 +162,20 @@ template <int MI, int NJ, int BK, int S, bool BT = false> struct Cfg {
 // BT: B is given as its transpose, [N][K] row-major (the rows of a weight
 // matrix W for C = X W^T); its tile is staged and read like A's. RES: C is
 // updated in place, C = bf16(C + bf16(A B)) (a residual add), C16 only.
-// PART (with BT): split K. Block b computes tile b % tiles over slices
-// split * kb .. split * kb + kb - 1, split = b / tiles (kb, a multiple of S,
-// is the slices per split here), and stores its FP32 partial tile into
-// ((float *) C)[split][M][N]; xpu_gemm_splitk_reduce adds the splits.
+// PART: split K. Block b computes tile b % tiles over slices split * kb ..
+// split * kb + kb - 1, split = b / tiles (kb, a multiple of S, is the slices
+// per split here), and stores its FP32 partial tile into ((float *)
+// C)[split][M][ldc] (ldc >= N, a multiple of 4: whole 16-byte groups of
+// columns are stored); xpu_gemm_splitk_reduce[_any] adds the splits.
 template <int DT, int MI, int NJ, int BK, int S, int P, int D, bool C16, bool ODD, bool BT = false,
-          bool RES = false, bool PART = false>
+          bool RES = false, bool PART = false, bool EDGE = false>
 XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
                      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {
   using G = Cfg<MI, NJ, BK, S, BT>;
+  const uint32_t K_ = K, M_ = M, N_ = N;  // for fix_tail, which shadows them
   static_assert(!RES || C16, "the residual epilogue stores 16-byte chunks");
-  static_assert(!PART || (BT && !RES && !ODD), "split K: [n][k] weights, the reduction applies any residual");
+  static_assert(!PART || (!RES && !ODD), "split K: the reduction applies any residual");
+  static_assert(!EDGE || !BT, "the [n][k] kernels take K % 8 == 0");
   __shared__ __align__(1024) uint8_t lds[G::kLds];
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -203,7 +219,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
                    (static_cast<int64_t>(N - n0) * K - static_cast<int64_t>(k0)) * 2);
     else
       d.r_b = rsrc(B + k0 * N + n0,
-                   (static_cast<int64_t>(kb) - static_cast<int64_t>(k0)) * N * 2 - static_cast<int64_t>(n0) * 2);
+                   (static_cast<int64_t>(K) - static_cast<int64_t>(k0)) * N * 2 - static_cast<int64_t>(n0) * 2);
     d.a_base = k0 + a_chunk * 8u < K ? a_voff : kOob;
     d.b_base = !BT || k0 + b_chunk * 8u < K ? b_voff : kOob;
     d.st_base = lds0 + stage * G::kStage;
@@ -327,6 +343,56 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 #pragma unroll
     for (uint32_t op = lo + x * (hi - lo) / nx; op < lo + (x + 1) * (hi - lo) / nx; ++op) dma(d, op);
   };
+  // The last K-slice's edges (EDGE kernels: K % 8 != 0 or N odd), in stage
+  // `stage`, after this wavefront's DMA of the slice has landed and before
+  // the barrier that publishes it. A: lane l owns tile row (wave + 4 (l /
+  // kRpi)) kRpi + l % kRpi (the rows this wave staged) and zeroes the
+  // elements of the chunk holding column K at and past K; the lane holding
+  // row M - 1 restores A[M-1][K-1] (K odd). B: the wave that staged tile row
+  // K - 1 restores B[K-1][N-1] (N odd). The shapes are passed through an
+  // empty asm first, so that the compiler derives the addresses here, once,
+  // instead of holding them in scalar registers across the K loop.
+  // (split K: the last slice of the whole product, in the last split's
+  // blocks; last_local is its index among this block's slices)
+  const uint32_t nk_total = (K + BK - 1) / BK;
+  const uint32_t last_local = nk_total - 1u - s_base;  // wraps past any slice of a block before it
+  auto fix_tail = [&](uint32_t stage) {
+    if constexpr (EDGE) {
+      uint32_t K = K_, M = M_, N = N_;
+      asm volatile("" : "+s"(K), "+s"(M), "+s"(N));
+      const uint32_t kc = K - (nk_total - 1u) * BK;  // live columns of the last slice, 1 .. BK
+      const uint32_t st_base = lds0 + stage * G::kStage;
+      typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+      typedef __attribute__((address_space(3))) uint16_t lds_u16;
+      constexpr uint32_t kRowsW = G::kDmaA * G::kRpi;  // A rows staged per wave (kBM / 4)
+      const uint32_t keep = kc % 8u;
+      if (keep != 0 && lane < kRowsW) {
+        const uint32_t r = (wave + 4u * (lane / G::kRpi)) * G::kRpi + lane % G::kRpi;
+        const uint32_t addr = st_base + r * (2u * BK) + 16u * ((kc / 8u) ^ a_swz<BK>(r & 15u));
+        const u32x4 v = *reinterpret_cast<const lds_u32x4 *>(addr);
+        // element keep - 1 (even when K is odd) is the low half of dword keep / 2
+        const bool restore = (K & 1u) && m0 + r == M - 1u;
+        const uint32_t e = restore ? A[static_cast<uint64_t>(M - 1u) * K + (K - 1u)] : 0u;
+        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (uint32_t d = 0; d < 4; ++d) {
+          if (restore && d == keep / 2u) w[d] = (w[d] & 0xffff0000u) | e;
+          if (2u * d >= keep) w[d] = 0u;
+          else if (2u * d + 1u >= keep) w[d] &= 0xffffu;
+        }
+        *reinterpret_cast<lds_u32x4 *>(addr) = u32x4{w[0], w[1], w[2], w[3]};
+      }
+      if (N & 1u) {
+        const uint32_t kt = kc - 1u, nt = N - 1u - n0;
+        if (nt < G::kBN && (kt / G::kBRpi) % 4u == wave && lane == 0) {
+          const uint32_t addr =
+              st_base + G::kABytes + kt * G::kBRow + 16u * ((nt / 8u) ^ b_swz(kt & 3u)) + 2u * (nt % 8u);
+          *reinterpret_cast<lds_u16 *>(addr) = B[static_cast<uint64_t>(K - 1u) * N + (N - 1u)];
+        }
+      }
+    }
+  };
+
   Frags frag[2];
   static_assert(S == 2 || (S >= 3 && S <= 6 && !ODD), "groups of 2 to 6 slices; the odd tail follows a pair");
   // Slice s lives in LDS stage s % S. Prologue: slices 0 .. S - 2 whole, and
@@ -341,6 +407,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   Slice pend = slice_of(S - 1, S - 1);
   dma_part(pend, 0, 0, 1);
   wait_vmcnt<(S - 2) * G::kDma + G::kDma / D>();  // slice 0 landed
+  if (EDGE && last_local == 0) fix_tail(0);
   __syncthreads();
 #pragma unroll
   for (uint32_t r = 0; r < G::kReads; ++r) read(0, 0, frag[0], r);
@@ -377,6 +444,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
             __builtin_amdgcn_sched_barrier(0);
           }
           wait_vmcnt<(S - 2) * G::kDma>();
+          if (EDGE && s0 + st + 1u == last_local) fix_tail((st + 1) % S);  // publishes the last slice
           __syncthreads();
           __builtin_amdgcn_sched_barrier(0);
           pend = slice_of(s0 + st + S, st);
@@ -450,7 +518,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   if constexpr (PART) {
     // FP32 partials straight from the accumulators: lane l holds columns
     // 32 j + 8 g + 4 (l / 32) .. + 3 of row 32 i + l % 32 of its wave tile
-    float *part = reinterpret_cast<float *>(C) + static_cast<uint64_t>(split) * M * N;
+    float *part = reinterpret_cast<float *>(C) + static_cast<uint64_t>(split) * M * ldc;
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -460,7 +528,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
           const uint32_t m = m0 + wm * G::kBMW + 32u * i + (lane & 31u);
           const uint32_t n = n0 + wn * G::kBNW + 32u * j + 8u * g + 4u * (lane >> 5);
           if (m < M && n < N)
-            *reinterpret_cast<f32x4 *>(part + static_cast<uint64_t>(m) * N + n) =
+            *reinterpret_cast<f32x4 *>(part + static_cast<uint64_t>(m) * ldc + n) =
                 f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
         }
     return;
@@ -549,13 +617,19 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 }  // namespace dma
 }  // namespace xpu
 
-#define XPU_GEMM_DMA_VARIANT(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD)                   \
-  extern "C" __global__ __launch_bounds__(256, MINB) void NAME(                               \
-      const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C, \
-      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {         \
-    XPU_STAMP(xpu::kStampGemm);                                                                 \
-    xpu::dma::body<DT, MI, NJ, BK, S, P, D, C16, ODD>(A, B, C, M, N, K, kb, ldc, n_out);       \
+// Each [k][n] kernel also comes in an _edge form (EDGE: the last slice's
+// fix-up for K % 8 != 0 or odd N), so that aligned shapes run code without it.
+#define XPU_GEMM_DMA_VARIANT1(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD, EDGE)                          \
+  extern "C" __global__ __launch_bounds__(256, MINB) void NAME(                                             \
+      const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,               \
+      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {                       \
+    XPU_STAMP(xpu::kStampGemm);                                                                               \
+    xpu::dma::body<DT, MI, NJ, BK, S, P, D, C16, ODD, false, false, false, EDGE>(A, B, C, M, N, K, kb, ldc,  \
+                                                                                  n_out);                    \
   }
+#define XPU_GEMM_DMA_VARIANT(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD) \
+  XPU_GEMM_DMA_VARIANT1(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD, false) \
+  XPU_GEMM_DMA_VARIANT1(NAME##_edge, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD, true)
 
 // C = A W^T with W given [N][K] (BT) for the batched prompt projections, bf16,
 // 16-byte aligned C; _res adds into C (residual)
@@ -626,6 +700,32 @@ extern "C" __global__ __launch_bounds__(256) void xpu_gemm_splitk_reduce(const f
       w[q] = h[0] | (h[1] << 16);
     }
     *reinterpret_cast<xpu::u32x4 *>(dst) = xpu::u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
+// C (M x N, bf16 or fp16, row stride ldc, any alignment) from the FP32
+// partials P[splits][M][pitch] of the [k][n] split-K GEMM (pitch >= N, a
+// multiple of 4), added in split order and rounded to nearest even; each
+// thread takes 4 consecutive columns of one row, grid-stride.
+extern "C" __global__ __launch_bounds__(256) void xpu_gemm_splitk_reduce_any(
+    const float *__restrict__ P, uint16_t *__restrict__ C, uint32_t M, uint32_t N, uint32_t pitch, uint32_t ldc,
+    uint32_t splits, uint32_t dtype) {
+  const uint32_t groups = (N + 3u) / 4u;
+  const uint64_t total = static_cast<uint64_t>(M) * groups, split4 = static_cast<uint64_t>(M) * pitch / 4u;
+  for (uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < total;
+       g += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+    const uint32_t m = static_cast<uint32_t>(g / groups), n = static_cast<uint32_t>(g % groups) * 4u;
+    const float4 *p = reinterpret_cast<const float4 *>(P + static_cast<uint64_t>(m) * pitch + n);
+    float4 acc = p[0];
+    for (uint32_t s = 1; s < splits; ++s) {
+      const float4 v = p[s * split4];
+      acc = float4{acc.x + v.x, acc.y + v.y, acc.z + v.z, acc.w + v.w};
+    }
+    const float y[4] = {acc.x, acc.y, acc.z, acc.w};
+    uint16_t *dst = C + static_cast<uint64_t>(m) * ldc + n;
+#pragma unroll
+    for (uint32_t e = 0; e < 4; ++e)
+      if (n + e < N) dst[e] = static_cast<uint16_t>(dtype ? xpu::f32_to_fp16(y[e]) : xpu::f32_to_bf16(y[e]));
   }
 }
 
@@ -746,10 +846,29 @@ XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_t128_dma, xpu::kFp16, 2, 2, 64, 2, 2, 2, 2, t
 XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_t128_dmau, xpu::kBf16, 2, 2, 64, 2, 2, 2, 2, false, false)
 XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_t128_dmau, xpu::kFp16, 2, 2, 64, 2, 2, 2, 2, false, false)
 
+// Split K for [k][n] products that leave most compute units idle even with
+// 128 x 128 tiles (a small output with a long reduction): FP32 partials of
+// each K range (kb slices, a multiple of 2), added by
+// xpu_gemm_splitk_reduce_any; _edge as for the whole-K kernels.
+#define XPU_GEMM_PART_KN(NAME, DT, EDGE)                                                                   \
+  extern "C" __global__ __launch_bounds__(256, 2) void NAME(                                               \
+      const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C, uint32_t M, \
+      uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {                                  \
+    XPU_STAMP(xpu::kStampGemm);                                                                             \
+    xpu::dma::body<DT, 2, 2, 64, 2, 2, 2, true, false, false, false, true, EDGE>(A, B, C, M, N, K, kb, ldc, \
+                                                                                n_out);                    \
+  }
+XPU_GEMM_PART_KN(xpu_gemm_bf16_t128_part_dma, xpu::kBf16, false)
+XPU_GEMM_PART_KN(xpu_gemm_bf16_t128_part_dma_edge, xpu::kBf16, true)
+XPU_GEMM_PART_KN(xpu_gemm_fp16_t128_part_dma, xpu::kFp16, false)
+XPU_GEMM_PART_KN(xpu_gemm_fp16_t128_part_dma_edge, xpu::kFp16, true)
+
 // dst[r][c] = src[r * src_ld + c] for c < cols, 0 for cols <= c < dst_cols
 // (dst_cols % 8 == 0, dst 16-byte aligned): the zero padding of the
 // reference's host GEMM setup (gemm.cpp:75-85) done on the device, so rows
-// of the copy are 16-byte aligned. One thread per 8 destination elements.
+// of the copy are 16-byte aligned. xpu_gemm does not use it (its kernels
+// read unpadded operands); it prepares operands for a measurement of the
+// reference's own method (pad once at setup, then time the GEMM). One thread per 8 destination elements.
 // src only needs 2-byte alignment: a whole chunk is one 16-byte load at a
 // 2-byte aligned address (global memory runs in unaligned access mode on
 // gfx950). The chunk holding the row's end is read element by element, so
@@ -806,16 +925,4 @@ extern "C" __global__ __launch_bounds__(256) void xpu_pad_rows(const uint16_t *_
                                                                uint32_t rows, uint32_t cols,
                                                                uint16_t *__restrict__ dst, uint32_t dst_cols) {
   xpu::pad_rows(src, src_ld, rows, cols, dst, dst_cols, 0, gridDim.x);
-}
-
-// Both GEMM operands in one launch: blocks 0 .. blocks_a - 1 copy the first
-// matrix, the others the second (same layout rules as xpu_pad_rows).
-extern "C" __global__ __launch_bounds__(256) void xpu_pad_rows2(
-    const uint16_t *__restrict__ src_a, uint64_t ld_a, uint32_t rows_a, uint32_t cols_a, uint16_t *__restrict__ dst_a,
-    uint32_t dst_cols_a, const uint16_t *__restrict__ src_b, uint64_t ld_b, uint32_t rows_b, uint32_t cols_b,
-    uint16_t *__restrict__ dst_b, uint32_t dst_cols_b, uint32_t blocks_a) {
-  if (blockIdx.x < blocks_a)
-    xpu::pad_rows(src_a, ld_a, rows_a, cols_a, dst_a, dst_cols_a, 0, blocks_a);
-  else
-    xpu::pad_rows(src_b, ld_b, rows_b, cols_b, dst_b, dst_cols_b, blocks_a, gridDim.x - blocks_a);
 }
