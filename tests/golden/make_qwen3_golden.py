@@ -63,9 +63,9 @@ CASES = {
     "small-varied-b": ("small", 3, 0.5, 4, 16, 32, 32),
     "tiny-varied": ("tiny", 1, 1.0, 2, 16, 32, 32),
     # the reference engine's untied lm_head at the small shape
-    "small-untied": ("small", 4, 0.5, 5, 16, 32, 32, {"untied"}),
+    "small-untied": ("small", 4, 0.5, 5, 16, 32, 32, {"untied", "forced"}),
     # the BASELINE shape with a stream that changes, teacher-forced
-    "qwen3-0.6b-varied": ("qwen3-0.6b", 7, 0.5, 2, 128, 32, 32, {"forced"}),
+    "qwen3-0.6b-varied": ("qwen3-0.6b", 7, 1.0, 2, 128, 32, 32, {"forced"}),
 }
 
 

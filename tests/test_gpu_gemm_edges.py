@@ -116,13 +116,13 @@ def test_ragged_baseline_shape_reads_operands_in_place(rt):
 
 
 @pytest.mark.parametrize("dtype", [xpu.BF16, xpu.FP16])
-@pytest.mark.parametrize("m,n,k,c_offset", [(1024, 1024, 4096, 0), (512, 512, 1024, 0), (300, 201, 1030, 2),
-                                            (129, 383, 2049, 6), (64, 8, 512, 0)])
+@pytest.mark.parametrize("m,n,k,c_offset", [(1024, 1024, 4096, 0), (512, 512, 2048, 0), (300, 201, 1030, 2),
+                                            (129, 383, 2049, 6), (64, 8, 512, 0), (512, 512, 512, 2)])
 def test_split_k_products(rt, dtype, m, n, k, c_offset):
-    # Outputs that leave most compute units idle with 128 x 128 tiles and 8
-    # or more K-slices are split over the idle units (FP32 partials added in
-    # split order): within the GEMM bar against FP64, written exactly over C
-    # (guard codes around it), on 16-byte and unaligned C
+    # Outputs that leave most compute units idle with 128 x 128 tiles and a
+    # long enough reduction are split over the idle units (FP32 partials
+    # added in split order): within the GEMM bar against FP64, written
+    # exactly over C (guard codes around it), on 16-byte and unaligned C
     print(f"gemm split-K dtype={dtype} {m}x{n}x{k} C offset {c_offset}", flush=True)
     a = orc.uniform(m * k, 100 + m, dtype)
     b = orc.uniform(k * n, 110 + n, dtype)

@@ -161,6 +161,36 @@ def test_transformers_fixtures_varied_streams(rt, name):
     eng.close()
 
 
+@pytest.mark.parametrize("name", qf.FORCED)
+def test_transformers_fixtures_teacher_forced(rt, name):
+    # the teacher-forced fixtures: the reference engine's untied lm_head
+    # (small-untied) and the BASELINE 0.6B shape with a stream that changes
+    # (28 distinct tokens in 32 steps). Fed the prompt and then
+    # transformers' step-path tokens, the engine's logits rows are the
+    # oracle's measured rows bit for bit, in graph and eager modes, so the
+    # fixture's distances to transformers and its token checks
+    # (tests/test_oracle_qwen3.py) hold for the GPU path
+    fx = qf.load(name)
+    cfg = orc.config(fx["preset"], tied=fx["tied"])
+    inputs = qf.forced_inputs(fx)
+    n_prompt = len(fx["prompt"])
+    eng = qwen3.Engine(qwen3.config_from(cfg), max_seq=len(inputs) + 1, seed=fx["weight_seed"],
+                       gain_std=fx["gain_std"], runtime=rt)
+    for mode in (qwen3.GRAPH, qwen3.EAGER):
+        eng.set_mode(mode)
+        rows, toks = [], []
+        for p, tok in enumerate(inputs):
+            t = eng.decode(int(tok), p)
+            if p >= n_prompt - 1:
+                rows.append(eng.logits().copy())
+                toks.append(t)
+        print(f"{name} mode {mode}: {sum(a == b for a, b in zip(toks, fx['hf_steps']))} of 32 tokens equal "
+              f"transformers' step path", flush=True)
+        assert toks == fx["oracle_tokens"][:len(toks)]
+        assert [qf.row_hash(r) for r in rows] == fx["oracle_logits_sha256"], mode
+    eng.close()
+
+
 @pytest.mark.parametrize("tied,sharded", [(1, False), (0, True)])
 def test_checkpoint_loading(rt, tmp_path, tied, sharded):
     cfg = orc.config("tiny", tied=tied)
@@ -374,7 +404,12 @@ def test_gemm_prefill_within_rounding(rt, preset, over, n_prompt, max_seq):
         dmax = float(np.abs(got - want).max())
         print(f"logits rel-L2 {rel:.3e} max|d| {dmax:.3e} (max|logit| {np.abs(want).max():.3e}), "
               f"hidden rel-L2 {rel_h:.3e}", flush=True)
-        assert rel <= 2e-2 and rel_h <= 2e-2, (rel, rel_h)
+        # measured: logits and hidden rel-L2 4e-3 - 1.2e-2, max |d| up to
+        # 5.9e-2 at these shapes: the GEMM form misses the decode's 2e-2
+        # max-abs bar (it is opt-in and labelled so); these bounds hold it
+        # where it is
+        assert rel <= 1.5e-2 and rel_h <= 1.5e-2, (rel, rel_h)
+        assert dmax <= 6.5e-2, dmax
         top2 = np.sort(want)[-2:]
         if top2[1] - top2[0] > 2 * dmax:
             assert out.tolist() == ref.tolist()
@@ -383,6 +418,35 @@ def test_gemm_prefill_within_rounding(rt, preset, over, n_prompt, max_seq):
     eng.set_prefill("batched" if preset == "small" else "stepwise")
     eng.generate(prompt, 1, stop_on_eos=False)
     assert np.array_equal(eng.logits(), ref_logits[0])
+    eng.close()
+
+
+def test_gemm_prefill_full_0_6b_shape(rt):
+    # the BASELINE workload's prompt (configs[4]: 0.6B shape, 28 layers,
+    # 128 seeded ids) in the GEMM form against the bit-exact batched form,
+    # whose first generated token's logits row is the oracle's (the hash the
+    # qwen3-0.6b fixture records)
+    fx = qf.load("qwen3-0.6b")
+    cfg = qwen3.preset("qwen3-0.6b")
+    prompt = np.array(fx["prompt"], np.uint32)
+    eng = qwen3.Engine(cfg, max_seq=256, seed=fx["weight_seed"], gain_std=fx["gain_std"], runtime=rt)
+    eng.set_mode(qwen3.EAGER)
+    out_b, _, _ = eng.generate(prompt, 1, stop_on_eos=False)
+    exact = eng.logits().copy()
+    assert qf.row_hash(exact) == fx["oracle_logits_sha256"][0]
+    eng.set_prefill("gemm")
+    out_g, _, _ = eng.generate(prompt, 1, stop_on_eos=False)
+    got = orc.decode(eng.logits(), xpu.BF16).astype(np.float64)
+    want = orc.decode(exact, xpu.BF16).astype(np.float64)
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    dmax = float(np.abs(got - want).max())
+    print(f"0.6B GEMM-form prompt: logits rel-L2 {rel:.3e}, max|d| {dmax:.3e}", flush=True)
+    # measured 1.36e-2 - 1.56e-2 and 0.041 - 0.049 (DESIGN's figures): above
+    # the decode's 2e-2 max-abs bar, held here as a regression bound
+    assert rel <= 2e-2 and dmax <= 6e-2, (rel, dmax)
+    top2 = np.sort(want)[-2:]
+    if top2[1] - top2[0] > 2 * dmax:
+        assert out_g.tolist() == out_b.tolist()
     eng.close()
 
 

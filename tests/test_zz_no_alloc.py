@@ -49,7 +49,8 @@ def split_bytes(rt, m, n, k):
     want = (rt.compute_units + t128 - 1) // t128
     spl = ((nslices + want - 1) // want + 1) // 2 * 2
     splits = (nslices + spl - 1) // spl
-    return splits * m * ((n + 3) // 4 * 4) * 4 if splits >= 2 else 0
+    nbytes = splits * m * ((n + 3) // 4 * 4) * 4
+    return nbytes if splits >= 2 and (nslices >= 24 or nbytes <= 4 << 20) else 0
 
 
 def test_noalloc_matches_xpu_gemm_on_consecutive_calls(rt):

@@ -86,21 +86,25 @@ int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, 
   const bool edge = K % 8 != 0 || N % 2 != 0;
   const char *dt = dtype ? "fp16" : "bf16";
   // Split K where even 128 x 128 tiles leave at least half the compute
-  // units idle and the reduction is long (8 or more 64-deep slices): about
-  // CUs / tiles ranges of a multiple of 2 slices; FP32 partials
-  // [split][M][pitch] in the workspace (the runtime's, or the caller's fixed
-  // array), then one reduction in split order that rounds to the output
-  // type. Within the GEMM's tolerance, not bit-equal to one chain (the FP32
-  // sum is re-associated at the range boundaries).
+  // units idle and the reduction is long enough to pay for the partials'
+  // round trip: about CUs / tiles ranges of a multiple of 2 slices; FP32
+  // partials [split][M][pitch] in the workspace (the runtime's, or the
+  // caller's fixed array), then one reduction in split order that rounds to
+  // the output type. Within the GEMM's tolerance, not bit-equal to one
+  // chain (the FP32 sum is re-associated at the range boundaries). Measured
+  // against whole-K 128 x 128 tiles (bf16): 1024 x 1024 x 4096 42.6 -> 23.0
+  // us, 768 x 768 x 8192 82.5 -> 26.9, 512^3 12.1 -> 9.2, but 1024^3 (16
+  // slices, 16 MB of partials) 12.5 -> 17.9: so K of 24 slices or more, or
+  // partials of at most 4 MiB.
   {
     const uint64_t t128 = ((static_cast<uint64_t>(M) + 127) / 128) * ((static_cast<uint64_t>(N) + 127) / 128);
     const uint32_t nslices = (K + 63) / 64;
     if (std::string(tile.tag) == "_t128" && t128 * 2 <= rt->compute_units && nslices >= 8) {
       const uint32_t want = static_cast<uint32_t>((rt->compute_units + t128 - 1) / t128);
       const uint32_t spl = ((nslices + want - 1) / want + 1) / 2 * 2, splits = (nslices + spl - 1) / spl;
-      if (splits >= 2) {
-        const uint32_t pitch = (N + 3) / 4 * 4;
-        const uint64_t bytes = static_cast<uint64_t>(splits) * M * pitch * 4;
+      const uint32_t pitch = (N + 3) / 4 * 4;
+      const uint64_t bytes = static_cast<uint64_t>(splits) * M * pitch * 4;
+      if (splits >= 2 && (nslices >= 24 || bytes <= (4ull << 20))) {
         void *ws = fixed_workspace;
         int rc = XPU_OK;
         if (!ws) rc = rt->scratch(bytes, &ws);

@@ -166,6 +166,11 @@ struct xpu_qwen3 {
   // module has its kernels)
   bool pf_ok = false, batched_prefill = false, pf_gemm_ok = false, gemm_prefill = false;
   uint32_t pf_chunk = 0, pf_chunk_gemm = 0;
+  // the prompt buffers are sized for the batched form's chunks at creation
+  // and grow to the GEMM form's (and its [T][2I] buffer) when that form is
+  // selected: pf_rows token rows, pf_gemm_sized with the [gate | up] buffer
+  uint64_t pf_rows = 0;
+  bool pf_gemm_sized = false;
   void *pf_block = nullptr;
   uint16_t *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_a = nullptr,
            *pf_h = nullptr, *pf_gu = nullptr;
@@ -375,6 +380,46 @@ int setup_launches(xpu_qwen3 &e) {
 // count the module has kernels for (xpu_q3_pf_gemv_e<epi>_c<K/512>); the
 // GEMM form needs none of those. The two share the embedding, RMSNorm and
 // QK-norm/RoPE/cache kernels and the chunk buffers.
+// The prompt chunk buffers for the batched form (gemm = false: pf_chunk
+// rows) or the GEMM form (pf_chunk_gemm rows plus the [T][2I] [gate | up]
+// output, and the GEMM's split-K partials reserved in the runtime's
+// workspace so that no prompt grows it mid-way): the residual stream X and
+// its normed copy [T][H], the QKV output [T][(Hq+2Hkv)·128], the roped
+// queries and the attention output [T][Hq·128], the SwiGLU output [T][I].
+// Grows only; the GEMM form's buffers serve the batched form too.
+int size_prompt_buffers(xpu_qwen3 &e, bool gemm) {
+  const xpu_qwen3_config &c = e.c;
+  const uint64_t T = gemm ? e.pf_chunk_gemm : e.pf_chunk;
+  if (T <= e.pf_rows && (!gemm || e.pf_gemm_sized)) return XPU_OK;
+  const uint64_t qd = uint64_t{c.heads} * c.head_dim;
+  const uint64_t qkv_rows = uint64_t{c.heads + 2 * c.kv_heads} * c.head_dim;
+  const uint64_t sizes[7] = {T * c.hidden, T * c.hidden, T * qkv_rows, T * qd, T * qd, T * c.intermediate,
+                             gemm ? T * 2 * c.intermediate : 0};
+  uint64_t total = 0;
+  for (uint64_t n : sizes) total += (n * 2 + 255) & ~uint64_t{255};
+  int rc;
+  if (e.pf_block) {
+    if ((rc = xpu_rt_free(e.rt, e.pf_block))) return rc;  // waits for the stream first
+    e.pf_block = nullptr;
+    e.pf_rows = 0;
+    e.pf_gemm_sized = false;
+  }
+  if ((rc = xpu_rt_alloc(e.rt, total, 4096, &e.pf_block))) return rc;
+  uint16_t **dst[7] = {&e.pf_x, &e.pf_xn, &e.pf_qkv, &e.pf_q, &e.pf_a, &e.pf_h, &e.pf_gu};
+  uint8_t *p = static_cast<uint8_t *>(e.pf_block);
+  for (int i = 0; i < 7; ++i) {
+    *dst[i] = sizes[i] ? reinterpret_cast<uint16_t *>(p) : nullptr;
+    p += (sizes[i] * 2 + 255) & ~uint64_t{255};
+  }
+  e.pf_rows = T;
+  e.pf_gemm_sized = gemm;
+  if (gemm) {
+    void *ws = nullptr;
+    if ((rc = e.rt->scratch(xpu::gemm_nt_workspace_bound(e.rt), &ws))) return rc;
+  }
+  return XPU_OK;
+}
+
 int setup_prefill(xpu_qwen3 &e) {
   const xpu_qwen3_config &c = e.c;
   const uint32_t qd = c.heads * c.head_dim;
@@ -423,27 +468,8 @@ int setup_prefill(xpu_qwen3 &e) {
   // GEMM form, whose GEMMs and attention fill the chip only with long chunks
   e.pf_chunk = e.pf_ok ? std::min<uint32_t>(e.max_seq, 256) : 0;
   e.pf_chunk_gemm = e.pf_gemm_ok ? std::min<uint32_t>(e.max_seq, 4096) : 0;
-  const uint64_t T = std::max(e.pf_chunk, e.pf_chunk_gemm);
-  const uint64_t sizes[7] = {T * c.hidden, T * c.hidden, T * qkv_rows, T * qd, T * qd, T * c.intermediate,
-                             T * 2 * c.intermediate};
-  uint64_t total = 0;
-  for (uint64_t n : sizes) total += (n * 2 + 255) & ~uint64_t{255};
-  int rc = xpu_rt_alloc(e.rt, total, 4096, &e.pf_block);
-  if (rc) return rc;
-  uint16_t **dst[7] = {&e.pf_x, &e.pf_xn, &e.pf_qkv, &e.pf_q, &e.pf_a, &e.pf_h, &e.pf_gu};
-  uint8_t *p = static_cast<uint8_t *>(e.pf_block);
-  for (int i = 0; i < 7; ++i) {
-    *dst[i] = reinterpret_cast<uint16_t *>(p);
-    p += (sizes[i] * 2 + 255) & ~uint64_t{255};
-  }
   e.batched_prefill = e.pf_ok;  // the default: the bit-identical form; the GEMM form is opt-in
-  if (e.pf_gemm_ok) {
-    // the GEMM form's split-K partials, reserved now rather than grown (with
-    // a stream synchronization) in the middle of a prompt
-    void *ws = nullptr;
-    if ((rc = e.rt->scratch(xpu::gemm_nt_workspace_bound(e.rt), &ws))) return rc;
-  }
-  return XPU_OK;
+  return e.pf_ok ? size_prompt_buffers(e, false) : XPU_OK;
 }
 
 int launch(xpu_qwen3 &e, const xpu_qwen3::Launch &l, uint32_t block, std::initializer_list<xpu_kernel_arg> args) {
@@ -1137,6 +1163,10 @@ extern "C" int xpu_qwen3_set_prefill(xpu_qwen3 *eng, int mode) {
     return set_error(XPU_ERR_INVALID, "batched prefill has no kernels for this model shape");
   if (mode == 2 && !eng->pf_gemm_ok)
     return set_error(XPU_ERR_INVALID, "gemm prefill has no kernels for this model shape");
+  if (mode != 0) {
+    const int rc = size_prompt_buffers(*eng, mode == 2);
+    if (rc) return rc;
+  }
   eng->batched_prefill = mode != 0;
   eng->gemm_prefill = mode == 2;
   return XPU_OK;
