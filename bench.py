@@ -218,6 +218,55 @@ def qwen3_decode(xpu, n_prompt=128, max_seq=256, prefill=None):
         rt.close()
 
 
+def vendor_gemm_comparison(rounds: int = 5, steps: int = 20) -> int:
+    """xpu_gemm against torch.matmul (hipBLASLt on ROCm) on the GEMM shapes,
+    interleaved on one box: per round, 5 warmups then `steps` back-to-back
+    launches of each, on the stream each library launches on (torch's
+    current stream for torch.matmul, the runtime's stream for xpu_gemm);
+    prints the median over rounds. Operands are contiguous row-major."""
+    import torch
+
+    import xpu_playground_amd as xpu
+
+    rt = xpu.Runtime()
+    shapes = [("bf16", 4096, 4096, 4096), ("bf16", 8192, 8192, 8192), ("fp16", 3000, 4097, 2050),
+              ("bf16", 1024, 1024, 4096)]
+    print(f"torch {torch.__version__}, device {torch.cuda.get_device_name(0)}", flush=True)
+    for name, m, n, k in shapes:
+        dt = torch.bfloat16 if name == "bf16" else torch.float16
+        code = xpu.BF16 if name == "bf16" else xpu.FP16
+        g = torch.Generator(device="cuda").manual_seed(1)
+        a = (torch.rand(m, k, device="cuda", generator=g) * 2 - 1).to(dt).contiguous()
+        b = (torch.rand(k, n, device="cuda", generator=g) * 2 - 1).to(dt).contiguous()
+        c = torch.empty(m, n, device="cuda", dtype=dt)
+        t_times, x_times = [], []
+        for _ in range(rounds):
+            for _ in range(5):
+                torch.matmul(a, b, out=c)
+            s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s0.record()
+            for _ in range(steps):
+                torch.matmul(a, b, out=c)
+            s1.record()
+            torch.cuda.synchronize()
+            t_times.append(s0.elapsed_time(s1) / steps)
+            for _ in range(5):
+                rt.gemm(code, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k)
+            e0, e1 = rt.event(), rt.event()
+            e0.record()
+            for _ in range(steps):
+                rt.gemm(code, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k)
+            e1.record()
+            rt.synchronize()
+            x_times.append(e0.elapsed_ms(e1) / steps)
+        flop = 2.0 * m * n * k
+        tm, xm = sorted(t_times)[rounds // 2], sorted(x_times)[rounds // 2]
+        print(f"{name} {m}x{n}x{k}: torch.matmul {tm * 1e3:8.2f} us {flop / tm / 1e9:7.1f} TFLOP/s | "
+              f"xpu_gemm {xm * 1e3:8.2f} us {flop / xm / 1e9:7.1f} TFLOP/s | ratio {tm / xm:.2f}x", flush=True)
+    rt.close()
+    return 0
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -381,9 +430,13 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-workload", action="store_true",
                     help="run one 512 MiB streaming copy and one GEMV launch (for rocprofv3 --pmc)")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="time xpu_gemm against torch.matmul (hipBLASLt) on the GEMM shapes and exit")
     args = ap.parse_args()
     if args.traffic_workload:
         return traffic_workload()
+    if args.vendor_gemm:
+        return vendor_gemm_comparison()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the hot path is "
               "built for a single device (no collectives, no sharded launch)", file=sys.stderr)
