@@ -244,13 +244,18 @@ XPU_DEVICE uint32_t lds_addr(const void *p) {
 // block and the XCD. Records go to a ring per (block, wave) slot, indexed by
 // that slot's own sequence counter: only one wave occupies a slot at a time
 // (launches on a stream do not overlap), so no atomics perturb the timing.
-// xpu_playground_amd/timeline.py reads and groups them. Without XPU_STAMPS
-// the macro is empty.
+// xpu_playground_amd/timeline.py reads and groups them. XPU_PHASE(i)
+// (i < 4) marks a point inside such a kernel: lane 0 of the wave writes the
+// shader clock into a wave-indexed LDS array (no memory traffic), and the
+// exit record of the first kPhaseSlots (block, wave) slots carries each
+// mark as shader-clock ticks since entry (0 where the wave did not pass
+// it). Without XPU_STAMPS both macros are empty.
 #ifdef XPU_STAMPS
 namespace xpu {
 // (block, wave) slots: up to 1024 blocks of 4 waves (the decode GEMVs' grid
-// cap); 2048 records each (a decode token launches 142 kernels)
-constexpr uint32_t kStampSlots = 4096, kStampRing = 2048;
+// cap); 2048 records each (a decode token launches 142 kernels); phase
+// marks for the first 1024 slots
+constexpr uint32_t kStampSlots = 4096, kStampRing = 2048, kPhaseSlots = 1024, kPhases = 4;
 struct StampRecord {
   uint32_t start_lo;     // s_memrealtime at entry, low 32 bits (100 MHz)
   uint32_t real_ticks;   // constant-clock ticks from entry to exit
@@ -260,6 +265,8 @@ struct StampRecord {
 }  // namespace xpu
 extern "C" __device__ uint32_t xpu_stamp_seq[xpu::kStampSlots];
 extern "C" __device__ xpu::StampRecord xpu_stamp_ring[xpu::kStampSlots * xpu::kStampRing];
+extern "C" __device__ uint32_t xpu_stamp_phase[xpu::kPhaseSlots * xpu::kStampRing * xpu::kPhases];
+__shared__ uint32_t xpu_phase_marks[16 * xpu::kPhases];  // [wave][phase], shader clock, low 32 bits
 namespace xpu {
 struct StampGuard {
   uint64_t r0, c0;
@@ -267,6 +274,8 @@ struct StampGuard {
   XPU_DEVICE explicit StampGuard(uint32_t kernel_id) : id(kernel_id) {
     r0 = __builtin_amdgcn_s_memrealtime();
     c0 = __builtin_amdgcn_s_memtime();
+    if ((threadIdx.x & 63u) == 0)
+      for (uint32_t i = 0; i < kPhases; ++i) xpu_phase_marks[(threadIdx.x >> 6) * kPhases + i] = 0;
   }
   XPU_DEVICE ~StampGuard() {
     const uint64_t c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
@@ -283,13 +292,27 @@ struct StampGuard {
     rec.clock_ticks = static_cast<uint32_t>(c1 - c0);
     rec.tag = (id << 24) | (xcc << 20) | ((wave & 15u) << 16) | (blockIdx.x & 0xffffu);
     xpu_stamp_ring[slot * kStampRing + seq % kStampRing] = rec;
+    if (slot < kPhaseSlots)
+      for (uint32_t i = 0; i < kPhases; ++i) {
+        const uint32_t mark = xpu_phase_marks[wave * kPhases + i];
+        xpu_stamp_phase[(slot * kStampRing + seq % kStampRing) * kPhases + i] =
+            mark ? mark - static_cast<uint32_t>(c0) : 0u;
+      }
   }
 };
+XPU_DEVICE void phase_mark(uint32_t i) {
+  const uint32_t t = static_cast<uint32_t>(__builtin_amdgcn_s_memtime());
+  if ((threadIdx.x & 63u) == 0) xpu_phase_marks[(threadIdx.x >> 6) * kPhases + i] = t | 1u;
+}
 }  // namespace xpu
 #define XPU_STAMP(id) const ::xpu::StampGuard xpu_stamp_guard_(id)
+#define XPU_PHASE(i) ::xpu::phase_mark(i)
 #else
 #define XPU_STAMP(id) \
   do {                \
+  } while (0)
+#define XPU_PHASE(i) \
+  do {               \
   } while (0)
 #endif
 

@@ -411,6 +411,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   __syncthreads();
 #pragma unroll
   for (uint32_t r = 0; r < G::kReads; ++r) read(0, 0, frag[0], r);
+  XPU_PHASE(0);  // (stamps build) prologue done: slice 0 published, its first fragments read
 
   // Instruction order is fixed with sched_barrier. Ordinary k-step: each of
   // the first kReads MFMAs is followed by one fragment read of the next
@@ -504,10 +505,12 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
       }
     }
   }
+  XPU_PHASE(1);  // (stamps build) the K loop's last MFMA issued
   // drain the DMA of slices past the end (they read zeros) before the
   // epilogue reuses the LDS
   wait_vmcnt<0>();
   __syncthreads();
+  XPU_PHASE(2);  // (stamps build) the epilogue starts
 
   // Epilogue through LDS, one 64-row band per round (MI / 2 rounds): each wave writes its
   // 64 x kBNW FP32 band (D layout of v_mfma_f32_32x32x16 with C^T tiles: lane

@@ -6,6 +6,7 @@ extern "C" __device__ uint32_t xpu_stamp_seq[xpu::kStampSlots];
 extern "C" __device__ xpu::StampRecord xpu_stamp_ring[xpu::kStampSlots * xpu::kStampRing];
 __device__ uint32_t xpu_stamp_seq[xpu::kStampSlots];
 __device__ xpu::StampRecord xpu_stamp_ring[xpu::kStampSlots * xpu::kStampRing];
+__device__ uint32_t xpu_stamp_phase[xpu::kPhaseSlots * xpu::kStampRing * xpu::kPhases];
 #endif
 #include "gemv.hip"
 #include "synth.hip"

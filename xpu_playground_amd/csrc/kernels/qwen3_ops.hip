@@ -717,6 +717,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
                             wave == 0 ? qs : wave == 1 ? ks : junk + (wave - 2) * xpu::kHeadDim);
   }
   __syncthreads();  // 1: qs, ks
+  XPU_PHASE(0);     // (stamps build) operand loads, QK-norm and RoPE done
   const uint32_t pos = state[0];
   if (pos >= max_seq) return;  // the reference skips the step (kernels.hpp:74-75)
   const uint32_t n = pos + 1;
@@ -751,6 +752,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   const float wmax = xpu::wave_reduce(sc, [](float x, float y) { return fmaxf(x, y); });
   if (lane == 0) red[wave] = wmax;
   __syncthreads();  // 2: wave maxima
+  XPU_PHASE(1);     // (stamps build) scores and their maximum done
   const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   // exponentials; canonical lane L = tid / 8 folds its 8 slots
   const float ex = tid < n ? xpu::canonical_exp(sc - mx) : 0.0f;
@@ -761,6 +763,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   float *lane_sum = red + 4;            // 32 canonical lane sums (n <= 256)
   if ((tid & 7u) == 0) lane_sum[tid >> 3] = f;
   __syncthreads();  // 3: exponentials and lane sums
+  XPU_PHASE(2);     // (stamps build) exponentials and the denominator's lane sums done
   const float total = xpu::wave_butterfly(lane < 32 ? lane_sum[lane] : 0.0f);
   const float inv = 1.0f / total;
   float part[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -958,6 +961,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_pv(
   load_s(0, min(kChunk, n), sv);
   load_tile(0, vv);
   const float mx = xpu::wave_reduce(pm, [](float x, float y) { return fmaxf(x, y); });
+  XPU_PHASE(0);  // (stamps build) the softmax maximum
   auto exps = [&](uint32_t len, const float (&s)[kPer], bool scaled, float sinv) {
 #pragma unroll
     for (int k = 0; k < static_cast<int>(kPer); ++k) {
@@ -993,6 +997,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_pv(
     }
     __syncthreads();
   }
+  XPU_PHASE(1);  // (stamps build) exponentials and the denominator's chunk sums
   float total = 0.0f;
   for (uint32_t c = 0; c < nchunks; ++c) total = total + csum[c];
   const float inv = 1.0f / total;
@@ -1011,6 +1016,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_pv(
     } else {
       exps(len, sv, true, inv);
     }
+    XPU_PHASE(2);  // (stamps build) the (last) chunk's probabilities
     float part = 0.0f;
     for (uint32_t i0 = 0; i0 < len; i0 += kTile) {
       store_tile(i0, vv);  // a region of the chunk's rows that no chain reads yet
@@ -1035,6 +1041,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_pv(
     }
     tot = tot + part;
   }
+  XPU_PHASE(3);  // (stamps build) the V tiles and their chains
   const float pair = tot + xpu::xor16_f(tot);  // (c0 + c1), (c2 + c3)
   const float sum = pair + xpu::xor32_f(pair); // (c0 + c1) + (c2 + c3)
   if (lane < 16) wsum[wave * kDims + lane] = sum;
@@ -1526,6 +1533,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_attention_short(
   const float wmax = xpu::wave_reduce(sc, [](float x, float y) { return fmaxf(x, y); });
   if (lane == 0) red[wave] = wmax;
   __syncthreads();  // 2: wave maxima
+  XPU_PHASE(1);     // (stamps build) scores and their maximum done
   const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float ex = tid < n ? xpu::canonical_exp(sc - mx) : 0.0f;
   sbuf[tid] = ex;
@@ -1535,6 +1543,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_pf_attention_short(
   float *lane_sum = red + 4;            // 32 canonical lane sums
   if ((tid & 7u) == 0) lane_sum[tid >> 3] = f;
   __syncthreads();  // 3: exponentials and lane sums
+  XPU_PHASE(2);     // (stamps build) exponentials and the denominator's lane sums done
   const float total = xpu::wave_butterfly(lane < 32 ? lane_sum[lane] : 0.0f);
   const float inv = 1.0f / total;
   float part[8] = {0, 0, 0, 0, 0, 0, 0, 0};

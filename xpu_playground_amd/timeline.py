@@ -9,6 +9,13 @@ groups them into launches, so graph-mode decode (where rocprofv3's kernel
 trace is not available here) gets per-kernel durations, the gaps between
 dependent launches, and the shader clock of each XCD.
 
+Phase marks: the GEMM body, the short-context attention and the long-context
+P.V kernel also mark up to four points of their own (XPU_PHASE in the
+sources), recorded for the first 1024 (block, wave) slots as shader-clock
+ticks since the wave's entry. PHASES names them; `phases` in the output gives,
+per kernel, the median ticks of each segment between consecutive marks (and
+from the last mark to the wave's exit) over the waves that passed the marks.
+
     python -m xpu_playground_amd.timeline gemm --size 4096 --type bf16
     python -m xpu_playground_amd.timeline decode --prompt 128 --new 12
 
@@ -34,6 +41,16 @@ TICK_NS = 10.0  # s_memrealtime: 100 MHz
 RECORD = np.dtype([("start_lo", "<u4"), ("real_ticks", "<u4"), ("clock_ticks", "<u4"), ("tag", "<u4")])
 KERNELS = {1: "gemv", 2: "gemm", 10: "qkv", 11: "attention", 12: "attn_scores", 13: "attn_pv", 14: "residual",
            15: "gate_up", 16: "logits", 17: "finish"}
+PHASE_COUNT = 4
+# segment names, one per mark and one for the rest of the wave after the last
+PHASES = {
+    "gemm": ["prologue (slice 0 staged, first fragments read)", "K loop (to the last MFMA issued)",
+             "DMA drain and barrier", "epilogue (C through LDS to HBM)"],
+    "attention": ["operand loads, QK-norm, RoPE", "scores and their maximum",
+                  "exponentials and lane sums", "denominator, P.V chains, combine, store"],
+    "attn_pv": ["softmax maximum (score and V loads issued)", "exponentials and denominator",
+                "probabilities", "V tiles and their chains", "combine and store"],
+}
 
 
 class Stamps:
@@ -43,8 +60,10 @@ class Stamps:
         self.rt = rt
         self.seq_ptr, self.seq_bytes = self._global(b"xpu_stamp_seq")
         self.ring_ptr, self.ring_bytes = self._global(b"xpu_stamp_ring")
+        self.phase_ptr, self.phase_bytes = self._global(b"xpu_stamp_phase")
         self.slots = self.seq_bytes // 4
         self.ring = self.ring_bytes // RECORD.itemsize // self.slots
+        self.phase_slots = self.phase_bytes // 4 // PHASE_COUNT // self.ring
 
     def _global(self, name):
         p, n = ctypes.c_void_p(), ctypes.c_uint64()
@@ -65,13 +84,21 @@ class Stamps:
         raw = self.rt.download(self.ring_ptr, self.ring_bytes, np.uint8).view(RECORD).reshape(self.slots, self.ring)
         keep = np.arange(self.ring)[None, :] < seq[:, None]
         recs = raw[keep]
+        slot, pos = np.nonzero(keep)
+        marks = self.rt.download(self.phase_ptr, self.phase_bytes // 4, np.uint32).reshape(
+            self.phase_slots, self.ring, PHASE_COUNT)
+        phases = np.zeros((slot.size, PHASE_COUNT), np.uint32)
+        lo_slot = slot < self.phase_slots
+        phases[lo_slot] = marks[slot[lo_slot], pos[lo_slot]]
         # entry times from the low 32 bits (43 s period) relative to the
         # earliest, across at most one wrap
         lo = recs["start_lo"].astype(np.int64)
         if lo.size and lo.max() - lo.min() > (1 << 31):
             lo = np.where(lo < (1 << 31), lo + (1 << 32), lo)
         out = np.zeros(lo.size, dtype=[("real_start", "<i8"), ("real_ticks", "<u4"), ("clock_ticks", "<u4"),
-                                       ("kernel", "<u4"), ("xcc", "<u4"), ("block", "<u4")])
+                                       ("kernel", "<u4"), ("xcc", "<u4"), ("block", "<u4"),
+                                       ("phases", "<u4", (PHASE_COUNT,))])
+        out["phases"] = phases
         out["real_start"] = lo - (lo.min() if lo.size else 0)
         out["real_ticks"], out["clock_ticks"] = recs["real_ticks"], recs["clock_ticks"]
         out["kernel"] = recs["tag"] >> 24
@@ -87,7 +114,7 @@ def launches(recs: np.ndarray) -> list[dict]:
         start, end = int(r["real_start"]), int(r["real_start"]) + int(r["real_ticks"])
         if cur is None or r["kernel"] != cur["kernel"] or start >= cur["end"]:
             cur = {"kernel": int(r["kernel"]), "start": start, "end": end, "waves": 0, "clock": defaultdict(list),
-                   "residency": [], "block_end": {}}
+                   "residency": [], "block_end": {}, "marks": []}
             out.append(cur)
         cur["end"] = max(cur["end"], end)
         b = int(r["block"])
@@ -96,6 +123,8 @@ def launches(recs: np.ndarray) -> list[dict]:
         if r["real_ticks"]:
             cur["clock"][int(r["xcc"])].append(r["clock_ticks"] / (r["real_ticks"] * TICK_NS))
         cur["residency"].append(int(r["clock_ticks"]))
+        if r["phases"].any():
+            cur["marks"].append([int(x) for x in r["phases"]] + [int(r["clock_ticks"])])
     for i, ln in enumerate(out):
         ln["name"] = KERNELS.get(ln["kernel"], str(ln["kernel"]))
         if ln["name"] == "residual":  # o_proj follows the attention, down_proj the gate/up kernel
@@ -106,6 +135,29 @@ def launches(recs: np.ndarray) -> list[dict]:
         ln["max_wave_cycles"] = max(ln["residency"])
         ln["median_wave_cycles"] = float(np.median(ln["residency"]))
     return out
+
+
+def phase_segments(marks: list[list[int]]) -> list[float] | None:
+    """Median shader-clock ticks of each segment, over the waves that passed
+    every mark the kernel's waves pass (marks of 0 are marks not passed):
+    entry to the first mark, mark to mark, the last mark to the exit."""
+    if not marks:
+        return None
+    m = np.asarray(marks, np.int64)
+    used = [i for i in range(PHASE_COUNT) if m[:, i].any()]
+    m = m[np.all(m[:, used] > 0, axis=1)][:, used + [PHASE_COUNT]]
+    if not m.size:
+        return None
+    seg = np.diff(np.concatenate([np.zeros((m.shape[0], 1), np.int64), m], axis=1), axis=1)
+    return [round(float(v), 0) for v in np.median(seg, axis=0)]
+
+
+def phase_table(name: str, marks: list[list[int]]) -> dict | None:
+    seg = phase_segments(marks)
+    if seg is None:
+        return None
+    labels = PHASES.get(name, [f"segment {i}" for i in range(len(seg))])
+    return {"waves": len(marks), "median_cycles": dict(zip(labels, seg))}
 
 
 def summarize(lns: list[dict]) -> dict:
@@ -125,6 +177,9 @@ def summarize(lns: list[dict]) -> dict:
             "shader_ghz_min_med_max": [round(min(clocks), 3), round(float(np.median(clocks)), 3),
                                        round(max(clocks), 3)] if clocks else None,
         }
+        phases = phase_table(name, [mk for g in group for mk in g["marks"]])
+        if phases:
+            table[name]["phases"] = phases
     return table
 
 
@@ -145,7 +200,7 @@ def run_gemm(args) -> dict:
     per = [{"us": round(ln["us"], 2), "tflops": round(flop / (ln["us"] * 1e-6) / 1e12, 1),
             "ghz_by_xcc": {x: round(v, 3) for x, v in ln["ghz_by_xcc"].items()},
             "median_wave_cycles": ln["median_wave_cycles"], "max_wave_cycles": ln["max_wave_cycles"],
-            "gap_us": round(ln["gap_us"], 2)} for ln in lns]
+            "gap_us": round(ln["gap_us"], 2), "phases": phase_table("gemm", ln["marks"])} for ln in lns]
     rt.close()
     return {"workload": f"gemm {args.type} {m}x{n}x{k}", "launches": per}
 
