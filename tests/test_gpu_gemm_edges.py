@@ -22,7 +22,8 @@ from xpu_playground_amd import Args
 pytestmark = pytest.mark.gpu
 
 GUARD = 0x7E7E
-TILES = {"": (256, 256), "_odd": (256, 256), "_m128": (128, 256), "_t128": (128, 128)}
+TILES = {"": (256, 256), "_odd": (256, 256), "_m224": (224, 256), "_m224_odd": (224, 256), "_m128": (128, 256),
+         "_t128": (128, 128)}
 
 
 @pytest.mark.parametrize("dtype", [xpu.BF16, xpu.FP16])
@@ -71,7 +72,7 @@ def launch_tile(rt, tag, dtype, a, b, m, n, k, offsets):
                                            (64, 40, 9, (2, 2, 2)), (257, 255, 1087, (0, 2, 6))])
 def test_each_tile_in_place(rt, tag, dtype, m, n, k, offsets):
     slices = (k + 63) // 64
-    if tag == "_odd" and (slices % 2 == 0 or slices < 3):
+    if tag.endswith("_odd") and (slices % 2 == 0 or slices < 3):
         pytest.skip("the odd form takes an odd slice count of 3 or more")
     a = orc.uniform(m * k, 80 + m, dtype)
     b = orc.uniform(k * n, 90 + n, dtype)

@@ -1,5 +1,6 @@
-"""The GEMM's block tiles (256x256, also in its odd-slice-count form;
-128x256, the reference's small tile of gemm_kernel.hpp:26-27; 128x128)
+"""The GEMM's block tiles (256x256 and 224x256, also in their
+odd-slice-count forms; 128x256, the reference's small tile of
+gemm_kernel.hpp:26-27; 128x128)
 launched by name on the same shapes, each against the FP64 oracle at the GEMM
 bar, with 16-byte and 2-byte-offset C; and the tile xpu_gemm picks
 (gemm.cpp:145's choice, made here by compute-unit fill)."""
@@ -13,10 +14,11 @@ from xpu_playground_amd import Args
 
 pytestmark = pytest.mark.gpu
 
-# "_odd": the 256x256 kernel for an odd number (3 or more) of 64-deep
-# K-slices (the last slice on its own after the pairs, only its k-steps below
-# K); launched only on such K, as xpu_gemm does
-TILES = {"": (256, 256), "_odd": (256, 256), "_m128": (128, 256), "_t128": (128, 128)}
+# "_odd": the 256x256 and 224x256 kernels for an odd number (3 or more) of
+# 64-deep K-slices (the last slice on its own after the pairs, only its
+# k-steps below K); launched only on such K, as xpu_gemm does
+TILES = {"": (256, 256), "_odd": (256, 256), "_m224": (224, 256), "_m224_odd": (224, 256), "_m128": (128, 256),
+         "_t128": (128, 128)}
 
 
 def slices(k):
@@ -55,7 +57,7 @@ def launch_tile(rt, tag, dtype, a, b, m, n, k, c_offset):
 @pytest.mark.parametrize("m,n,k", [(128, 128, 64), (255, 264, 72), (37, 56, 8), (300, 8, 16), (513, 392, 1032),
                                    (1000, 600, 520), (255, 264, 136), (300, 8, 184), (64, 520, 1056)])
 def test_tile_variant(rt, tag, dtype, c_offset, m, n, k):
-    if tag == "_odd" and (slices(k) % 2 == 0 or slices(k) < 3):
+    if tag.endswith("_odd") and (slices(k) % 2 == 0 or slices(k) < 3):
         pytest.skip("the odd form takes an odd slice count of 3 or more")
     a = orc.uniform(m * k, 50 + m, dtype)
     b = orc.uniform(k * n, 60 + n, dtype)
@@ -63,8 +65,8 @@ def test_tile_variant(rt, tag, dtype, c_offset, m, n, k):
 
 
 def test_tiles_same_bits(rt):
-    # every tile runs the same k-order in each MFMA chain, so all three give
-    # the same output bits
+    # every tile runs the same k-order in each MFMA chain, so all of them
+    # give the same output bits
     m, n, k = 700, 520, 1064  # 17 slices, 3 live k-steps in the last
     a = orc.uniform(m * k, 71, xpu.BF16)
     b = orc.uniform(k * n, 72, xpu.BF16)
@@ -75,11 +77,13 @@ def test_tiles_same_bits(rt):
 def test_tile_choice(rt):
     if rt.compute_units != 256:
         pytest.skip("the expected choices are for MI355X's 256 compute units")
-    # configs[2] and configs[3] keep the large tile (it already gives every
-    # compute unit at most one block); outputs that leave most units idle
-    # with it take a small one
+    # configs[2] keeps the large tile (it gives every compute unit one
+    # block); configs[3] takes 224 x 256 (238 blocks of 7/8 the work instead
+    # of 204); outputs that leave most units idle take a small one
     assert rt.gemm_tile(4096, 4096) == (256, 256)
-    assert rt.gemm_tile(3000, 4097) == (256, 256)
+    assert rt.gemm_tile(3000, 4097) == (224, 256)
+    assert rt.gemm_tile(3072, 3072) == (224, 256)
+    assert rt.gemm_tile(6144, 6144) == (224, 256)  # three blocks per unit with either large tile
     assert rt.gemm_tile(8192, 8192) == (256, 256)
     assert rt.gemm_tile(2048, 4096) == (128, 256)
     assert rt.gemm_tile(1000, 4097) == (128, 256)

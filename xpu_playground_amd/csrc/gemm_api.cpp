@@ -16,32 +16,39 @@ namespace {
 uint64_t round_up8(uint64_t v) { return (v + 7) & ~uint64_t{7}; }
 
 // Block tiles of the MFMA kernels (kernels/gemm.hip), largest first. Rates
-// are FLOP per compute unit relative to the large tile, measured at shapes
-// where every compute unit is busy: a 128 x 256 block alone on a unit runs at
+// are FLOP per compute unit relative to the large tile, measured with one
+// block per busy compute unit: a 224 x 256 block runs at 0.89-0.97 (median
+// 0.93 over six shapes; its four wavefronts each read all 224 A rows, and
+// its B rows cost as much as in the 256 x 256 block); a 128 x 256 block at
 // 0.85; a 128 x 128 block alone at 0.59, and two of them sharing a unit (its
 // LDS holds two) at 0.82 together.
 struct GemmTile {
-  const char *tag;  // kernel name part: xpu_gemm_<type><tag>_dma[u]
+  const char *tag;  // kernel name part: xpu_gemm_<type><tag>[_odd]_dma[u][_edge]
   uint32_t rows, cols;
   uint32_t per_cu;   // blocks one compute unit holds at once
   double solo_rate;  // one block on a unit
   double pair_rate;  // two blocks on a unit, together (per_cu == 2)
+  bool odd_forms;    // has _odd kernels (an odd count, 3 or more, of 64-deep K-slices)
+  bool nt_forms;     // has [n][k] (_nt) kernels for the prompt projections
 };
-constexpr GemmTile kTiles[] = {{"", 256, 256, 1, 1.0, 0.0},
-                               {"_m128", 128, 256, 1, 0.85, 0.0},
-                               {"_t128", 128, 128, 2, 0.59, 0.82}};
+constexpr GemmTile kTiles[] = {{"", 256, 256, 1, 1.0, 0.0, true, true},
+                               {"_m224", 224, 256, 1, 0.93, 0.0, true, false},
+                               {"_m128", 128, 256, 1, 0.85, 0.0, false, true},
+                               {"_t128", 128, 128, 2, 0.59, 0.82, false, true}};
 
 // The tile with the least estimated time. The blocks spread evenly over the
 // compute units, so the busiest unit gets w = ceil(tiles / CUs) of them and
 // runs them in pairs where it holds two. The larger tile wins ties. The
 // reference takes its small tile when M or N is below 2560 (gemm.cpp:145);
-// here the 256 x 256 tile stays wherever it already fills the chip (4096^3,
-// 3000 x 4097), and outputs that leave most compute units idle with it take
-// a smaller one.
-const GemmTile &choose_tile(uint32_t compute_units, uint32_t M, uint32_t n_cols) {
+// here the 256 x 256 tile stays where it gives each compute unit one block
+// (4096^3), 224 x 256 takes outputs where it still does and cuts each unit's
+// work by 1/8 (3000 x 4097: 238 blocks instead of 204), and outputs that
+// leave most compute units idle take a smaller one.
+const GemmTile &choose_tile(uint32_t compute_units, uint32_t M, uint32_t n_cols, bool nt = false) {
   const GemmTile *best = &kTiles[0];
   double best_cost = 0;
   for (const GemmTile &t : kTiles) {
+    if (nt && !t.nt_forms) continue;
     const uint64_t tiles = ((static_cast<uint64_t>(M) + t.rows - 1) / t.rows) *
                            ((static_cast<uint64_t>(n_cols) + t.cols - 1) / t.cols);
     const uint64_t w = (tiles + compute_units - 1) / std::max(1u, compute_units);
@@ -130,11 +137,11 @@ int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, 
       }
     }
   }
-  // the 256 x 256 kernels come in a form for an odd number (3 or more) of
-  // 64-deep K-slices, which skips the slice of zeros that closes the last
-  // pair and the last slice's k-steps past K
+  // the 256 x 256 and 224 x 256 kernels come in a form for an odd number (3
+  // or more) of 64-deep K-slices, which skips the slice of zeros that closes
+  // the last pair and the last slice's k-steps past K
   const uint32_t slices = (k_run + 63) / 64;
-  const bool odd = tile.tag[0] == '\0' && slices % 2 == 1 && slices >= 3;
+  const bool odd = tile.odd_forms && slices % 2 == 1 && slices >= 3;
   const std::string name = std::string("xpu_gemm_") + dt + tile.tag + (odd ? "_odd" : "") +
                            (c16 ? "_dma" : "_dmau") + (edge ? "_edge" : "");
   const xpu::KernelInfo *k = rt->find_exact(name);
@@ -168,7 +175,7 @@ int gemm_nt(xpu_runtime *rt, const void *A, const void *W, void *C, uint32_t M, 
                                       "operands");
   if (static_cast<uint64_t>(K) * 256 * 2 >= (1ull << 31) || static_cast<uint64_t>(N) >= (1u << 24))
     return set_error(XPU_ERR_INVALID, "gemm_nt: K must be below 4M and N below 16M");
-  const GemmTile &tile = choose_tile(rt->compute_units, M, N);
+  const GemmTile &tile = choose_tile(rt->compute_units, M, N, true);
   const uint32_t slices = (K + 63) / 64;
   const bool odd = tile.tag[0] == '\0' && slices % 2 == 1 && slices >= 3;
   auto count = [&](uint32_t rows, uint32_t cols) {

@@ -9,7 +9,12 @@
 // 256 x 256 (MI = NJ = 4, 256 FP32 accumulators per lane). The small tiles,
 // 128 x 256 (the reference's small tile, gemm_kernel.hpp:26-27) and
 // 128 x 128, cut shapes that fill few compute units with the large tile
-// into more blocks; the host picks the tile by compute-unit fill.
+// into more blocks. The 224 x 256 tile puts the four wavefronts side by
+// side along N (1 x 4, MI = 7, NJ = 2): outputs whose 256 x 256 tiles leave
+// compute units idle but whose 224-row tiles still fit one per unit
+// (3000 x 4097: 204 of 256 units busy with 256 x 256, 238 with 224 x 256)
+// run 7/8 of the work per unit. The host picks the tile by compute-unit
+// fill.
 //
 // Operands go from global memory straight into LDS with buffer_load_dwordx4
 // ... lds (the LDS-DMA form: lane t's 16 bytes land at M0 + 16 t), so no
@@ -124,12 +129,15 @@ template <int DT> XPU_DEVICE uint32_t cvt_pack(float lo, float hi) {
 }
 
 // MI, NJ: 32 x 32 MFMA tiles per wavefront along M and N (wavefront tile
-// 32 MI x 32 NJ, block tile 64 MI x 64 NJ); BK: K-slice; S: LDS stages.
-template <int MI, int NJ, int BK, int S, bool BT = false> struct Cfg {
+// 32 MI x 32 NJ); WN: wavefronts along N (2: a 2 x 2 arrangement, block tile
+// 64 MI x 64 NJ; 4: 1 x 4, block tile 32 MI x 128 NJ); BK: K-slice; S: LDS
+// stages.
+template <int MI, int NJ, int BK, int S, bool BT = false, int WN = 2> struct Cfg {
+  static_assert(WN == 2 || WN == 4, "2 x 2 or 1 x 4 wavefronts");
   static constexpr uint32_t kBMW = 32u * MI;                 // rows per wavefront
-  static constexpr uint32_t kBM = 2u * kBMW;                 // block tile rows
+  static constexpr uint32_t kBM = (4u / WN) * kBMW;          // block tile rows
   static constexpr uint32_t kBNW = 32u * NJ;                 // columns per wavefront
-  static constexpr uint32_t kBN = 2u * kBNW;                 // block tile columns
+  static constexpr uint32_t kBN = WN * kBNW;                 // block tile columns
   static constexpr uint32_t kKs = BK / 16;                   // k-steps per slice
   static constexpr uint32_t kABytes = kBM * 2u * BK;         // kBM rows x 2 BK bytes
   static constexpr uint32_t kBRow = 2u * kBN;                // bytes per B row in LDS
@@ -150,8 +158,7 @@ template <int MI, int NJ, int BK, int S, bool BT = false> struct Cfg {
   static constexpr uint32_t kLds = S * kStage > kEpBytes ? S * kStage : kEpBytes;
   static_assert(kLds <= 160u * 1024u, "LDS");
   static_assert(BT || kBCpr == 16 || kBCpr == 32, "[k][n] B rows of 16 or 32 chunks (the swizzle permutes 16)");
-  static_assert(MI == 2 || MI == 4, "64-row epilogue bands");
-  static_assert(kDmaA >= 1, "every wave issues A DMA");
+  static_assert(kBM % (4u * kRpi) == 0 && kDmaA >= 1, "every wave issues the same A DMA, at least one");
 };
 
 // ODD: the slice count nk is odd and at least 3 (the host's choice; other
@@ -168,10 +175,10 @@ template <int MI, int NJ, int BK, int S, bool BT = false> struct Cfg {
 // C)[split][M][ldc] (ldc >= N, a multiple of 4: whole 16-byte groups of
 // columns are stored); xpu_gemm_splitk_reduce[_any] adds the splits.
 template <int DT, int MI, int NJ, int BK, int S, int P, int D, bool C16, bool ODD, bool BT = false,
-          bool RES = false, bool PART = false, bool EDGE = false>
+          bool RES = false, bool PART = false, bool EDGE = false, int WN = 2>
 XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
                      uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {
-  using G = Cfg<MI, NJ, BK, S, BT>;
+  using G = Cfg<MI, NJ, BK, S, BT, WN>;
   const uint32_t K_ = K, M_ = M, N_ = N;  // for fix_tail, which shadows them
   static_assert(!RES || C16, "the residual epilogue stores 16-byte chunks");
   static_assert(!PART || (!RES && !ODD), "split K: the reduction applies any residual");
@@ -237,7 +244,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   // logical chunk 2 ks + l/32. B: k-row 16 ks + 8 (l/32) + 4 h + (l%16)/4,
   // column wn*kBNW + 32 j + 16 ((l/16) % 2) + 4 (l % 4): the 4-element row
   // that lane l contributes to its group's transposing read.
-  const uint32_t wm = wave >> 1, wn = wave & 1u;
+  const uint32_t wm = wave / WN, wn = wave % WN;
   // The ds_read offset field holds 16 bits, so the stages are addressed from
   // one base per 64 KiB group; the bases are made opaque to the compiler so
   // that it keeps them in registers instead of materialising one register per
@@ -512,7 +519,8 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   __syncthreads();
   XPU_PHASE(2);  // (stamps build) the epilogue starts
 
-  // Epilogue through LDS, one 64-row band per round (MI / 2 rounds): each wave writes its
+  // Epilogue through LDS, one 64-row band per round ((MI + 1) / 2 rounds; with
+  // MI odd the last band has 32 rows): each wave writes its
   // 64 x kBNW FP32 band (D layout of v_mfma_f32_32x32x16 with C^T tiles: lane
   // l holds row l % 32, columns 8 g + 4 (l / 32) + 0..3 in accumulators
   // 4 g..4 g + 3) as 16-byte rows into its own region (pitch kBNW + 4
@@ -543,7 +551,8 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
   const uint32_t m_lane = lane & 31u, n_lane = (lane >> 5) * 4u;
   const uint32_t r_lane = lane / kLpr, c_lane = (lane % kLpr) * 8u;
 #pragma unroll
-  for (int band = 0; band < MI / 2; ++band) {
+  for (int band = 0; band < (MI + 1) / 2; ++band) {
+    const uint32_t band_rows = 2 * band + 1 < MI ? 64u : 32u;
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
@@ -551,6 +560,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int i = band * 2 + ii;
+          if (i >= MI) continue;
           *reinterpret_cast<f32x4 *>(ep + (ii * 32u + m_lane) * kEpPitch + j * 32u + 8u * g + n_lane) =
               f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
         }
@@ -560,11 +570,14 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     // Rows of the band in batches of kBatch read-back rows: every LDS read of
     // a batch is issued before the first conversion. Bands inside M x n_out
     // skip the per-row bounds checks.
-    constexpr uint32_t kIter = 64u / kRpr, kBatch = 4;
+    constexpr uint32_t kBatch = 4;
+    static_assert((64u / kRpr) % kBatch == 0 && (MI % 2 == 0 || (32u / kRpr) % kBatch == 0),
+                  "whole batches in every band");
+    const uint32_t iters = band_rows / kRpr;
     const uint32_t mb = m0 + wm * G::kBMW + band * 64u, nb0 = n0 + wn * G::kBNW;
-    const bool inside = mb + 64u <= M && nb0 + G::kBNW <= n_out;
+    const bool inside = mb + band_rows <= M && nb0 + G::kBNW <= n_out;
 #pragma unroll
-    for (uint32_t rr0 = 0; rr0 < kIter; rr0 += kBatch) {
+    for (uint32_t rr0 = 0; rr0 < iters; rr0 += kBatch) {
       f32x4 lo[kBatch], hi[kBatch];
 #pragma unroll
       for (uint32_t b = 0; b < kBatch; ++b) {
@@ -603,7 +616,7 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
       // band by the wave whose columns hold it: lane = row of the band.
       const uint32_t nb = n0 + wn * G::kBNW, edge = n_out & ~7u, cnt = n_out & 7u;
       const uint32_t m = m0 + wm * G::kBMW + band * 64u + lane;
-      if (cnt != 0 && edge >= nb && edge < nb + G::kBNW && m < M) {
+      if (cnt != 0 && edge >= nb && edge < nb + G::kBNW && lane < band_rows && m < M) {
         const float *src = ep + lane * kEpPitch + (edge - nb);
         uint16_t *dst = C + static_cast<uint64_t>(m) * ldc + edge;
 #pragma unroll
@@ -622,17 +635,21 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
 
 // Each [k][n] kernel also comes in an _edge form (EDGE: the last slice's
 // fix-up for K % 8 != 0 or odd N), so that aligned shapes run code without it.
-#define XPU_GEMM_DMA_VARIANT1(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD, EDGE)                          \
+#define XPU_GEMM_DMA_VARIANT1(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD, EDGE, WN)                      \
   extern "C" __global__ __launch_bounds__(256, MINB) void NAME(                                             \
       const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, uint16_t *__restrict__ C,               \
       uint32_t M, uint32_t N, uint32_t K, uint32_t kb, uint32_t ldc, uint32_t n_out) {                       \
     XPU_STAMP(xpu::kStampGemm);                                                                               \
-    xpu::dma::body<DT, MI, NJ, BK, S, P, D, C16, ODD, false, false, false, EDGE>(A, B, C, M, N, K, kb, ldc,  \
-                                                                                  n_out);                    \
+    xpu::dma::body<DT, MI, NJ, BK, S, P, D, C16, ODD, false, false, false, EDGE, WN>(A, B, C, M, N, K, kb,   \
+                                                                                      ldc, n_out);           \
   }
-#define XPU_GEMM_DMA_VARIANT(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD) \
-  XPU_GEMM_DMA_VARIANT1(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD, false) \
-  XPU_GEMM_DMA_VARIANT1(NAME##_edge, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD, true)
+#define XPU_GEMM_DMA_VARIANT(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD)        \
+  XPU_GEMM_DMA_VARIANT1(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD, false, 2) \
+  XPU_GEMM_DMA_VARIANT1(NAME##_edge, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD, true, 2)
+// 1 x 4 wavefronts
+#define XPU_GEMM_DMA_VARIANT_W4(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD)     \
+  XPU_GEMM_DMA_VARIANT1(NAME, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD, false, 4) \
+  XPU_GEMM_DMA_VARIANT1(NAME##_edge, DT, MI, NJ, BK, S, P, D, MINB, C16, ODD, true, 4)
 
 // C = A W^T with W given [N][K] (BT) for the batched prompt projections, bf16,
 // 16-byte aligned C; _res adds into C (residual)
@@ -842,6 +859,16 @@ XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_m128_dma, xpu::kBf16, 2, 4, 64, 2, 4, 2, 1, t
 XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_m128_dma, xpu::kFp16, 2, 4, 64, 2, 4, 2, 1, true, false)
 XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_m128_dmau, xpu::kBf16, 2, 4, 64, 2, 4, 2, 1, false, false)
 XPU_GEMM_DMA_VARIANT(xpu_gemm_fp16_m128_dmau, xpu::kFp16, 2, 4, 64, 2, 4, 2, 1, false, false)
+
+// 224 x 256 (1 x 4 wavefronts of 224 x 64), with odd-slice forms as the 256 x 256 tile
+XPU_GEMM_DMA_VARIANT_W4(xpu_gemm_bf16_m224_dma, xpu::kBf16, 7, 2, 64, 2, 4, 2, 1, true, false)
+XPU_GEMM_DMA_VARIANT_W4(xpu_gemm_fp16_m224_dma, xpu::kFp16, 7, 2, 64, 2, 4, 2, 1, true, false)
+XPU_GEMM_DMA_VARIANT_W4(xpu_gemm_bf16_m224_dmau, xpu::kBf16, 7, 2, 64, 2, 4, 2, 1, false, false)
+XPU_GEMM_DMA_VARIANT_W4(xpu_gemm_fp16_m224_dmau, xpu::kFp16, 7, 2, 64, 2, 4, 2, 1, false, false)
+XPU_GEMM_DMA_VARIANT_W4(xpu_gemm_bf16_m224_odd_dma, xpu::kBf16, 7, 2, 64, 2, 4, 2, 1, true, true)
+XPU_GEMM_DMA_VARIANT_W4(xpu_gemm_fp16_m224_odd_dma, xpu::kFp16, 7, 2, 64, 2, 4, 2, 1, true, true)
+XPU_GEMM_DMA_VARIANT_W4(xpu_gemm_bf16_m224_odd_dmau, xpu::kBf16, 7, 2, 64, 2, 4, 2, 1, false, true)
+XPU_GEMM_DMA_VARIANT_W4(xpu_gemm_fp16_m224_odd_dmau, xpu::kFp16, 7, 2, 64, 2, 4, 2, 1, false, true)
 // 128 x 128 (two blocks per compute unit: 64 KiB of stages, 68 KiB of
 // epilogue staging); the barrier after 2 of the k-step's 4 MFMAs
 XPU_GEMM_DMA_VARIANT(xpu_gemm_bf16_t128_dma, xpu::kBf16, 2, 2, 64, 2, 2, 2, 2, true, false)
