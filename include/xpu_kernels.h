@@ -36,8 +36,8 @@ int xpu_gemv(xpu_runtime *rt, int dtype, const void *A, const void *x, void *y,
 /* C[M x N] = A[M x K] . B[K x N], row-major, FP32 accumulation on MFMA.
  * Replaces gemm::Kernel<T, Large> (gemm_kernel.hpp:25-143) launched by
  * gemm.cpp:98-101 / peak_l0.cpp:929-934, and the choice between its large
- * and small tile (gemm.cpp:145): the block tile (256x256, 128x256 or
- * 128x128) is the one with the least estimated time at this shape on this
+ * and small tile (gemm.cpp:145): the block tile (256x256, 224x256, 128x256
+ * or 128x128) is the one with the least estimated time at this shape on this
  * GPU's compute units (xpu_gemm_tile). Any M, N, K and 2-byte aligned
  * pointers: the operands are read in place (the reference pads them on the
  * host, gemm.cpp:75-85). Outputs that leave most compute units idle even

@@ -44,11 +44,11 @@ template <typename T> T arg_value(const xpu_kernel_arg *args, uint32_t index) {
   return *static_cast<const T *>(args[index].value);
 }
 
-// The GEMM launch behind xpu_gemm and xpu_gemm_noalloc: operands whose rows
-// are not 16-byte aligned are first copied, zero-padded to a multiple of 8
-// columns, into a workspace: the runtime's grow-only one when
-// fixed_workspace is null, else fixed_workspace (fixed_capacity bytes; a
-// larger need fails with XPU_ERR_INVALID before any launch).
+// The GEMM launch behind xpu_gemm and xpu_gemm_noalloc: A and B are read in
+// place; where K is split, the FP32 partials go to a workspace: the
+// runtime's grow-only one when fixed_workspace is null, else
+// fixed_workspace (fixed_capacity bytes; a larger need fails with
+// XPU_ERR_INVALID before any launch).
 int gemm_run(xpu_runtime *rt, int dtype, const void *A, const void *B, void *C, uint32_t M, uint32_t N, uint32_t K,
              void *fixed_workspace, uint64_t fixed_capacity);
 
