@@ -94,7 +94,7 @@ def test_tile_choice(rt):
 
 @pytest.mark.parametrize("m,n,k", [(1024, 1024, 1024), (2048, 4096, 256), (1000, 4097, 520), (777, 1001, 300)])
 def test_small_tile_shapes_through_xpu_gemm(rt, m, n, k):
-    # aligned operands read in place, and padded copies with unaligned C
+    # operands read in place, aligned and ragged (unaligned C rows with N % 8 != 0)
     print(f"xpu_gemm {m}x{n}x{k} tile {rt.gemm_tile(m, n)}", flush=True)
     a = orc.uniform(m * k, 80 + m, xpu.BF16)
     b = orc.uniform(k * n, 90 + n, xpu.BF16)
