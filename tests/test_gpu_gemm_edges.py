@@ -106,6 +106,26 @@ def test_values_past_k_do_not_leak_and_cut_elements_are_restored(rt, dtype, m, n
     assert not np.any(np.isfinite(orc.decode(c[1::2], dtype)))
 
 
+def tile_shapes(count, seed):
+    """Seeded shapes for which the 224 x 256 tile is a candidate: M and N
+    of a few thousand, any K, ragged and aligned, with operand offsets."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 3600)), int(rng.integers(1, 4300)), int(rng.integers(1, 700)),
+             tuple(int(x) for x in rng.choice([0, 2, 4, 6, 8, 10, 12, 14], 3))) for _ in range(count)]
+
+
+@pytest.mark.parametrize("m,n,k,offsets", tile_shapes(12, 224))
+def test_224_tile_equals_256_tile(rt, m, n, k, offsets):
+    # the two wavefront arrangements run the same k-order in every MFMA
+    # chain, so their outputs are the same bits (and stay inside C)
+    dtype = xpu.FP16 if (m + n + k) % 2 else xpu.BF16
+    odd = "_odd" if (k + 63) // 64 % 2 == 1 and (k + 63) // 64 >= 3 else ""
+    a = orc.uniform(m * k, 3 * m + 1, dtype)
+    b = orc.uniform(k * n, 5 * n + 2, dtype)
+    big = launch_tile(rt, odd, dtype, a, b, m, n, k, offsets)
+    assert np.array_equal(launch_tile(rt, "_m224" + odd, dtype, a, b, m, n, k, offsets), big)
+
+
 def test_ragged_baseline_shape_reads_operands_in_place(rt):
     # configs[3] (fp16 3000 x 4097 x 2050) with A and B at 2-byte offsets,
     # all 12.3 M outputs against FP64
@@ -113,7 +133,9 @@ def test_ragged_baseline_shape_reads_operands_in_place(rt):
     a = orc.uniform(m * k, 7, xpu.FP16)
     b = orc.uniform(k * n, 8, xpu.FP16)
     out = launch_tile(rt, "_odd", xpu.FP16, a, b, m, n, k, (2, 2, 2))
-    print("rel-L2", check(out, a, b, m, n, k, xpu.FP16))
+    print("rel-L2", check(out, a, b, m, n, k, xpu.FP16), flush=True)
+    # the 224 x 256 tile (the one xpu_gemm picks here): the same bits
+    assert np.array_equal(launch_tile(rt, "_m224_odd", xpu.FP16, a, b, m, n, k, (2, 2, 2)), out)
 
 
 @pytest.mark.parametrize("dtype", [xpu.BF16, xpu.FP16])
