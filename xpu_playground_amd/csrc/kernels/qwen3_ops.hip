@@ -623,9 +623,10 @@ XPU_Q3_REG_SET(4)
 XPU_Q3_REG_SET(6)
 XPU_Q3_REG_SET(8)
 
-// One block per query head: QK-norm + RoPE of q and of its kv head's k; the
-// first query head of each group writes k and v into the engine caches at
-// position state[0]; then attention over positions 0..state[0].
+// One block per query head: QK-norm + RoPE of q and of its kv head's k,
+// attention over positions 0..state[0] (position state[0] itself from the
+// roped k and the qkv row), then the first query head of each group writes k
+// and v into the engine caches at position state[0].
 // cos_row / sin_row are the RoPE table rows of position state[0] (the engine
 // keeps them in a fixed buffer, rewritten whenever the position changes), so
 // that no load before the QK-norm depends on the position.
@@ -687,6 +688,9 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
     asm volatile("" : : "v"(acc));  // keeps the loads
     return;
   }
+  // the position: a scalar load issued early, so that its latency overlaps
+  // the operand loads and the QK-norm instead of following barrier 1
+  uint32_t pos = state[0];
   const uint32_t group = heads / kv_heads;
   const uint32_t kv = head / group;
   const uint16_t *qsrc = qkv + head * xpu::kHeadDim;
@@ -708,6 +712,9 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   // replaced below)
   u32x4 krow[16];
   xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(min(tid, max_seq - 1)) * 8u, krow, kchunk);
+  // the position in a register here, while the vector loads are in flight
+  // (otherwise the compiler issues its load next to its first use)
+  asm volatile("" : "+s"(pos));
   {
     // every wave evaluates a QK-norm / RoPE (waves 2 and 3 into scratch) so
     // that the four operand loads stay ahead of the K loads
@@ -718,20 +725,25 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   }
   __syncthreads();  // 1: qs, ks
   XPU_PHASE(0);     // (stamps build) operand loads, QK-norm and RoPE done
-  const uint32_t pos = state[0];
   if (pos >= max_seq) return;  // the reference skips the step (kernels.hpp:74-75)
   const uint32_t n = pos + 1;
   const bool short_ctx = n <= xpu::kAttnTile;
-  if (head % group == 0 && tid < 16) {
-    // the new k and v (chunk-major) at position pos
-    *reinterpret_cast<u32x4 *>(kcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) =
-        *reinterpret_cast<const u32x4 *>(ks + tid * 8u);
-    *reinterpret_cast<u32x4 *>(vcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) = hv;
-  }
+  // The new k and v (chunk-major) at position pos, stored by the first query
+  // head of each group after its output: this kernel reads position pos from
+  // ks / the qkv row, never from the caches, so the stores stay off the
+  // wait for the K rows (on gfx950 stores count in vmcnt like loads).
+  auto store_kv = [&]() {
+    if (head % group == 0 && tid < 16) {
+      *reinterpret_cast<u32x4 *>(kcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) =
+          *reinterpret_cast<const u32x4 *>(ks + tid * 8u);
+      *reinterpret_cast<u32x4 *>(vcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) = hv;
+    }
+  };
   if (!short_ctx) {
     xpu::attention_head<true>(qs, kcache + head_base, vcache + head_base,
                               xpu::KvLayout{8u, kchunk, 8u, kchunk}, n, ks, vsrc, scale,
                               out + head * xpu::kHeadDim, sbuf, vtile, red);
+    store_kv();
     return;
   }
   // scores (the current position from ks) and the block maximum
@@ -794,6 +806,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attention(
   if (cls == 0)
     *reinterpret_cast<u32x4 *>(out + head * xpu::kHeadDim + vch * 8u) =
         u32x4{code[0] | (code[1] << 16), code[2] | (code[3] << 16), code[4] | (code[5] << 16), code[6] | (code[7] << 16)};
+  store_kv();
 }
 
 // Attention split over compute units (two kernels, for long contexts): the
@@ -815,9 +828,9 @@ XPU_DEVICE void split_block(uint32_t b, uint32_t heads, uint32_t kv_heads, uint3
   part = rest / group;
 }
 
-// Part 1: QK-norm + RoPE of q and of its kv head's k (every block; the
-// first query head of each group with part 0 writes k and v into the caches
-// at position state[0]), then the scores of the 256-position tiles
+// Part 1: QK-norm + RoPE of q and of its kv head's k (every block; after
+// its scores the first query head of each group with part 0 writes k and v
+// into the caches at position state[0]), then the scores of the 256-position tiles
 // part, part + parts, ... (thread t <-> position tile * 256 + t, the current
 // position from the freshly roped k) into scores[head * spitch + t], and the
 // block's maximum into maxima[head * parts + part] (-inf without a tile).
@@ -834,6 +847,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_scores(
   __shared__ __align__(16) uint16_t qs[xpu::kHeadDim];
   __shared__ __align__(16) uint16_t ks[xpu::kHeadDim];
   __shared__ __align__(16) uint16_t junk[2 * xpu::kHeadDim];
+  uint32_t pos = state[0];  // issued early (see xpu_q3_attention)
   uint32_t kv, head, part;
   split_block(blockIdx.x, heads, kv_heads, kv, head, part);
   const uint32_t group = heads / kv_heads;
@@ -856,6 +870,7 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_scores(
   u32x4 knext[16];
   xpu::load_head_row(kcache + head_base + static_cast<uint64_t>(min(part * 256u + tid, max_seq - 1)) * 8u, knext,
                      kchunk);
+  asm volatile("" : "+s"(pos));  // the position in a register while the vector loads are in flight
   {
     const bool active = lane < 16;
     const u32x4 zero{0, 0, 0, 0};
@@ -863,14 +878,8 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_scores(
                             wave == 0 ? qs : wave == 1 ? ks : junk + (wave - 2) * xpu::kHeadDim);
   }
   __syncthreads();  // qs, ks
-  const uint32_t pos = state[0];
   if (pos >= max_seq) return;  // the reference skips the step (kernels.hpp:74-75)
   const uint32_t n = pos + 1, ntiles = (n + 255u) / 256u;
-  if (head % group == 0 && part == 0 && tid < 16) {
-    *reinterpret_cast<u32x4 *>(kcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) =
-        *reinterpret_cast<const u32x4 *>(ks + tid * 8u);
-    *reinterpret_cast<u32x4 *>(vcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) = hv;
-  }
   float *srow = scores + static_cast<uint64_t>(head) * spitch;
   float local_max = -__builtin_inff();
   for (uint32_t tile = part; tile < ntiles; tile += parts) {
@@ -886,6 +895,13 @@ extern "C" __global__ __launch_bounds__(256) void xpu_q3_attn_scores(
       srow[t] = s;
       local_max = fmaxf(local_max, s);
     }
+  }
+  // the new k and v at position pos, after the scores (which take position
+  // pos from ks): xpu_q3_attn_pv, the next kernel, reads them from the caches
+  if (head % group == 0 && part == 0 && tid < 16) {
+    *reinterpret_cast<u32x4 *>(kcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) =
+        *reinterpret_cast<const u32x4 *>(ks + tid * 8u);
+    *reinterpret_cast<u32x4 *>(vcache + head_base + tid * kchunk + static_cast<uint64_t>(pos) * 8u) = hv;
   }
   const float wmax = xpu::wave_reduce(local_max, [](float x, float y) { return fmaxf(x, y); });
   if (lane == 0) red[wave] = wmax;
