@@ -203,10 +203,15 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // Raw buffer descriptor: 48-bit base, stride 0, num_records bytes, 32-bit
 // data format. Offsets at or past num_records read as zero.
 XPU_DEVICE i32x4 rsrc(const void *base, int64_t records) {
-  records = records < 0 ? 0 : (records > 0x7fffffff ? 0x7fffffff : records);
+  // clamp to [0, 2^31 - 1] on the two 32-bit halves (scalar compares; a
+  // 64-bit signed compare would run on the vector ALU)
+  int32_t hi = static_cast<int32_t>(static_cast<uint64_t>(records) >> 32);
+  uint32_t lo = static_cast<uint32_t>(records);
+  asm("" : "+s"(hi), "+s"(lo));  // keeps the halves apart (no 64-bit compare)
+  const uint32_t n = hi < 0 ? 0u : (hi > 0 || lo > 0x7fffffffu ? 0x7fffffffu : lo);
   const uint64_t a = reinterpret_cast<uint64_t>(base);
-  return i32x4{static_cast<int>(a & 0xffffffffu), static_cast<int>((a >> 32) & 0xffffu),
-               static_cast<int>(records), 0x00020000};
+  return i32x4{static_cast<int>(a & 0xffffffffu), static_cast<int>((a >> 32) & 0xffffu), static_cast<int>(n),
+               0x00020000};
 }
 
 // 16 bytes per lane from the buffer at voff into LDS at m0 + 16 * lane (m0

@@ -209,15 +209,33 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
                              : (n0 + b_chunk * 8u < N ? (b_row * N + b_chunk * 8u) * 2u : kOob);
   const uint32_t b_istride = BT ? a_istride : 4u * G::kBRpi * N * 2u;
 
+  // Each lane's buffer offset of every DMA instruction, computed once: the
+  // slices differ only in their descriptors, so the K loop issues its DMA
+  // with scalar work only (vector ALU instructions between the MFMAs cost
+  // the MFMA pipe their issue cycles).
+  // a_cur / b_cur: the offsets the next slice's DMA uses (a_off / b_off
+  // with the chunks at or past column K sent out of range, from the first
+  // slice that is not live on)
+  uint32_t a_off[G::kDmaA], b_off[G::kDmaB], a_cur[G::kDmaA], b_cur[G::kDmaB];
+#pragma unroll
+  for (uint32_t op = 0; op < G::kDmaA; ++op) a_cur[op] = a_off[op] = a_voff + op * a_istride;
+#pragma unroll
+  for (uint32_t op = 0; op < G::kDmaB; ++op) b_cur[op] = b_off[op] = b_voff + op * b_istride;
+
   // DMA instruction d (0 .. kDma-1) of slice s into stage st: A rows first,
   // then B rows. Per slice the descriptors are rebased to the slice's first
-  // column (A) and row (B).
+  // column (A) and row (B); from the slice that holds column K on (the last
+  // one, and the zero slices that complete a group), the chunks at or past
+  // column K of A (and of an [n][k] B) go past the descriptor range and read
+  // zeros. Slices are set up in ascending order, so a_cur / b_cur only ever
+  // lose lanes.
   struct Slice {
     i32x4 r_a, r_b;
-    uint32_t a_base, b_base, st_base;
+    uint32_t st_base;
   };
   auto slice_of = [&](uint32_t s, uint32_t stage) {
-    const uint64_t k0 = static_cast<uint64_t>(s_base + s) * BK;
+    const uint32_t k0_32 = (s_base + s) * BK;
+    const uint64_t k0 = k0_32;
     Slice d;
     d.r_a = rsrc(A + static_cast<uint64_t>(m0) * K + k0,
                  (static_cast<int64_t>(M - m0) * K - static_cast<int64_t>(k0)) * 2);
@@ -227,17 +245,22 @@ XPU_DEVICE void body(const uint16_t *__restrict__ A, const uint16_t *__restrict_
     else
       d.r_b = rsrc(B + k0 * N + n0,
                    (static_cast<int64_t>(K) - static_cast<int64_t>(k0)) * N * 2 - static_cast<int64_t>(n0) * 2);
-    d.a_base = k0 + a_chunk * 8u < K ? a_voff : kOob;
-    d.b_base = !BT || k0 + b_chunk * 8u < K ? b_voff : kOob;
     d.st_base = lds0 + stage * G::kStage;
+    if (k0_32 + BK > K) {  // the last slice of A's columns, or one past them (a uniform branch)
+#pragma unroll
+      for (uint32_t op = 0; op < G::kDmaA; ++op) a_cur[op] = k0_32 + a_chunk * 8u < K ? a_off[op] : kOob;
+      if constexpr (BT) {
+#pragma unroll
+        for (uint32_t op = 0; op < G::kDmaB; ++op) b_cur[op] = k0_32 + b_chunk * 8u < K ? b_off[op] : kOob;
+      }
+    }
     return d;
   };
   auto dma = [&](const Slice &d, uint32_t op) {
     if (op < G::kDmaA)
-      dma16(d.st_base + (wave + 4u * op) * 1024u, d.r_a, d.a_base + op * a_istride);
+      dma16(d.st_base + (wave + 4u * op) * 1024u, d.r_a, a_cur[op]);
     else
-      dma16(d.st_base + G::kABytes + (wave + 4u * (op - G::kDmaA)) * 1024u, d.r_b,
-            d.b_base + (op - G::kDmaA) * b_istride);
+      dma16(d.st_base + G::kABytes + (wave + 4u * (op - G::kDmaA)) * 1024u, d.r_b, b_cur[op - G::kDmaA]);
   };
 
   // Fragment addresses (bytes within a stage). A: row wm*kBMW + 32 i + l%32,
